@@ -1,0 +1,52 @@
+// fqa_common.h — shared device helpers for the gfx950 attention-path kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/fqa.h"
+
+namespace fqa {
+
+constexpr int kD = 128;        // head_dim
+constexpr int kHq = 32;        // query heads
+constexpr int kHkv = 8;        // kv heads
+constexpr int kG = kHq / kHkv; // GQA group (query heads per kv head)
+constexpr int kPage = FQA_PAGE_TOKENS;
+constexpr int kQkvStride = (kHq + 2 * kHkv) * kD;  // 6144
+// One (page, kv head) run in the pool: K [16][128] then V^T [128][16], bf16.
+constexpr int kRunElems = 2 * kPage * kD;  // 4096 elements = 8 KiB
+constexpr int kVOff = kPage * kD;          // V^T starts 2048 elements into the run
+constexpr int kWave = 64;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ int64_t run_offset(int64_t page, int kvh) {
+  return (page * kHkv + kvh) * (int64_t)kRunElems;
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __uint_as_float((uint32_t)b << 16);
+}
+
+// Round-to-nearest-even float -> bf16 bits (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Two floats -> packed bf16x2 in one dword (RNE).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+}
+
+__device__ __forceinline__ float wave_max_xor(float v, int mask) {
+  return fmaxf(v, __shfl_xor(v, mask, kWave));
+}
+
+}  // namespace fqa

@@ -1,0 +1,224 @@
+/*
+ * fqa.h — C ABI of the MI355X (gfx950) per-step attention path.
+ *
+ * The path replaces, one for one, the attention block of the reference engine's
+ * forward step (engine/src/model_runtime.cu:261-278 per layer, and the host pack
+ * StepContext::PrepareInputs at model_runtime.cu:295-302 once per step):
+ *
+ *   fqa_schedule            <- Scheduler::BuildBatch token-budget selection   (scheduler.cc:116-143)
+ *   fqa_pack                <- StepContext::PrepareInputs: UploadRows, PackBlockTables,
+ *                              SplitDecodePrefill                             (model_runtime.cu:47-91, 295-302)
+ *   fqa_rope_tables         <- RopeTables::Build                              (model_runtime.cu:111-126)
+ *   fqa_qknorm_rope_append  <- LaunchHeadNormRope + KvStore::StoreKV          (kernels.cu:97-139, kv_store.cu:48-75)
+ *   fqa_decode              <- LaunchAttnDecodeCute (split + combine)         (attn_cute.cu:165-261)
+ *   fqa_prefill             <- LaunchAttnPrefillCute                          (attn_cute.cu:30-163)
+ *   fqa_pool_bytes          <- KvStore pool sizing                            (kv_store.cu:10-46)
+ *
+ * Conventions (all entry points):
+ *   - Plain device pointers and sizes; every launch goes on the caller's hipStream_t
+ *     (passed as void*, NULL = default stream). Nothing allocates; nothing synchronises.
+ *   - Return 0 on success, a negative FQA_E* code for a rejected call (no kernel is
+ *     launched then), never exit().  The reference aborts on these (assert / CUDA_CHECK,
+ *     attn_cute.cu:156,248, cuda_helpers.h:15-23).
+ *   - Counts that only the device knows after fqa_pack (rows, decode/prefill lists, work
+ *     items) are read by the later kernels from the pack's `meta` array, so a whole step
+ *     is stream-ordered with no host round trip; the host passes only upper bounds for
+ *     grid sizing.  A launch is therefore capture-safe (no hipMemset, no host sync).
+ *
+ * Supported shape: Qwen3-8B attention (32 q heads, 8 kv heads, head_dim 128, 16-token
+ * pages, GQA group 4), the only shape the reference kernels accept (attn_cute.cu:248).
+ *
+ * KV pool layout (one array per layer, bf16):
+ *   page p, kv head h occupies one contiguous 8 KiB run at element offset
+ *       ((p * n_kv_heads + h) * 2) * 16 * 128
+ *   holding K as [16 tokens][128 dims] followed by V transposed as [128 dims][16 tokens].
+ *   Slot s = page * 16 + token-in-page, as in the reference (kv_store.cu:56-60).
+ *   All pool offsets are 64-bit: one layer of a 200 GB pool exceeds 2^31 elements.
+ */
+#ifndef FQA_H_
+#define FQA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FQA_OK 0
+#define FQA_EINVAL (-1)       /* null pointer, negative size, size over a stated maximum */
+#define FQA_EUNSUPPORTED (-2) /* shape other than 32/8/128/16 */
+#define FQA_ELAUNCH (-3)      /* hipGetLastError() after a launch */
+
+#define FQA_PAGE_TOKENS 16
+#define FQA_MAX_REQS 2048 /* max requests in one step (reference: `slots`, args.h:13) */
+
+/* Indices into the int32 `meta` array written by fqa_pack. */
+enum {
+  FQA_META_ROWS = 0,         /* T: query rows in the step                      */
+  FQA_META_N_DECODE = 1,     /* requests with qlen == 1                        */
+  FQA_META_N_PREFILL = 2,    /* requests with qlen != 1                        */
+  FQA_META_MAX_QLEN = 3,     /* max(1, max prefill qlen) (model_runtime.cu:82) */
+  FQA_META_DEC_ITEMS = 4,    /* decode work items (sequence, page range)      */
+  FQA_META_PRE_ITEMS = 5,    /* prefill work items (request, query tile)      */
+  FQA_META_SPLIT_PAGES = 6,  /* pages per decode split chosen this step       */
+  FQA_META_STATUS = 7,       /* 0 or an FQA_PACK_* code                       */
+  FQA_META_REQS = 8,         /* R                                             */
+  FQA_META_DEC_PAGES = 9,    /* sum over decode sequences of their pages      */
+  FQA_META_LEN = 16
+};
+
+/* Pack status codes (meta[FQA_META_STATUS]). On 1..3 and 5 every count is zeroed, so
+ * the later kernels of the step do no work. On 4 counts stand; the attention and append
+ * kernels skip any page id outside [0, pool_pages). */
+enum {
+  FQA_PACK_OK = 0,
+  FQA_PACK_SHORT_TABLE = 1, /* block table shorter than ceil((computed+n)/16)   */
+  FQA_PACK_WIDE_TABLE = 2,  /* block table longer than max_blocks               */
+  FQA_PACK_ROWS = 3,        /* sum of n over requests > max_rows                */
+  FQA_PACK_PAGE_RANGE = 4,  /* a page id outside [0, pool_pages)                */
+  FQA_PACK_NEGATIVE = 5,    /* negative computed or n                           */
+  FQA_PACK_ITEMS = 6        /* work items would exceed the plan capacity        */
+};
+
+typedef struct fqa_dims {
+  int32_t n_q_heads;  /* 32                                    */
+  int32_t n_kv_heads; /* 8                                     */
+  int32_t head_dim;   /* 128                                   */
+  int32_t page_size;  /* 16                                    */
+  int32_t qkv_stride; /* row stride of qkv in elements (6144)  */
+  float eps;          /* RMSNorm epsilon (1e-6)                */
+  float scale;        /* softmax scale 1/sqrt(head_dim)        */
+} fqa_dims;
+
+/* The ragged batch of one step, in batch order (what Scheduler::BuildBatch hands to
+ * Forward through ForwardInput, scheduler.h:66-72): request r contributes rows
+ * (pos = computed[r] + k, k < n_new[r]) and owns pages bt_pages[bt_off[r] .. bt_off[r+1]).
+ * All arrays are device arrays.  If `n_reqs_dev` is non-NULL the request count is read
+ * from it on the device (fqa_schedule's output) and `n_reqs` is only an upper bound. */
+typedef struct fqa_batch {
+  const int32_t* computed; /* [R] tokens already in the KV cache          */
+  const int32_t* n_new;    /* [R] rows this step                          */
+  const int32_t* bt_off;   /* [R+1] offsets into bt_pages                 */
+  const int32_t* bt_pages; /* concatenated block tables (page ids)        */
+  const int32_t* n_reqs_dev;
+  int32_t n_reqs;
+} fqa_batch;
+
+/* Everything the pack writes (device arrays, caller-allocated at capacity). */
+typedef struct fqa_pack_out {
+  int32_t* cu_seqlens;     /* [R+1]  qstart = cu_seqlens[r]                   */
+  int32_t* qlen;           /* [R]                                             */
+  int32_t* positions;      /* [max_rows]                                      */
+  int32_t* row_req;        /* [max_rows] request index of each row            */
+  int32_t* slot_mapping;   /* [max_rows] page*16 + pos%16                     */
+  int32_t* block_tables;   /* [R * max_blocks], tail padded with -1           */
+  int32_t* decode_rids;    /* [R] qlen==1 requests, increasing; pad -1        */
+  int32_t* prefill_rids;   /* [R] the others, increasing; pad -1              */
+  int32_t* dec_item_start; /* [R+1] first item of decode index di; pad -1     */
+  int32_t* dec_items;      /* [dec_cap][4] {r, split, page_begin, page_end}   */
+  int32_t* pre_items;      /* [pre_cap][4] {r, q0, q1, n_keys}                */
+  int32_t* meta;           /* [FQA_META_LEN]                                  */
+} fqa_pack_out;
+
+typedef struct fqa_pack_cfg {
+  int32_t max_rows;          /* capacity of the per-row arrays             */
+  int32_t max_blocks;        /* block table stride                         */
+  int64_t pool_pages;        /* pages in the per-layer pool                */
+  int32_t dec_target_items;  /* aim for this many decode splits (0: one per sequence) */
+  int32_t dec_min_split;     /* never split finer than this many pages     */
+  int32_t dec_item_cap;      /* capacity of dec_items                      */
+  int32_t pre_tile_q;        /* query rows per prefill item: 32, 64 or 128 */
+  int32_t pre_item_cap;      /* capacity of pre_items                      */
+} fqa_pack_cfg;
+
+/* --- host-side helpers (no device work) ------------------------------------------ */
+
+/* cos/sin tables [max_pos][head_dim/2], float, angle = p * theta^(-2i/head_dim),
+ * computed in float exactly as RopeTables::Build (model_runtime.cu:111-126). Host memory. */
+int fqa_rope_tables(int32_t max_pos, int32_t head_dim, float theta, float* cos_tab,
+                    float* sin_tab);
+
+/* Bytes of one layer's pool for `pages` pages (replaces KvStore's per-block sizing,
+ * kv_store.cu:24-26). */
+int64_t fqa_pool_bytes(const fqa_dims* dims, int64_t pages);
+
+/* Upper bounds for plan capacities and launch grids, from host-known sizes. */
+int32_t fqa_dec_item_bound(int32_t n_reqs, int32_t dec_target_items);
+int32_t fqa_pre_item_bound(int32_t n_reqs, int32_t max_rows, int32_t pre_tile_q);
+
+/* Bytes of the decode workspace fqa_decode needs for `dec_item_cap` items. */
+int64_t fqa_decode_workspace_bytes(const fqa_dims* dims, int32_t dec_item_cap);
+
+/* --- device entry points (stream-ordered launches) -------------------------------- */
+
+/* Token-budget selection of Scheduler::BuildBatch (scheduler.cc:116-143) on the GPU:
+ * stable-sorts the running requests by remaining = num_tokens - computed, then takes
+ * n = min(remaining, budget left, prefill_chunk if remaining > 1) in that order.
+ * Writes batch_req[R] (index into the running arrays), batch_n[R], and *n_batch (R).
+ * Block tables must already cover each chosen request's computed + n tokens (the
+ * allocator's Grow stays on the host). One workgroup; n_running <= FQA_MAX_REQS. */
+int fqa_schedule(const int32_t* num_tokens, const int32_t* computed, int32_t n_running,
+                 int32_t token_budget, int32_t prefill_chunk, int32_t* batch_req,
+                 int32_t* batch_n, int32_t* n_batch, void* stream);
+
+/* Gather the running requests chosen by fqa_schedule into a fqa_batch:
+ * out_computed/out_n_new/out_bt_off[0..R] and out_bt_pages (concatenated tables).
+ * run_bt_off/run_bt_pages are the running requests' tables. bt_pages_cap bounds
+ * out_bt_pages; rows past it are dropped and flagged by status 1 in the pack. */
+int fqa_gather_batch(const int32_t* batch_req, const int32_t* batch_n,
+                     const int32_t* n_batch, int32_t n_running, const int32_t* run_computed,
+                     const int32_t* run_bt_off, const int32_t* run_bt_pages,
+                     int32_t* out_computed, int32_t* out_n_new, int32_t* out_bt_off,
+                     int32_t* out_bt_pages, int32_t bt_pages_cap, void* stream);
+
+/* The GPU pack (replaces StepContext::PrepareInputs' host loops + H2D copies,
+ * model_runtime.cu:47-91): rows, slot mapping, padded block tables, decode/prefill
+ * split by qlen, and the decode/prefill work plans. One launch. */
+int fqa_pack(const fqa_batch* batch, const fqa_pack_cfg* cfg, const fqa_pack_out* out,
+             void* stream);
+
+/* Fused per-head QK-RMSNorm + rotate-half RoPE on the q and k heads of each row and the
+ * paged append of k and v (replaces HeadNormRopeKernel + StoreKvKernel).  q is normalised
+ * in place in `qkv` (the attention kernels read it from there, as in the reference);
+ * k and v go to the pool at slot_mapping[t].  With `write_k_inplace` the normalised k is
+ * also written back into qkv, leaving qkv bit-identical to the reference's.
+ * Rows: meta[FQA_META_ROWS] (device) <= rows_bound (host, grid size).  The tables hold
+ * rope_max_pos positions; a row whose position is outside [0, rope_max_pos) is left
+ * untouched and appends nothing (the reference would read past its table). */
+int fqa_qknorm_rope_append(const fqa_dims* dims, uint16_t* qkv, const float* q_norm_w,
+                           const float* k_norm_w, const float* cos_tab, const float* sin_tab,
+                           int32_t rope_max_pos, const int32_t* positions, const int32_t* slot_mapping,
+                           const int32_t* meta, int32_t rows_bound, uint16_t* pool,
+                           int64_t pool_pages, int32_t write_k_inplace, void* stream);
+
+/* GQA-shared split-K flash decoding over the pack's decode plan: one wavefront per
+ * (work item, kv head) streams its page range once for all 4 query heads; sequences
+ * with more than one split are merged by a log-sum-exp combine.  Output rows
+ * out[cu_seqlens[r]] ([n_q_heads][head_dim] bf16, row stride n_q_heads*head_dim).
+ * `workspace` must hold fqa_decode_workspace_bytes(dims, dec_item_cap) bytes. */
+int fqa_decode(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
+               int64_t pool_pages, const int32_t* block_tables, int32_t max_blocks,
+               const int32_t* cu_seqlens, const int32_t* positions,
+               const int32_t* dec_items, const int32_t* dec_item_start,
+               const int32_t* decode_rids, const int32_t* meta, int32_t dec_item_cap,
+               int32_t n_reqs_bound, void* workspace, uint16_t* out, void* stream);
+
+/* Varlen causal FlashAttention-2 prefill on bf16 MFMA over the pack's prefill plan:
+ * one workgroup per (query tile, kv head) computes all 4 query heads of the kv head
+ * from one LDS-staged copy of each K/V tile.  Mask: key pos <= query pos (cached
+ * prefix included).  Output rows out[cu_seqlens[r] + i]. */
+int fqa_prefill(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
+                int64_t pool_pages, const int32_t* block_tables, int32_t max_blocks,
+                const int32_t* cu_seqlens, const int32_t* positions,
+                const int32_t* pre_items, const int32_t* meta, int32_t pre_tile_q,
+                int32_t pre_item_cap, uint16_t* out, void* stream);
+
+/* Library version string. */
+const char* fqa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FQA_H_ */

@@ -1,0 +1,433 @@
+/*
+ * fqa_oracle.c — CPU restatement of the reference engine's per-step attention path.
+ *
+ * TEST INFRASTRUCTURE.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg load this library, and only as the checker / the reported CPU
+ * baseline.  The product (flashqwen_amd, libfqa.so) never links or calls it.
+ *
+ * Every function follows a reference file:line (paths relative to the reference's
+ * engine/src/).  Arithmetic is fp32 with bf16 inputs and bf16 outputs, the semantics
+ * the reference kernels implement; differences are limited to summation order, the
+ * exp implementation, and two-pass (exact-max) instead of online softmax, all of which
+ * the attention tolerance (bf16 max-abs 2e-2, mean-abs 2e-3) absorbs.
+ *
+ * Pinning (see tests/test_oracle.py): the pack is checked against a second,
+ * independent pure-Python restatement and hand-built cases with known answers; RoPE
+ * and RMSNorm against torch fp64 library routines plus closed forms (pos 0 identity,
+ * pair-norm preservation, relative-position invariance of q.k); attention against
+ * torch's fp64 scaled_dot_product_attention and closed forms (single key -> V,
+ * identical keys -> mean V, first causal row -> V[0], page-permutation invariance).
+ */
+#include "fqa_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define PAGE 16
+
+float fqo_bf16_to_f32(uint16_t b) {
+  uint32_t bits = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &bits, sizeof f);
+  return f;
+}
+
+uint16_t fqo_f32_to_bf16(float f) {
+  uint32_t bits;
+  memcpy(&bits, &f, sizeof bits);
+  if ((bits & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((bits >> 16) | 0x40u); /* NaN */
+  bits += 0x7fffu + ((bits >> 16) & 1u);
+  return (uint16_t)(bits >> 16);
+}
+
+int fqo_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+/* Pool layout of include/fqa.h: per (page, kv head) an 8 KiB run: K [16][D] then
+ * V transposed [D][16].  The reference's layout is NHD [page][2][16][kv_dim]
+ * (kv_store.h:13-16); only the addressing differs, not what is stored. */
+int64_t fqo_pool_offset(int n_kv, int head_dim, int64_t page, int kvh, int plane, int tok,
+                        int d) {
+  int64_t base = ((page * n_kv + kvh) * 2 + plane) * (int64_t)PAGE * head_dim;
+  return plane == 0 ? base + (int64_t)tok * head_dim + d : base + (int64_t)d * PAGE + tok;
+}
+
+/* RopeTables::Build (model_runtime.cu:111-126): float pow/cos/sin, angle = p * inv. */
+void fqo_rope_tables(int max_pos, int head_dim, float theta, float* cos_tab, float* sin_tab) {
+  int half = head_dim / 2;
+  for (int p = 0; p < max_pos; ++p)
+    for (int i = 0; i < half; ++i) {
+      float inv = powf(theta, -2.0f * (float)i / (float)head_dim);
+      float ang = (float)p * inv;
+      cos_tab[(int64_t)p * half + i] = cosf(ang);
+      sin_tab[(int64_t)p * half + i] = sinf(ang);
+    }
+}
+
+/* Scheduler::BuildBatch (scheduler.cc:116-143) with every Grow succeeding: stable sort of
+ * the running requests by Remaining() ascending, then n = min(remaining, budget) capped
+ * at prefill_chunk when remaining > 1; stop when the budget is spent, skip finished
+ * requests (remaining <= 0).  Returns the number of requests in the batch. */
+int fqo_schedule(int n_running, const int32_t* num_tokens, const int32_t* computed,
+                 int token_budget, int prefill_chunk, int32_t* batch_req, int32_t* batch_n) {
+  int* order = (int*)malloc(sizeof(int) * (n_running > 0 ? n_running : 1));
+  for (int i = 0; i < n_running; ++i) order[i] = i;
+  /* insertion sort: stable */
+  for (int i = 1; i < n_running; ++i) {
+    int v = order[i], rv = num_tokens[v] - computed[v], j = i - 1;
+    while (j >= 0 && num_tokens[order[j]] - computed[order[j]] > rv) {
+      order[j + 1] = order[j];
+      --j;
+    }
+    order[j + 1] = v;
+  }
+  int budget = token_budget, R = 0;
+  for (int k = 0; k < n_running; ++k) {
+    if (budget <= 0) break;
+    int idx = order[k];
+    int remaining = num_tokens[idx] - computed[idx];
+    if (remaining <= 0) continue;
+    int n = remaining < budget ? remaining : budget;
+    if (remaining > 1 && n > prefill_chunk) n = prefill_chunk;
+    batch_req[R] = idx;
+    batch_n[R] = n;
+    ++R;
+    budget -= n;
+  }
+  free(order);
+  return R;
+}
+
+static int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+/* Pack: UploadRows + PackBlockTables + SplitDecodePrefill (model_runtime.cu:47-91) and
+ * EmitChunk's row generation (scheduler.h:66-72), plus the slot mapping implied by
+ * StoreKvKernel (kv_store.cu:56-60) and this library's decode/prefill work plans. */
+int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t* bt_off,
+             const int32_t* bt_pages, int max_rows, int max_blocks, int64_t pool_pages,
+             int dec_target_items, int dec_min_split, int dec_item_cap, int pre_tile_q,
+             int pre_item_cap, int32_t* cu_seqlens, int32_t* qlen, int32_t* positions,
+             int32_t* row_req, int32_t* slot_mapping, int32_t* block_tables,
+             int32_t* decode_rids, int32_t* prefill_rids, int32_t* dec_item_start,
+             int32_t* dec_items, int32_t* pre_items, int32_t* meta) {
+  for (int i = 0; i < 16; ++i) meta[i] = 0;
+  meta[8] = R;
+  /* structural checks: the smallest violated code wins */
+  int code = 0;
+  int64_t T64 = 0;
+  for (int r = 0; r < R; ++r) {
+    int c = 0;
+    if (computed[r] < 0 || n_new[r] < 0) c = 5;
+    else {
+      int nb = bt_off[r + 1] - bt_off[r];
+      int need = ceil_div((int64_t)computed[r] + n_new[r], PAGE);
+      if (nb < need) c = 1;
+      else if (nb > max_blocks) c = 2;
+      T64 += n_new[r];
+    }
+    if (c && (code == 0 || c < code)) code = c;
+  }
+  if (T64 > max_rows && (code == 0 || 3 < code)) code = 3;
+  if (code) {
+    meta[7] = code;
+    return code;
+  }
+  int T = (int)T64;
+
+  /* SplitDecodePrefill: qlen, qstart (exclusive scan), classification by qlen == 1 */
+  int acc = 0, nd = 0, np = 0, maxq = 1;
+  for (int r = 0; r < R; ++r) {
+    qlen[r] = n_new[r];
+    cu_seqlens[r] = acc;
+    acc += n_new[r];
+    if (n_new[r] == 1) decode_rids[nd++] = r;
+    else {
+      prefill_rids[np++] = r;
+      if (n_new[r] > maxq) maxq = n_new[r];
+    }
+  }
+  cu_seqlens[R] = acc;
+  for (int i = nd; i < R; ++i) decode_rids[i] = -1;
+  for (int i = np; i < R; ++i) prefill_rids[i] = -1;
+
+  /* rows (EmitChunk: pos = computed_ + k) and slot mapping */
+  int bad_page = 0;
+  for (int r = 0; r < R; ++r)
+    for (int k = 0; k < n_new[r]; ++k) {
+      int t = cu_seqlens[r] + k, p = computed[r] + k;
+      positions[t] = p;
+      row_req[t] = r;
+      int page = bt_pages[bt_off[r] + p / PAGE];
+      slot_mapping[t] = page * PAGE + p % PAGE;
+    }
+  /* PackBlockTables; the tail is defined as -1 (the reference leaves it stale) */
+  for (int r = 0; r < R; ++r) {
+    int nb = bt_off[r + 1] - bt_off[r];
+    for (int g = 0; g < max_blocks; ++g) {
+      int v = g < nb ? bt_pages[bt_off[r] + g] : -1;
+      if (g < nb && (v < 0 || v >= pool_pages)) bad_page = 1;
+      block_tables[(int64_t)r * max_blocks + g] = v;
+    }
+  }
+
+  /* decode plan: split size S pages, ceil(pages / S) items per sequence */
+  int64_t total = 0;
+  int maxpages = 0;
+  for (int di = 0; di < nd; ++di) {
+    int pages = computed[decode_rids[di]] / PAGE + 1;
+    total += pages;
+    if (pages > maxpages) maxpages = pages;
+  }
+  int minsplit = dec_min_split > 0 ? dec_min_split : 1;
+  int S;
+  if (dec_target_items <= 0) S = maxpages > 0 ? maxpages : 1;
+  else {
+    int64_t s = (total + dec_target_items - 1) / dec_target_items;
+    S = s > minsplit ? (int)s : minsplit;
+  }
+  int nitems = 0;
+  for (int di = 0; di < nd; ++di) {
+    dec_item_start[di] = nitems;
+    nitems += ceil_div(computed[decode_rids[di]] / PAGE + 1, S);
+  }
+  dec_item_start[nd] = nitems;
+  for (int i = nd + 1; i <= R; ++i) dec_item_start[i] = -1;
+
+  /* prefill plan: query tiles of pre_tile_q rows, ordered by key count descending
+   * (longest first), ties by (prefill index, tile) ascending */
+  int npi = 0;
+  for (int pi = 0; pi < np; ++pi) npi += ceil_div(n_new[prefill_rids[pi]], pre_tile_q);
+
+  if (nitems > dec_item_cap || npi > pre_item_cap) {
+    for (int i = 0; i < 16; ++i) meta[i] = 0;
+    meta[8] = R;
+    meta[7] = 6;
+    return 6;
+  }
+  for (int di = 0; di < nd; ++di) {
+    int r = decode_rids[di], pages = computed[r] / PAGE + 1;
+    for (int s = 0, it = dec_item_start[di]; s * S < pages; ++s, ++it) {
+      int pe = (s + 1) * S < pages ? (s + 1) * S : pages;
+      dec_items[4 * it + 0] = r;
+      dec_items[4 * it + 1] = s;
+      dec_items[4 * it + 2] = s * S;
+      dec_items[4 * it + 3] = pe;
+    }
+  }
+  {
+    int32_t* tmp = (int32_t*)malloc(sizeof(int32_t) * 4 * (npi > 0 ? npi : 1));
+    int k = 0;
+    for (int pi = 0; pi < np; ++pi) {
+      int r = prefill_rids[pi], q = n_new[r];
+      for (int q0 = 0; q0 < q; q0 += pre_tile_q, ++k) {
+        int q1 = q0 + pre_tile_q < q ? q0 + pre_tile_q : q;
+        tmp[4 * k + 0] = r;
+        tmp[4 * k + 1] = q0;
+        tmp[4 * k + 2] = q1;
+        tmp[4 * k + 3] = computed[r] + q1;
+      }
+    }
+    /* stable sort by n_keys descending: rank = #(greater) + #(equal and earlier) */
+    for (int i = 0; i < npi; ++i) {
+      int rank = 0;
+      for (int j = 0; j < npi; ++j)
+        if (tmp[4 * j + 3] > tmp[4 * i + 3] || (tmp[4 * j + 3] == tmp[4 * i + 3] && j < i))
+          ++rank;
+      memcpy(&pre_items[4 * rank], &tmp[4 * i], 4 * sizeof(int32_t));
+    }
+    free(tmp);
+  }
+
+  meta[0] = T;
+  meta[1] = nd;
+  meta[2] = np;
+  meta[3] = maxq;
+  meta[4] = nitems;
+  meta[5] = npi;
+  meta[6] = S;
+  meta[7] = bad_page ? 4 : 0;
+  meta[9] = (int32_t)total;
+  return meta[7];
+}
+
+/* HeadNormRopeKernel (kernels.cu:97-131) + StoreKvKernel (kv_store.cu:48-64):
+ * per q/k head: inv = 1/sqrt(mean(x^2) + eps); y = x*inv*w in fp32; rotate-half RoPE
+ * on (y_i, y_{i+half}) with cos/sin[pos][i]; one bf16 rounding at the end.  q written
+ * back in place; k and raw v appended to the pool at slot_mapping[t]. */
+void fqo_qknorm_rope_append(int n_q, int n_kv, int D, int stride, float eps, uint16_t* qkv,
+                            const float* wq, const float* wk, const float* cos_tab,
+                            const float* sin_tab, int rope_max_pos,
+                            const int32_t* positions, const int32_t* slot_mapping, int rows, uint16_t* pool,
+                            int64_t pool_pages, int write_k_inplace) {
+  int half = D / 2;
+#pragma omp parallel for schedule(static)
+  for (int t = 0; t < rows; ++t) {
+    float x[512], y[512];
+    int p = positions[t];
+    if (p < 0 || p >= rope_max_pos) continue; /* no table row: the row is left untouched */
+    int64_t slot = slot_mapping[t];
+    int64_t page = slot / PAGE;
+    int tok = (int)(slot % PAGE);
+    int page_ok = page >= 0 && page < pool_pages;
+    for (int g = 0; g < n_q + n_kv; ++g) {
+      uint16_t* v = qkv + (int64_t)t * stride + (int64_t)g * D;
+      const float* w = g < n_q ? wq : wk;
+      float ss = 0.f;
+      for (int i = 0; i < D; ++i) {
+        x[i] = fqo_bf16_to_f32(v[i]);
+        ss += x[i] * x[i];
+      }
+      float inv = 1.0f / sqrtf(ss / (float)D + eps);
+      for (int i = 0; i < D; ++i) y[i] = x[i] * inv * w[i];
+      uint16_t o[512];
+      for (int i = 0; i < half; ++i) {
+        float cs = cos_tab[(int64_t)p * half + i], sn = sin_tab[(int64_t)p * half + i];
+        o[i] = fqo_f32_to_bf16(y[i] * cs - y[i + half] * sn);
+        o[i + half] = fqo_f32_to_bf16(y[i + half] * cs + y[i] * sn);
+      }
+      if (g < n_q) {
+        memcpy(v, o, sizeof(uint16_t) * D);
+      } else {
+        int kvh = g - n_q;
+        if (write_k_inplace) memcpy(v, o, sizeof(uint16_t) * D);
+        if (page_ok)
+          for (int i = 0; i < D; ++i) pool[fqo_pool_offset(n_kv, D, page, kvh, 0, tok, i)] = o[i];
+      }
+    }
+    if (page_ok)
+      for (int kvh = 0; kvh < n_kv; ++kvh) {
+        const uint16_t* vv = qkv + (int64_t)t * stride + (int64_t)(n_q + n_kv + kvh) * D;
+        for (int i = 0; i < D; ++i) pool[fqo_pool_offset(n_kv, D, page, kvh, 1, tok, i)] = vv[i];
+      }
+  }
+}
+
+/* Gather keys [0, nkeys) of one request's kv head into float rows K[n][D], V[n][D];
+ * rows whose page id is out of range are flagged so they are skipped. */
+static void gather_kv(int n_kv, int D, const uint16_t* pool, int64_t pool_pages,
+                      const int32_t* bt_row, int nkeys, int kvh, float* K, float* V,
+                      unsigned char* ok) {
+  for (int kp = 0; kp < nkeys; ++kp) {
+    int64_t page = bt_row[kp / PAGE];
+    ok[kp] = page >= 0 && page < pool_pages;
+    if (!ok[kp]) continue;
+    int tok = kp % PAGE;
+    const uint16_t* kb = pool + fqo_pool_offset(n_kv, D, page, kvh, 0, tok, 0);
+    const uint16_t* vb = pool + fqo_pool_offset(n_kv, D, page, kvh, 1, 0, 0);
+    for (int d = 0; d < D; ++d) {
+      K[(int64_t)kp * D + d] = fqo_bf16_to_f32(kb[d]);
+      V[(int64_t)kp * D + d] = fqo_bf16_to_f32(vb[d * PAGE + tok]);
+    }
+  }
+}
+
+static float dot_d(const float* a, const float* b, int D) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int d = 0; d < D; d += 8)
+    for (int j = 0; j < 8; ++j) acc[j] += a[d + j] * b[d + j];
+  return ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+}
+
+/* softmax(scale * q.K^T over keys [0, nk)) V for one query row; P optionally rounded
+ * to bf16 in the numerator (prefill, attn_cute.cu:128) but summed unrounded into l
+ * (attn_cute.cu:122-127).  Output 0 when no key contributes (l == 0, attn_cute.cu:141). */
+static void attend_row(const float* q, const float* K, const float* V, const unsigned char* ok,
+                       int nk, int D, float scale, int round_p, float* s, uint16_t* out) {
+  float m = -INFINITY;
+  for (int k = 0; k < nk; ++k) {
+    s[k] = ok[k] ? dot_d(q, K + (int64_t)k * D, D) * scale : -INFINITY;
+    if (s[k] > m) m = s[k];
+  }
+  float acc[512];
+  for (int d = 0; d < D; ++d) acc[d] = 0.f;
+  float l = 0.f;
+  if (m > -INFINITY)
+    for (int k = 0; k < nk; ++k) {
+      if (!ok[k]) continue;
+      float p = expf(s[k] - m);
+      l += p;
+      float pv = round_p ? fqo_bf16_to_f32(fqo_f32_to_bf16(p)) : p;
+      const float* vr = V + (int64_t)k * D;
+      for (int d = 0; d < D; ++d) acc[d] += pv * vr[d];
+    }
+  float inv = l > 0.f ? 1.0f / l : 0.f;
+  for (int d = 0; d < D; ++d) out[d] = fqo_f32_to_bf16(acc[d] * inv);
+}
+
+/* CuteDecodeSplitKernel + CuteDecodeCombineKernel (attn_cute.cu:165-238) without the
+ * split: for each qlen==1 request, the 4 query heads of each kv head attend keys
+ * [0, pos]; fp32 P (the decode kernel does not round P). */
+void fqo_decode(int n_q, int n_kv, int D, int stride, float scale, const uint16_t* qkv,
+                const uint16_t* pool, int64_t pool_pages, const int32_t* block_tables,
+                int max_blocks, const int32_t* cu_seqlens, const int32_t* positions,
+                const int32_t* decode_rids, int n_decode, uint16_t* out) {
+  int G = n_q / n_kv;
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int w = 0; w < n_decode * n_kv; ++w) {
+    int di = w / n_kv, kvh = w % n_kv;
+    int r = decode_rids[di], row = cu_seqlens[r], nk = positions[row] + 1;
+    float* K = (float*)malloc(sizeof(float) * (size_t)nk * D);
+    float* V = (float*)malloc(sizeof(float) * (size_t)nk * D);
+    float* s = (float*)malloc(sizeof(float) * (size_t)nk);
+    unsigned char* ok = (unsigned char*)malloc((size_t)nk);
+    gather_kv(n_kv, D, pool, pool_pages, block_tables + (int64_t)r * max_blocks, nk, kvh, K, V,
+              ok);
+    for (int g = 0; g < G; ++g) {
+      int h = kvh * G + g;
+      float q[512];
+      for (int d = 0; d < D; ++d) q[d] = fqo_bf16_to_f32(qkv[(int64_t)row * stride + h * D + d]);
+      attend_row(q, K, V, ok, nk, D, scale, 0, s, out + ((int64_t)row * n_q + h) * D);
+    }
+    free(K);
+    free(V);
+    free(s);
+    free(ok);
+  }
+}
+
+/* CutePrefillKernel (attn_cute.cu:30-147): for each qlen!=1 request and each of its
+ * rows i, head h attends keys kpos <= pos[qstart+i] of kv head h/G, cached prefix
+ * included; P rounded to bf16 before PV. */
+void fqo_prefill(int n_q, int n_kv, int D, int stride, float scale, const uint16_t* qkv,
+                 const uint16_t* pool, int64_t pool_pages, const int32_t* block_tables,
+                 int max_blocks, const int32_t* cu_seqlens, const int32_t* positions,
+                 const int32_t* prefill_rids, int n_prefill, uint16_t* out) {
+  int G = n_q / n_kv;
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int w = 0; w < n_prefill * n_kv; ++w) {
+    int pi = w / n_kv, kvh = w % n_kv;
+    int r = prefill_rids[pi], qs = cu_seqlens[r], ql = cu_seqlens[r + 1] - qs;
+    if (ql <= 0) continue;
+    int nk = 0;
+    for (int i = 0; i < ql; ++i)
+      if (positions[qs + i] + 1 > nk) nk = positions[qs + i] + 1;
+    float* K = (float*)malloc(sizeof(float) * (size_t)nk * D);
+    float* V = (float*)malloc(sizeof(float) * (size_t)nk * D);
+    float* s = (float*)malloc(sizeof(float) * (size_t)nk);
+    unsigned char* ok = (unsigned char*)malloc((size_t)nk);
+    gather_kv(n_kv, D, pool, pool_pages, block_tables + (int64_t)r * max_blocks, nk, kvh, K, V,
+              ok);
+    for (int i = 0; i < ql; ++i) {
+      int row = qs + i, kv_end = positions[row] + 1;
+      for (int g = 0; g < G; ++g) {
+        int h = kvh * G + g;
+        float q[512];
+        for (int d = 0; d < D; ++d) q[d] = fqo_bf16_to_f32(qkv[(int64_t)row * stride + h * D + d]);
+        attend_row(q, K, V, ok, kv_end, D, scale, 1, s, out + ((int64_t)row * n_q + h) * D);
+      }
+    }
+    free(K);
+    free(V);
+    free(s);
+    free(ok);
+  }
+}

@@ -1,0 +1,133 @@
+"""GPU parity of the whole attention step (pack -> norm/rope/append -> decode + prefill)
+against the CPU oracle, through the C ABI (libfqa.so via flashqwen_amd.step)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from flashqwen_amd import synth
+from flashqwen_amd.synth import HEAD_DIM, N_Q, PAGE, QKV_STRIDE
+from tests import stepcase as sc
+
+PACK_KEYS_R = ("cu_seqlens", "qlen", "decode_rids", "prefill_rids", "dec_item_start")
+
+
+def _t(x, dev):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+def _host_u16(t) -> np.ndarray:
+    import torch
+
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def make_pool(pages: int, seed: int, dev, layers: int = 1):
+    import torch
+
+    from flashqwen_amd.step import alloc_pool
+
+    pool = alloc_pool(pages, layers, dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    flat = pool.view(-1)
+    chunk = 1 << 28
+    for s in range(0, flat.numel(), chunk):
+        e = min(s + chunk, flat.numel())
+        flat[s:e] = torch.randn(e - s, generator=g, device=dev, dtype=torch.float32).to(
+            torch.bfloat16)
+    return pool
+
+
+def gpu_chain(cfg, qkv_host, pool, wq, wk, dev, kw, schedule=False):
+    import torch
+
+    from flashqwen_amd.step import AttnStep
+
+    step = AttnStep(max_rows=kw["max_rows"], max_reqs=cfg.n_reqs, max_ctx=cfg.max_ctx,
+                    pool_pages=cfg.pool_pages, device=dev,
+                    dec_target_items=kw["dec_target_items"], dec_min_split=kw["dec_min_split"],
+                    pre_tile_q=kw["pre_tile_q"])
+    qkv = _t(qkv_host.view(np.int16), dev).view(torch.bfloat16)
+    out = torch.zeros((kw["max_rows"], N_Q * HEAD_DIM), dtype=torch.bfloat16, device=dev)
+    if schedule:
+        step.schedule_and_prepare(_t(cfg.num_tokens, dev), _t(cfg.computed, dev),
+                                  _t(cfg.bt_off, dev), _t(cfg.bt_pages, dev), cfg.token_budget,
+                                  cfg.prefill_chunk)
+    else:
+        step.prepare_inputs(_t(cfg.computed, dev), _t(cfg.n_new, dev), _t(cfg.bt_off, dev),
+                            _t(cfg.bt_pages, dev))
+    step.run_layer(qkv, pool[0], _t(wq, dev), _t(wk, dev), out)
+    torch.cuda.synchronize()
+    return step, qkv, out
+
+
+def check_pack(step, ref_pk, R, T, kw):
+    meta = step.meta.cpu().numpy()
+    assert np.array_equal(meta, ref_pk["meta"]), (meta, ref_pk["meta"])
+    for k in PACK_KEYS_R:
+        got = getattr(step, k).cpu().numpy()
+        n = R + 1 if k in ("cu_seqlens", "dec_item_start") else R
+        assert np.array_equal(got[:n], ref_pk[k][:n]), k
+    for k in ("positions", "row_req", "slot_mapping"):
+        assert np.array_equal(getattr(step, k).cpu().numpy()[:T], ref_pk[k][:T]), k
+    bt = step.block_tables.cpu().numpy().reshape(-1)[: R * kw["max_blocks"]]
+    assert np.array_equal(bt, ref_pk["block_tables"][: R * kw["max_blocks"]])
+    nd, npi = int(meta[4]), int(meta[5])
+    assert np.array_equal(step.dec_items.cpu().numpy()[:nd], ref_pk["dec_items"][:nd])
+    assert np.array_equal(step.pre_items.cpu().numpy()[:npi], ref_pk["pre_items"][:npi])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cfgno", [1, 2, 3])
+def test_step_parity(gpu, cfgno):
+    from oracle import oracle as orc
+
+    print(f"[test_step_parity] config{cfgno}", flush=True)
+    cfg = synth.CONFIGS[cfgno]()
+    rng = np.random.default_rng(100 + cfgno)
+    T, R = cfg.rows, cfg.n_reqs
+    kw = sc.pack_kwargs(cfg, dec_target_items=256 if cfgno == 1 else 1024, dec_min_split=2)
+    qkv_h = synth.rand_bf16(rng, (T, QKV_STRIDE))
+    wq, wk = synth.norm_weights()
+    pool = make_pool(cfg.pool_pages, 1000 + cfgno, gpu)
+    pool_h = _host_u16(pool).reshape(-1).copy()
+
+    ref = sc.oracle_chain(cfg, qkv_h, pool_h, wq, wk, kw)
+    step, qkv, out = gpu_chain(cfg, qkv_h, pool, wq, wk, gpu, kw)
+
+    check_pack(step, ref["pack"], R, T, kw)
+
+    # norm + rope: q in place, k/v into the pool (within 1 bf16 ulp; v exact)
+    q_got = _host_u16(qkv)
+    sc.assert_rope_close(q_got[:, : N_Q * HEAD_DIM], ref["qkv"][:, : N_Q * HEAD_DIM], "q")
+    assert np.array_equal(q_got[:, N_Q * HEAD_DIM:], qkv_h[:, N_Q * HEAD_DIM:])  # k, v untouched
+    pool_got = _host_u16(pool).reshape(-1)
+    changed = pool_got != ref["pool"]
+    if changed.any():
+        sc.assert_rope_close(pool_got[changed], ref["pool"][changed], "pool")
+    pages, toks = sc.written_mask(ref["pack"], T)
+    for t in range(0, T, max(1, T // 64)):  # V exact on a sample of rows
+        for kvh in range(8):
+            base = ((pages[t] * 8 + kvh) * 2 + 1) * PAGE * HEAD_DIM
+            idx = base + np.arange(HEAD_DIM) * PAGE + toks[t]
+            assert np.array_equal(pool_got[idx], ref["pool"][idx])
+
+    # attention end to end
+    o_got = _host_u16(out)[:T]
+    mx, mean = sc.att_errors(o_got, ref["out"])
+    print(f"config{cfgno}: end-to-end max-abs {mx:.3e} mean-abs {mean:.3e}")
+    assert mx <= sc.ATT_MAX_ABS and mean <= sc.ATT_MEAN_ABS
+
+    # attention alone: oracle attention on the GPU's post-append qkv and pool
+    o_ref = np.zeros((T, N_Q * HEAD_DIM), np.uint16)
+    pk = ref["pack"]
+    orc.decode(q_got, pool_got.copy(), cfg.pool_pages, pk["block_tables"], kw["max_blocks"],
+               pk["cu_seqlens"], pk["positions"], pk["decode_rids"], int(pk["meta"][1]), o_ref)
+    orc.prefill(q_got, pool_got.copy(), cfg.pool_pages, pk["block_tables"], kw["max_blocks"],
+                pk["cu_seqlens"], pk["positions"], pk["prefill_rids"], int(pk["meta"][2]), o_ref)
+    mx, mean = sc.att_errors(o_got, o_ref)
+    print(f"config{cfgno}: kernel-only max-abs {mx:.3e} mean-abs {mean:.3e}")
+    assert mx <= sc.ATT_MAX_ABS and mean <= sc.ATT_MEAN_ABS
