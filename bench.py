@@ -1,0 +1,322 @@
+#!/usr/bin/env python3
+"""Benchmark of the per-step attention path on one MI355X.
+
+A step is one pass of the hot path over one synthetic batch: GPU pack, fused QK-norm/RoPE/
+paged append, decode (split-K + combine) and prefill, for every layer of the config.  The
+default workload is config 2 (64 decode sequences, contexts U[512, 4096], one Qwen3-8B
+layer); `--config 3|4|5` runs the others.  The step is captured once as a HIP graph and
+replayed (as the reference replays decode steps, model_runtime.cu:227-233); inputs are
+resident in HBM before timing starts.
+
+Prints ONE JSON line.  `roofline` is for the dominant kernel of the workload (decode: HBM
+bytes; prefill: MFMA flops), timed with HIP events around a graph of repeated launches of
+that kernel on the stream it is launched on.  `cpu_baseline` is the OpenMP fp32 CPU oracle
+(oracle/fqa_oracle.c) timed on a bounded sample of the same workload on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--kernel-reps", type=int, default=50)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--dec-target-items", type=int, default=1024)
+    ap.add_argument("--dec-min-split", type=int, default=8)
+    ap.add_argument("--layers", type=int, default=None, help="config 5 only (default 36)")
+    ap.add_argument("--profile-kernels", action="store_true",
+                    help="only run the per-kernel graphs (for rocprofv3 passes)")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the attention path is "
+                          "per-GPU work (kv-head or sequence sharding needs no exchange); "
+                          "run with --gpus 1"}))
+        sys.exit(2)
+
+    import torch
+
+    from flashqwen_amd import synth
+    from flashqwen_amd.step import AttnStep, alloc_pool
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.config == 5:
+        cfg = synth.config5(layers=args.layers or 36)
+    else:
+        cfg = synth.CONFIGS[args.config]()
+    layers = cfg.layers
+    scheduled = cfg.num_tokens is not None
+
+    # ---- batch as the scheduler would hand it over ------------------------------------
+    if scheduled:  # config 4: selection on the GPU; the oracle's selection sizes the rows
+        from oracle import oracle as orc
+
+        sel_req, sel_n = orc.schedule(cfg.num_tokens, cfg.computed, cfg.token_budget,
+                                      cfg.prefill_chunk)
+        T = int(sel_n.sum())
+        comp_sel = cfg.computed[sel_req]
+        n_sel = sel_n
+    else:
+        T = cfg.rows
+        comp_sel, n_sel = cfg.computed, cfg.n_new
+    has_decode = bool((n_sel == 1).any())
+    has_prefill = bool((n_sel != 1).any())
+
+    rng = np.random.default_rng(1234)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)  # noqa: E731
+    qkv = t(synth.rand_bf16(rng, (T, synth.QKV_STRIDE)).view(np.int16)).view(torch.bfloat16)
+    wq, wk = synth.norm_weights()
+    wq_d, wk_d = t(wq), t(wk)
+    pool = alloc_pool(cfg.pool_pages, layers, dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(99)
+    flat = pool.view(-1)
+    for s in range(0, flat.numel(), 1 << 30):
+        e = min(s + (1 << 30), flat.numel())
+        flat[s:e].normal_(generator=g)
+    out = torch.zeros((T, synth.N_Q * synth.HEAD_DIM), dtype=torch.bfloat16, device=dev)
+
+    step = AttnStep(max_rows=T, max_reqs=cfg.n_reqs, max_ctx=cfg.max_ctx,
+                    pool_pages=cfg.pool_pages, device=dev,
+                    dec_target_items=args.dec_target_items, dec_min_split=args.dec_min_split)
+    d_computed, d_n_new = t(cfg.computed), t(cfg.n_new)
+    d_off, d_pages = t(cfg.bt_off), t(cfg.bt_pages)
+    d_ntok = t(cfg.num_tokens) if scheduled else None
+
+    def pack():
+        if scheduled:
+            step.schedule_and_prepare(d_ntok, d_computed, d_off, d_pages, cfg.token_budget,
+                                      cfg.prefill_chunk, rows_bound=T)
+        else:
+            step.prepare_inputs(d_computed, d_n_new, d_off, d_pages, rows_bound=T)
+
+    def one_step():
+        pack()
+        for l in range(layers):
+            step.run_layer(qkv, pool[l], wq_d, wk_d, out, decode=has_decode,
+                           prefill=has_prefill)
+
+    # eager once (also validates the pack), then capture the step
+    one_step()
+    torch.cuda.synchronize()
+    meta = step.meta_host()
+    if meta[7] not in (0,):
+        raise SystemExit(f"pack status {meta[7]}")
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        one_step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        one_step()
+    torch.cuda.synchronize()
+
+    def kernel_graph(fn, reps):
+        kg = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(kg):
+            for _ in range(reps):
+                fn()
+        return kg
+
+    def time_graph(gr, n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n  # ms
+
+    reps = args.kernel_reps
+    kernels = {"pack": pack,
+               "qknorm_rope_append": lambda: step.head_norm_rope_store_kv(qkv, pool[0], wq_d,
+                                                                          wk_d)}
+    if has_decode:
+        kernels["decode"] = lambda: step.attn_decode(qkv, pool[0], out)
+    if has_prefill:
+        kernels["prefill"] = lambda: step.attn_prefill(qkv, pool[0], out)
+    kgraphs = {k: kernel_graph(f, reps) for k, f in kernels.items()}
+    torch.cuda.synchronize()
+    if args.profile_kernels:
+        for k, kg in kgraphs.items():
+            for _ in range(3):
+                kg.replay()
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_kernels": list(kgraphs)}))
+        return
+
+    # ---- timed region: K whole steps -----------------------------------------------------
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ms_events = time_graph(graph, args.steps)
+    wall = time.perf_counter() - t0
+    ms_step = ms_events
+
+    kern_ms = {}
+    for k, kg in kgraphs.items():
+        kg.replay()
+        torch.cuda.synchronize()
+        kern_ms[k] = time_graph(kg, 5) / reps
+
+    # ---- roofline of the dominant kernel ---------------------------------------------------
+    meta = step.meta_host()
+    if has_decode and (not has_prefill or args.config == 5):
+        logical, unique = synth.decode_bytes(_selected(cfg, comp_sel, n_sel))
+        bt_bytes = int(meta[9]) * 4
+        bytes_per = logical + bt_bytes
+        achieved = bytes_per / (kern_ms["decode"] * 1e-3) / 1e9
+        roof = {"kernel": "decode (fqa_decode: split-K + combine)", "bound": "hbm",
+                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "bytes_per_launch": bytes_per, "unique_kv_bytes": unique,
+                "launch_us": round(kern_ms["decode"] * 1e3, 2)}
+    else:
+        flops = synth.prefill_flops(comp_sel, n_sel)
+        achieved = flops / (kern_ms["prefill"] * 1e-3) / 1e12
+        roof = {"kernel": "prefill (fqa_prefill)", "bound": "mfma",
+                "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                "flops_per_launch": flops, "launch_us": round(kern_ms["prefill"] * 1e3, 2)}
+        if has_decode:
+            logical, _ = synth.decode_bytes(_selected(cfg, comp_sel, n_sel))
+            roof["decode_GBps"] = round(logical / (kern_ms["decode"] * 1e-3) / 1e9, 1)
+
+    # ---- CPU baseline (OpenMP fp32 oracle, bounded sample) ------------------------------
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(cfg, comp_sel, n_sel, T, args.cpu_seconds)
+
+    tokens_per_step = T
+    value = tokens_per_step / (ms_step * 1e-3)
+    line = {
+        "metric": "attn-step tokens/s",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 q/k/v and pool, seeded page placement)",
+        "config": {"workload": f"config{args.config}: {_describe(args.config)}",
+                   "rows_per_step": T, "requests": int(len(n_sel)), "layers": layers,
+                   "pool_pages_per_layer": cfg.pool_pages, "head_shape": "32q/8kv/128",
+                   "dec_split_pages": int(meta[6]), "dec_items": int(meta[4]),
+                   "pre_items": int(meta[5])},
+        "roofline": roof,
+        "kernels_us": {k: round(v * 1e3, 2) for k, v in kern_ms.items()},
+        "cpu_baseline": cpu,
+        "wall_s_timed": round(wall, 3),
+    }
+    print(json.dumps(line))
+
+
+def _selected(cfg, comp_sel, n_sel):
+    """A StepConfig view of the batch actually run (config 4 is selected on the GPU)."""
+    from flashqwen_amd import synth
+
+    if cfg.num_tokens is None:
+        return cfg
+    return synth.StepConfig(cfg.name, comp_sel, n_sel, np.zeros(len(n_sel) + 1, np.int32),
+                            np.zeros(0, np.int32), cfg.pool_pages, cfg.max_ctx)
+
+
+def _describe(n):
+    return {1: "4 decode seqs, L in {17,100,255,512}",
+            2: "64 decode seqs, L~U[512,4096], 1 layer, pool 200k tokens",
+            3: "16 log-normal prompts (median 400) within 8192 tokens, causal varlen prefill",
+            4: "mixed 8192-token budget: 2x2048 chunks on 3000 prefixes + 512/700/900 fresh + "
+               "256 decodes, selection on GPU",
+            5: "36 layers, 32x32768 + 96 shared-prefix decodes, ~200 GB pool"}[n]
+
+
+def cpu_baseline(cfg, comp_sel, n_sel, T, seconds):
+    """The OpenMP fp32 oracle on the same step: pack + norm/rope/append + decode + prefill,
+    on one layer, repeated for about `seconds`; tokens/s = rows / time per step (x layers)."""
+    from flashqwen_amd import synth
+    from oracle import oracle as orc
+    from tests import stepcase as sc
+
+    sub = cfg
+    if cfg.num_tokens is not None:
+        sel_req, _ = orc.schedule(cfg.num_tokens, cfg.computed, cfg.token_budget,
+                                  cfg.prefill_chunk)
+        tabs = cfg.tables()
+        sub = synth._assemble(cfg.name, comp_sel, n_sel, [tabs[i] for i in sel_req],
+                              cfg.pool_pages, cfg.max_ctx)
+    sample = "full step, one layer"
+    if cfg.name == "config5":
+        # a sample of 8 long and 24 shared-prefix sequences, re-paged into a compact pool
+        keep = list(range(8)) + list(range(32, 56))
+        sub, sample = _compact(cfg, keep), "8 of 32 long + 24 of 96 shared-prefix seqs, 1 layer"
+    rng = np.random.default_rng(5)
+    kw = sc.pack_kwargs(sub)
+    qkv = synth.rand_bf16(rng, (sub.rows, synth.QKV_STRIDE))
+    pool = synth.rand_bf16(rng, sc.pool_elems(sub.pool_pages))
+    wq, wk = synth.norm_weights()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while True:
+        t0 = time.perf_counter()
+        sc.oracle_chain(sub, qkv, pool, wq, wk, kw)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end or len(times) >= 50:
+            break
+    per = float(np.median(times))
+    rows = sub.rows
+    if cfg.name == "config5":
+        value = rows / (per * cfg.layers)
+        sample += f"; x{cfg.layers} layers extrapolated"
+    else:
+        value = rows / (per * cfg.layers)
+    return {"value": round(value, 2), "unit": "tokens/s", "cores": orc.num_threads(),
+            "kind": "port", "sample": f"{sample}; {len(times)} reps, median {per * 1e3:.1f} ms",
+            "nproc": os.cpu_count()}
+
+
+def _compact(cfg, keep):
+    """Subset of config 5's sequences with their pages renumbered into a small pool (shared
+    prefix pages stay shared)."""
+    from flashqwen_amd import synth
+
+    tabs = [cfg.tables()[i] for i in keep]
+    uniq = {p: i for i, p in enumerate(dict.fromkeys(np.concatenate(tabs).tolist()))}
+    new = [np.array([uniq[p] for p in tb], np.int32) for tb in tabs]
+    return synth._assemble(cfg.name, cfg.computed[keep], cfg.n_new[keep], new, len(uniq),
+                           cfg.max_ctx, layers=cfg.layers)
+
+
+if __name__ == "__main__":
+    main()

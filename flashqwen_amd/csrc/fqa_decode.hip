@@ -22,8 +22,9 @@
 //    way (about 5% of the CU's matrix rate at full HBM bandwidth).
 //  * P is rounded to bf16 for the PV product (the reference's decode keeps P in fp32;
 //    the difference is below the bf16 output rounding the tolerance allows).
-//  * The next page's 12 loads are issued before the current page's math
-//    (register double buffer), so every wave keeps 8 KiB in flight.
+//  * Pages rotate through four register buffers: while page p is processed the loads of
+//    p+1..p+3 are in flight, 24 KiB per wave (HBM latency x bandwidth needs ~64 KiB in
+//    flight per CU; at 2 waves per SIMD this gives ~190 KiB).
 //  * Sequences whose plan has one split write bf16 directly; the others write fp32
 //    partials (m, l, acc) and a combine wave per (sequence, kv head) merges them.
 #include "fqa_common.h"
@@ -69,6 +70,57 @@ __device__ __forceinline__ void load_page(PageFrag& f, const uint16_t* run, int 
     f.v[b] = *reinterpret_cast<const short4_t*>(run + kVOff + (b * 16 + m) * kPage + g * 4);
 }
 
+struct DecState {
+  float4_t acc[8];  // O^T: lane (col = head n, rows d = b*16 + 4g + j)
+  float m;          // running max (exp2 domain), same in the 4 lanes of a column
+  float l;          // running sum of this lane's 4 keys per page
+};
+
+// One page (16 keys) of online softmax for the 4 heads: S^T = K Q^T, P^T = exp2(S^T - m),
+// O^T = O^T * corr + V^T P^T.
+__device__ __forceinline__ void process_page(PageFrag& f, const bf16x8 (&qf)[4], int p, int L,
+                                             int g, float scale_log2, DecState& st) {
+  float4_t s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.k[ks], qf[ks], s, 0, 0, 0);
+  const int key0 = p * kPage + g * 4;
+  float sv[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    sv[j] = key0 + j < L ? s[j] * scale_log2 : -INFINITY;
+    mx = fmaxf(mx, sv[j]);
+  }
+  if ((p + 1) * kPage > L) {  // last page: unwritten slots must not reach PV
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (key0 + j >= L) f.v[b][j] = 0;
+  }
+  mx = wave_max_xor(mx, 16);
+  mx = wave_max_xor(mx, 32);
+  const float m_new = fmaxf(st.m, mx);
+  const float corr = exp2f(st.m - m_new);
+  float pj[4], psum = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    pj[j] = exp2f(sv[j] - m_new);
+    psum += pj[j];
+  }
+  st.l = st.l * corr + psum;
+  st.m = m_new;
+  short4_t pt;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) pt[j] = (short)f32_to_bf16_bits(pj[j]);
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    st.acc[b] *= corr;
+    st.acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(f.v[b], pt, st.acc[b], 0, 0, 0);
+  }
+}
+
 __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel(DecArgs a) {
   const int wave = blockIdx.x * kDecWavesPerBlock + (threadIdx.x >> 6);
   const int item = wave >> 3, kvh = wave & 7;
@@ -95,68 +147,40 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
       for (int i = 0; i < 8; ++i) qf[ks][i] = (__bf16)0.0f;
   }
 
-  float4_t acc[8];
+  DecState st;
 #pragma unroll
-  for (int b = 0; b < 8; ++b) acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run = -1e30f, l_run = 0.f;
+  for (int b = 0; b < 8; ++b) st.acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
+  st.m = -1e30f;
+  st.l = 0.f;
 
-  auto page_ptr = [&](int p, bool& ok) {
-    long long page = btr[p];
+  auto load = [&](PageFrag& f, bool& ok, int p) {
+    const long long page = btr[p];
     ok = page >= 0 && page < a.pool_pages;
-    return a.pool + run_offset(ok ? page : 0, kvh);
+    load_page(f, a.pool + run_offset(ok ? page : 0, kvh), lane);
   };
-
-  PageFrag cur, nxt;
-  bool ok_cur, ok_nxt = false;
-  load_page(cur, page_ptr(pb, ok_cur), lane);
-  for (int p = pb; p < pe; ++p) {
-    if (p + 1 < pe) load_page(nxt, page_ptr(p + 1, ok_nxt), lane);
-    if (ok_cur) {
-      float4_t s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.k[ks], qf[ks], s, 0, 0, 0);
-      const int key0 = p * kPage + g * 4;
-      float sv[4];
-      float mx = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        sv[j] = key0 + j < L ? s[j] * a.scale_log2 : -INFINITY;
-        mx = fmaxf(mx, sv[j]);
-      }
-      if ((p + 1) * kPage > L) {  // last page: unwritten slots must not reach PV
-#pragma unroll
-        for (int b = 0; b < 8; ++b)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (key0 + j >= L) cur.v[b][j] = 0;
-      }
-      mx = wave_max_xor(mx, 16);
-      mx = wave_max_xor(mx, 32);
-      const float m_new = fmaxf(m_run, mx);
-      const float corr = exp2f(m_run - m_new);
-      float pj[4], psum = 0.f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        pj[j] = exp2f(sv[j] - m_new);
-        psum += pj[j];
-      }
-      l_run = l_run * corr + psum;
-      m_run = m_new;
-      short4_t pt;
-      pt[0] = (short)f32_to_bf16_bits(pj[0]);
-      pt[1] = (short)f32_to_bf16_bits(pj[1]);
-      pt[2] = (short)f32_to_bf16_bits(pj[2]);
-      pt[3] = (short)f32_to_bf16_bits(pj[3]);
-#pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        acc[b] *= corr;
-        acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(cur.v[b], pt, acc[b], 0, 0, 0);
-      }
-    }
-    cur = nxt;
-    ok_cur = ok_nxt;
+  // Four page buffers in registers: page p is processed while p+1..p+3 are in flight
+  // (24 KiB per wave).  The buffers rotate through a 4-way unrolled loop so every index
+  // is static.
+  PageFrag f0, f1, f2, f3;
+  bool k0 = false, k1 = false, k2 = false, k3 = false;
+  load(f0, k0, pb);
+  if (pb + 1 < pe) load(f1, k1, pb + 1);
+  if (pb + 2 < pe) load(f2, k2, pb + 2);
+  for (int p = pb; p < pe; p += 4) {
+    if (p + 3 < pe) load(f3, k3, p + 3);
+    if (k0) process_page(f0, qf, p, L, g, a.scale_log2, st);
+    if (p + 1 >= pe) break;
+    if (p + 4 < pe) load(f0, k0, p + 4);
+    if (k1) process_page(f1, qf, p + 1, L, g, a.scale_log2, st);
+    if (p + 2 >= pe) break;
+    if (p + 5 < pe) load(f1, k1, p + 5);
+    if (k2) process_page(f2, qf, p + 2, L, g, a.scale_log2, st);
+    if (p + 3 >= pe) break;
+    if (p + 6 < pe) load(f2, k2, p + 6);
+    if (k3) process_page(f3, qf, p + 3, L, g, a.scale_log2, st);
   }
+  float l_run = st.l, m_run = st.m;
+  float4_t* acc = st.acc;
   l_run += __shfl_xor(l_run, 16, kWave);
   l_run += __shfl_xor(l_run, 32, kWave);
   if (n >= kG) return;
@@ -183,33 +207,34 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
   for (int b = 0; b < 8; ++b) *reinterpret_cast<float4_t*>(wa + b * 16) = acc[b];
 }
 
-// Log-sum-exp merge of a sequence's split partials (attn_cute.cu:225-238): one wave
-// per (decode sequence, kv head); lane -> (head = lane/16, 8 dims).
+// Log-sum-exp merge of a sequence's split partials (attn_cute.cu:225-238): one wave per
+// (decode sequence, query head), lane -> 2 dims; splits are folded with an online
+// max so the loop carries no second pass and its loads can run ahead.
 __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_combine_kernel(DecArgs a) {
   const int wave = blockIdx.x * kDecWavesPerBlock + (threadIdx.x >> 6);
-  const int di = wave >> 3, kvh = wave & 7;
+  const int di = wave / kHq, h = wave % kHq;
   if (di >= a.meta[FQA_META_N_DECODE]) return;
   const int i0 = a.item_start[di], i1 = a.item_start[di + 1];
   if (i1 - i0 <= 1) return;
   const int lane = threadIdx.x & 63;
-  const int h = lane >> 4, d0 = (lane & 15) * 8;
-  float gm = -1e30f;
-  for (int it = i0; it < i1; ++it) gm = fmaxf(gm, a.ws_m[((long long)it * kHkv + kvh) * kG + h]);
-  float gl = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const int kvh = h / kG, hh = h % kG;
+  float gm = -1e30f, gl = 0.f, a0 = 0.f, a1 = 0.f;
+#pragma unroll 4
   for (int it = i0; it < i1; ++it) {
-    const long long slot = ((long long)it * kHkv + kvh) * kG + h;
-    const float c = exp2f(a.ws_m[slot] - gm);
-    gl += a.ws_l[slot] * c;
-    const float4* src = reinterpret_cast<const float4*>(a.ws_acc + slot * kD + d0);
-    float4 x0 = src[0], x1 = src[1];
-    acc[0] += x0.x * c; acc[1] += x0.y * c; acc[2] += x0.z * c; acc[3] += x0.w * c;
-    acc[4] += x1.x * c; acc[5] += x1.y * c; acc[6] += x1.z * c; acc[7] += x1.w * c;
+    const long long slot = ((long long)it * kHkv + kvh) * kG + hh;
+    const float m = a.ws_m[slot], l = a.ws_l[slot];
+    const float2 x = *reinterpret_cast<const float2*>(a.ws_acc + slot * kD + 2 * lane);
+    const float mn = fmaxf(gm, m);
+    const float co = exp2f(gm - mn), cn = exp2f(m - mn);
+    gl = gl * co + l * cn;
+    a0 = a0 * co + x.x * cn;
+    a1 = a1 * co + x.y * cn;
+    gm = mn;
   }
   const float inv = gl > 0.f ? 1.0f / gl : 0.f;
   const int row = a.cu[a.decode_rids[di]];
-  uint4 v = make_uint4(pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv),
-                       pack_bf16x2(acc[4] * inv, acc[5] * inv), pack_bf16x2(acc[6] * inv, acc[7] * inv));
-  *reinterpret_cast<uint4*>(a.out + (long long)row * (kHq * kD) + (kvh * kG + h) * kD + d0) = v;
+  *reinterpret_cast<uint32_t*>(a.out + (long long)row * (kHq * kD) + h * kD + 2 * lane) =
+      pack_bf16x2(a0 * inv, a1 * inv);
 }
 
 bool dims_ok(const fqa_dims* d) {
@@ -253,7 +278,7 @@ int fqa_decode(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
   const int waves1 = dec_item_cap * kHkv;
   hipLaunchKernelGGL(decode_split_kernel, dim3((waves1 + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
                      dim3(kDecWavesPerBlock * kWave), 0, (hipStream_t)stream, a);
-  const int waves2 = n_reqs_bound * kHkv;
+  const int waves2 = n_reqs_bound * kHq;
   hipLaunchKernelGGL(decode_combine_kernel,
                      dim3((waves2 + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
                      dim3(kDecWavesPerBlock * kWave), 0, (hipStream_t)stream, a);

@@ -20,10 +20,11 @@
 namespace fqa {
 namespace {
 
-constexpr int kPackThreads = 256;
+constexpr int kPackThreads = 1024;
+constexpr int kPackWaves = kPackThreads / 64;
 
-// Exclusive scan of one value per thread over a 256-thread workgroup; returns the
-// thread's exclusive prefix and the total via *total.  `sh` holds >= 4 ints.
+// Exclusive scan of one value per thread over the workgroup; returns the thread's
+// exclusive prefix and the total via *total.  `sh` holds >= kPackWaves values.
 template <typename T>
 __device__ T block_excl_scan(T v, T* sh, T* total) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
@@ -61,6 +62,82 @@ __device__ T block_reduce(T v, T* sh, Op op) {
   return r;
 }
 
+// The per-request totals of pass 1 (code: min, rows/dpages: saturating sum,
+// dmax/qmax: max) reduced together, and the five exclusive scans of pass 2 done
+// together.  Small kernels here are bound by instruction fetch (the instruction cache
+// starts cold at every dispatch), so these loops are kept rolled: code size, not
+// instruction count, sets their latency.
+__device__ __forceinline__ int sat_add(int a, int b) {
+  long long s = (long long)a + b;
+  return s > INT_MAX ? INT_MAX : (int)s;
+}
+
+struct Stats {
+  int v[5];  // code, rows, dpages, dmax, qmax
+};
+
+__device__ __forceinline__ void stats_combine(Stats& a, const Stats& b) {
+  a.v[0] = min(a.v[0], b.v[0]);
+  a.v[1] = sat_add(a.v[1], b.v[1]);
+  a.v[2] = sat_add(a.v[2], b.v[2]);
+  a.v[3] = max(a.v[3], b.v[3]);
+  a.v[4] = max(a.v[4], b.v[4]);
+}
+
+__device__ Stats block_reduce_stats(Stats v, Stats* sh) {
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
+#pragma unroll 1
+  for (int d = 1; d < kWave; d <<= 1) {
+    Stats o;
+#pragma unroll
+    for (int k = 0; k < 5; ++k) o.v[k] = __shfl_xor(v.v[k], d, kWave);
+    stats_combine(v, o);
+  }
+  if (lane == 0) sh[w] = v;
+  __syncthreads();
+  Stats r = sh[0];
+#pragma unroll 1
+  for (int i = 1; i < kPackWaves; ++i) stats_combine(r, sh[i]);
+  __syncthreads();
+  return r;
+}
+
+struct Counts {
+  int v[5];
+};
+
+__device__ Counts block_excl_scan5(const Counts& in, Counts* sh, Counts* total) {
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
+  Counts x = in;
+#pragma unroll 1
+  for (int d = 1; d < kWave; d <<= 1) {
+    int y[5];
+#pragma unroll
+    for (int k = 0; k < 5; ++k) y[k] = __shfl_up(x.v[k], d, kWave);
+    if (lane >= d)
+#pragma unroll
+      for (int k = 0; k < 5; ++k) x.v[k] += y[k];
+  }
+  if (lane == kWave - 1) sh[w] = x;
+  __syncthreads();
+  Counts base = {{0, 0, 0, 0, 0}}, tot = {{0, 0, 0, 0, 0}};
+#pragma unroll 1
+  for (int i = 0; i < kPackWaves; ++i) {
+    const Counts s = sh[i];
+#pragma unroll
+    for (int k = 0; k < 5; ++k) {
+      if (i < w) base.v[k] += s.v[k];
+      tot.v[k] += s.v[k];
+    }
+  }
+  __syncthreads();
+  *total = tot;
+  Counts out;
+#pragma unroll
+  for (int k = 0; k < 5; ++k) out.v[k] = base.v[k] + x.v[k] - in.v[k];
+  return out;
+}
+
 struct MinOp { __device__ int operator()(int a, int b) const { return a < b ? a : b; } };
 struct MaxOp { __device__ int operator()(int a, int b) const { return a > b ? a : b; } };
 struct SumOp64 {
@@ -94,8 +171,9 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   __shared__ int s_preidx[FQA_MAX_REQS + 1];
   __shared__ int s_decit[FQA_MAX_REQS + 1];
   __shared__ int s_preit[FQA_MAX_REQS + 1];
-  __shared__ long long sh64[4];
-  __shared__ int sh32[4];
+  __shared__ Stats s_stats[kPackWaves];
+  __shared__ Counts s_counts[kPackWaves];
+  __shared__ int sh32[kPackWaves];
 
   const int tid = threadIdx.x;
   int R = a.b.n_reqs_dev ? *a.b.n_reqs_dev : a.b.n_reqs;
@@ -105,45 +183,41 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   const int maxb = a.c.max_blocks;
 
   // ---- pass 1: load, structural checks, totals ---------------------------------
-  int code = INT_MAX;
-  long long rows = 0, dpages = 0;
-  int dmax = 0, qmax = 1;
+  Stats st = {{INT_MAX, 0, 0, 0, 1}};
   for (int r = tid; r < R; r += kPackThreads) {
-    int c = a.b.computed[r], n = a.b.n_new[r];
-    int o0 = a.b.bt_off[r], o1 = a.b.bt_off[r + 1];
+    const int c = a.b.computed[r], n = a.b.n_new[r];
+    const int o0 = a.b.bt_off[r], o1 = a.b.bt_off[r + 1];
     s_comp[r] = c;
     s_n[r] = n;
     s_btoff[r] = o0;
     int cc = 0;
     if (c < 0 || n < 0) cc = FQA_PACK_NEGATIVE;
     else {
-      int nb = o1 - o0;
+      const int nb = o1 - o0;
       if (nb < cdiv((long long)c + n, kPage)) cc = FQA_PACK_SHORT_TABLE;
       else if (nb > maxb) cc = FQA_PACK_WIDE_TABLE;
-      rows += n;
+      st.v[1] = sat_add(st.v[1], n);
       if (n == 1) {
-        int pg = c / kPage + 1;
-        dpages += pg;
-        dmax = pg > dmax ? pg : dmax;
-      } else if (n > qmax) {
-        qmax = n;
+        const int pg = c / kPage + 1;
+        st.v[2] = sat_add(st.v[2], pg);
+        st.v[3] = max(pg, st.v[3]);
+      } else {
+        st.v[4] = max(n, st.v[4]);
       }
     }
-    if (cc && cc < code) code = cc;
+    if (cc) st.v[0] = min(st.v[0], cc);
   }
   if (tid == 0) s_btoff[R] = a.b.bt_off[R];
-  code = block_reduce(code, sh32, MinOp());
-  rows = block_reduce(rows, sh64, SumOp64());
-  dpages = block_reduce(dpages, sh64, SumOp64());
-  dmax = block_reduce(dmax, sh32, MaxOp());
-  qmax = block_reduce(qmax, sh32, MaxOp());
+  st = block_reduce_stats(st, s_stats);
+  int code = st.v[0];
+  const int rows = st.v[1], dpages = st.v[2], dmax = st.v[3], qmax = st.v[4];
   if (rows > a.c.max_rows && code > FQA_PACK_ROWS) code = FQA_PACK_ROWS;
   if (code != INT_MAX) {
     if (blockIdx.x == 0 && tid < FQA_META_LEN)
       a.o.meta[tid] = tid == FQA_META_STATUS ? code : (tid == FQA_META_REQS ? R : 0);
     return;
   }
-  const int T = (int)rows;
+  const int T = rows;
 
   // decode split size (pages per work item)
   int S;
@@ -156,38 +230,36 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
 
   // ---- pass 2: exclusive scans over requests ------------------------------------
   {
-    int cq = 0, cd = 0, cp = 0, cdi = 0, cpi = 0;
+    Counts carry = {{0, 0, 0, 0, 0}};
     for (int base = 0; base < R; base += kPackThreads) {
-      int r = base + tid;
-      int n = 0, isd = 0, isp = 0, di = 0, pi = 0;
+      const int r = base + tid;
+      Counts v = {{0, 0, 0, 0, 0}};
       if (r < R) {
-        n = s_n[r];
-        isd = n == 1;
-        isp = !isd;
-        di = isd ? cdiv(s_comp[r] / kPage + 1, S) : 0;
-        pi = isp ? cdiv(n, QT) : 0;
+        const int n = s_n[r];
+        v.v[0] = n;
+        v.v[1] = n == 1;
+        v.v[2] = n != 1;
+        v.v[3] = n == 1 ? (s_comp[r] / kPage + S) / S : 0;  // ceil(pages / S)
+        v.v[4] = n != 1 ? (n + QT - 1) / QT : 0;
       }
-      int t0, t1, t2, t3, t4;
-      int e0 = block_excl_scan(n, sh32, &t0);
-      int e1 = block_excl_scan(isd, sh32, &t1);
-      int e2 = block_excl_scan(isp, sh32, &t2);
-      int e3 = block_excl_scan(di, sh32, &t3);
-      int e4 = block_excl_scan(pi, sh32, &t4);
+      Counts tot;
+      const Counts e = block_excl_scan5(v, s_counts, &tot);
       if (r < R) {
-        s_qstart[r] = cq + e0;
-        s_decidx[r] = cd + e1;
-        s_preidx[r] = cp + e2;
-        s_decit[r] = cdi + e3;
-        s_preit[r] = cpi + e4;
+        s_qstart[r] = carry.v[0] + e.v[0];
+        s_decidx[r] = carry.v[1] + e.v[1];
+        s_preidx[r] = carry.v[2] + e.v[2];
+        s_decit[r] = carry.v[3] + e.v[3];
+        s_preit[r] = carry.v[4] + e.v[4];
       }
-      cq += t0; cd += t1; cp += t2; cdi += t3; cpi += t4;
+#pragma unroll
+      for (int k = 0; k < 5; ++k) carry.v[k] += tot.v[k];
     }
     if (tid == 0) {
-      s_qstart[R] = cq;
-      s_decidx[R] = cd;
-      s_preidx[R] = cp;
-      s_decit[R] = cdi;
-      s_preit[R] = cpi;
+      s_qstart[R] = carry.v[0];
+      s_decidx[R] = carry.v[1];
+      s_preidx[R] = carry.v[2];
+      s_decit[R] = carry.v[3];
+      s_preit[R] = carry.v[4];
     }
     __syncthreads();
   }
@@ -232,25 +304,28 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     }
   }
   // ---- prefill items, sorted by key count descending (stable) --------------------
-  for (int i = gtid; i < npi; i += gsz) {
-    // locate item i: request r with s_preit[r] <= i < s_preit[r+1] and prefill
-    int r = upper_index(s_preit, R, i);
-    int t = i - s_preit[r];
-    int n = s_n[r], c = s_comp[r];
-    int q0 = t * QT, q1 = q0 + QT < n ? q0 + QT : n;
-    int nk = c + q1;
+  // Tile t of prefill request r covers rows [t*QT, min((t+1)*QT, n)) and needs
+  // c + min((t+1)*QT, n) keys, so per request the number of tiles with more keys than X
+  // (and with exactly X) has a closed form; an item's rank is a sum over requests.
+  for (int i = blockIdx.x + tid * gridDim.x; i < npi; i += gsz) {
+    const int r = upper_index(s_preit, R, i);  // the prefill request owning item i
+    const int t = i - s_preit[r];
+    const int n = s_n[r], c = s_comp[r];
+    const int q0 = t * QT, q1 = min(q0 + QT, n);
+    const int X = c + q1;
     int rank = 0;
     for (int rr = 0; rr < R; ++rr) {
-      int nn = s_n[rr];
-      if (nn == 1 || nn == 0) continue;
-      int cc = s_comp[rr], nt = cdiv(nn, QT), j0 = s_preit[rr];
-      for (int tt = 0; tt < nt; ++tt) {
-        int qq1 = (tt + 1) * QT < nn ? (tt + 1) * QT : nn;
-        int k = cc + qq1;
-        rank += (k > nk) || (k == nk && j0 + tt < i);
-      }
+      const int nt = s_preit[rr + 1] - s_preit[rr];
+      if (nt == 0) continue;  // decode request or empty prefill
+      const int cc = s_comp[rr], nn = s_n[rr], y = X - cc;
+      const int k = y < 0 ? 0 : y / QT;
+      rank += (cc + nn > X) + max(0, nt - 1 - k);  // tiles with more keys than X
+      // tiles with exactly X keys that come earlier in (request, tile) order
+      const int te = (y > 0 && y % QT == 0 && y / QT - 1 < nt - 1) ? y / QT - 1
+                     : (cc + nn == X ? nt - 1 : -1);
+      if (te >= 0 && (rr < r || (rr == r && te < t))) ++rank;
     }
-    *reinterpret_cast<int4*>(a.o.pre_items + 4 * (long long)rank) = make_int4(r, q0, q1, nk);
+    *reinterpret_cast<int4*>(a.o.pre_items + 4 * (long long)rank) = make_int4(r, q0, q1, X);
   }
 
   if (blockIdx.x != 0) return;
@@ -274,11 +349,29 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     if (i == nd) a.o.dec_item_start[i] = ndi;
     else if (i > nd) a.o.dec_item_start[i] = -1;
   }
+  // page-id range check over the concatenated tables: 16-byte loads, 4 in flight per
+  // thread (the scalar head and tail are the at most 3 ids on either side of alignment)
   int bad = 0;
-  const int npages = s_btoff[R] - s_btoff[0];
-  for (int e = tid; e < npages; e += kPackThreads) {
-    int v = a.b.bt_pages[s_btoff[0] + e];
-    bad |= v < 0 || (long long)v >= a.c.pool_pages;
+  {
+    const int32_t* pg = a.b.bt_pages + s_btoff[0];
+    const int npages = s_btoff[R] - s_btoff[0];
+    const int lead = min(npages, (int)(((16 - ((uintptr_t)pg & 15)) & 15) >> 2));
+    const int nvec = (npages - lead) >> 2;
+    const int4* pv = reinterpret_cast<const int4*>(pg + lead);
+    const long long np64 = a.c.pool_pages;
+    auto badv = [&](int v) { return v < 0 || (long long)v >= np64; };
+    for (int e = tid; e < lead; e += kPackThreads) bad |= badv(pg[e]);
+    for (int e = lead + 4 * nvec + tid; e < npages; e += kPackThreads) bad |= badv(pg[e]);
+    for (int base = 0; base < nvec; base += 4 * kPackThreads) {
+      int4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = base + u * kPackThreads + tid;
+        v[u] = e < nvec ? pv[e] : make_int4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) bad |= (int)badv(v[u].x) | (int)badv(v[u].y) | (int)badv(v[u].z) | (int)badv(v[u].w);
+    }
   }
   bad = block_reduce(bad, sh32, MaxOp());
   if (tid < FQA_META_LEN) {
@@ -394,7 +487,7 @@ gather_kernel(const int32_t* __restrict__ batch_req, const int32_t* __restrict__
               int32_t* out_n_new, int32_t* out_bt_off, int32_t* out_bt_pages, int cap) {
   __shared__ int s_off[FQA_MAX_REQS + 1];
   __shared__ int s_src[FQA_MAX_REQS];
-  __shared__ int sh32[4];
+  __shared__ int sh32[kPackWaves];
   const int tid = threadIdx.x;
   int R = *n_batch;
   if (R > R_bound) R = R_bound;
@@ -486,7 +579,7 @@ int fqa_pack(const fqa_batch* batch, const fqa_pack_cfg* cfg, const fqa_pack_out
     return FQA_EINVAL;
   long long work = (long long)R * cfg->max_blocks;
   if (cfg->max_rows > work) work = cfg->max_rows;
-  long long grid = (work + 4 * kPackThreads - 1) / (4 * kPackThreads);
+  long long grid = (work + 2 * kPackThreads - 1) / (2 * kPackThreads);
   grid = grid < 1 ? 1 : (grid > 256 ? 256 : grid);
   PackArgs a{*batch, *cfg, *out};
   hipLaunchKernelGGL(pack_kernel, dim3((unsigned)grid), dim3(kPackThreads), 0,
