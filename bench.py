@@ -41,8 +41,9 @@ def parse():
     ap.add_argument("--kernel-reps", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--dec-target-items", type=int, default=1024)
-    ap.add_argument("--dec-min-split", type=int, default=8)
+    ap.add_argument("--dec-grid-waves", type=int, default=None,
+                    help="decode wavefronts (default: CUs x 8)")
+    ap.add_argument("--dec-min-pages", type=int, default=8)
     ap.add_argument("--layers", type=int, default=None, help="config 5 only (default 36)")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only run the per-kernel graphs (for rocprofv3 passes)")
@@ -103,7 +104,7 @@ def main():
 
     step = AttnStep(max_rows=T, max_reqs=cfg.n_reqs, max_ctx=cfg.max_ctx,
                     pool_pages=cfg.pool_pages, device=dev,
-                    dec_target_items=args.dec_target_items, dec_min_split=args.dec_min_split)
+                    dec_grid_waves=args.dec_grid_waves, dec_min_pages=args.dec_min_pages)
     d_computed, d_n_new = t(cfg.computed), t(cfg.n_new)
     d_off, d_pages = t(cfg.bt_off), t(cfg.bt_pages)
     d_ntok = t(cfg.num_tokens) if scheduled else None
@@ -233,7 +234,7 @@ def main():
         "config": {"workload": f"config{args.config}: {_describe(args.config)}",
                    "rows_per_step": T, "requests": int(len(n_sel)), "layers": layers,
                    "pool_pages_per_layer": cfg.pool_pages, "head_shape": "32q/8kv/128",
-                   "dec_split_pages": int(meta[6]), "dec_items": int(meta[4]),
+                   "dec_wave_runs": int(meta[6]), "dec_waves": int(meta[4]),
                    "pre_items": int(meta[5])},
         "roofline": roof,
         "kernels_us": {k: round(v * 1e3, 2) for k, v in kern_ms.items()},

@@ -18,7 +18,7 @@ FQA_PAGE_TOKENS = 16
 FQA_MAX_REQS = 2048
 
 META_ROWS, META_N_DECODE, META_N_PREFILL, META_MAX_QLEN = 0, 1, 2, 3
-META_DEC_ITEMS, META_PRE_ITEMS, META_SPLIT_PAGES, META_STATUS = 4, 5, 6, 7
+META_DEC_WAVES, META_PRE_ITEMS, META_DEC_WAVE_PAGES, META_STATUS = 4, 5, 6, 7
 META_REQS, META_DEC_PAGES = 8, 9
 META_LEN = 16
 
@@ -63,8 +63,8 @@ class FqaPackOut(C.Structure):
         ("block_tables", P),
         ("decode_rids", P),
         ("prefill_rids", P),
-        ("dec_item_start", P),
-        ("dec_items", P),
+        ("dec_seqs", P),
+        ("dec_waves", P),
         ("pre_items", P),
         ("meta", P),
     ]
@@ -75,9 +75,9 @@ class FqaPackCfg(C.Structure):
         ("max_rows", I32),
         ("max_blocks", I32),
         ("pool_pages", I64),
-        ("dec_target_items", I32),
-        ("dec_min_split", I32),
-        ("dec_item_cap", I32),
+        ("dec_grid_waves", I32),
+        ("dec_min_pages", I32),
+        ("dec_wave_cap", I32),
         ("pre_tile_q", I32),
         ("pre_item_cap", I32),
     ]
@@ -87,7 +87,8 @@ class FqaPackCfg(C.Structure):
 SIGNATURES = {
     "fqa_rope_tables": (C.c_int, [I32, I32, C.c_float, P, P]),
     "fqa_pool_bytes": (I64, [C.POINTER(FqaDims), I64]),
-    "fqa_dec_item_bound": (I32, [I32, I32]),
+    "fqa_dec_wave_bound": (I32, [I32, I32]),
+    "fqa_dec_default_waves": (I32, [I32]),
     "fqa_pre_item_bound": (I32, [I32, I32, I32]),
     "fqa_decode_workspace_bytes": (I64, [C.POINTER(FqaDims), I32]),
     "fqa_schedule": (C.c_int, [P, P, I32, I32, I32, P, P, P, P]),
@@ -99,7 +100,7 @@ SIGNATURES = {
     ),
     "fqa_decode": (
         C.c_int,
-        [C.POINTER(FqaDims), P, P, I64, P, I32, P, P, P, P, P, P, I32, I32, P, P, P],
+        [C.POINTER(FqaDims), P, P, I64, P, I32, P, P, P, I32, I32, P, P, P],
     ),
     "fqa_prefill": (
         C.c_int,

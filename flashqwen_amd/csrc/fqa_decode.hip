@@ -6,11 +6,16 @@
 // online softmax; partials merged by log-sum-exp; output bf16, 0 when l == 0.
 //
 // MI355X design:
-//  * One wavefront per (work item, kv head).  A work item is a page range of one
-//    sequence sized by the pack so that all sequences split into near-equal pieces
-//    (the reference uses one split factor 128/n_decode for every sequence,
-//    attn_cute.cu:249-251).  Each (page, kv head) is one contiguous 8 KiB run
-//    (K [16][128] then V^T [128][16]) that the wave reads exactly once for all 4 heads.
+//  * Stream-K split: the (sequence, kv head) page streams of all decode requests are
+//    laid end to end and cut into equal shares, one per wavefront of a grid sized to
+//    the machine (CUs x resident waves), so every wavefront streams the same number of
+//    8 KiB runs and they all finish together (the reference fixes one split factor
+//    128/n_decode for every sequence, attn_cute.cu:249-251, which leaves long tails when
+//    lengths differ).  A stream inside one share is finished in place; a share boundary
+//    that cuts a stream leaves fp32 partials, at most two per wavefront, which a
+//    log-sum-exp combine merges.
+//  * Each (page, kv head) is one contiguous 8 KiB run (K [16][128] then V^T [128][16])
+//    read exactly once for all 4 query heads of the kv head.
 //  * Both products run on MFMA in transposed form so that no operand is ever
 //    shuffled between lanes:
 //        S^T[16 keys x 16 cols] = K[16 x 128] . Q^T[128 x 16]  (4 x mfma 16x16x32 bf16)
@@ -25,8 +30,6 @@
 //  * Pages rotate through four register buffers: while page p is processed the loads of
 //    p+1..p+3 are in flight, 24 KiB per wave (HBM latency x bandwidth needs ~64 KiB in
 //    flight per CU; at 2 waves per SIMD this gives ~190 KiB).
-//  * Sequences whose plan has one split write bf16 directly; the others write fp32
-//    partials (m, l, acc) and a combine wave per (sequence, kv head) merges them.
 #include "fqa_common.h"
 
 namespace fqa {
@@ -41,11 +44,8 @@ struct DecArgs {
   long long pool_pages;
   const int32_t* bt;
   int max_blocks;
-  const int32_t* cu;
-  const int32_t* pos;
-  const int32_t* items;
-  const int32_t* item_start;
-  const int32_t* decode_rids;
+  const int32_t* waves;  // [G][4] {di, kvh, page, n_runs}
+  const int32_t* seqs;   // [n_decode][4] {r, row, n_keys, 8*P}
   const int32_t* meta;
   float* ws_m;
   float* ws_l;
@@ -121,46 +121,18 @@ __device__ __forceinline__ void process_page(PageFrag& f, const bf16x8 (&qf)[4],
   }
 }
 
-__global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel(DecArgs a) {
-  const int wave = blockIdx.x * kDecWavesPerBlock + (threadIdx.x >> 6);
-  const int item = wave >> 3, kvh = wave & 7;
-  if (item >= a.meta[FQA_META_DEC_ITEMS]) return;
-  const int lane = threadIdx.x & 63;
-  const int n = lane & 15, g = lane >> 4;
-
-  const int4 it = *reinterpret_cast<const int4*>(a.items + 4 * (long long)item);
-  const int r = it.x, pb = it.z, pe = it.w;
-  const int row = a.cu[r];
-  const int L = a.pos[row] + 1;  // keys [0, L)
-  const int32_t* btr = a.bt + (long long)r * a.max_blocks;
-
-  // Q^T as the B operand: column n = head (kvh*4 + n) for n < 4, zeros elsewhere.
-  bf16x8 qf[4];
-  if (n < kG) {
-    const uint16_t* q = a.qkv + (long long)row * a.stride + (kvh * kG + n) * kD + g * 8;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(q + ks * 32);
-  } else {
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qf[ks][i] = (__bf16)0.0f;
-  }
-
-  DecState st;
-#pragma unroll
-  for (int b = 0; b < 8; ++b) st.acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
-  st.m = -1e30f;
-  st.l = 0.f;
-
+// Stream pages [pb, pe) of (sequence `seq`, kv head kvh) into `st`.
+__device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* btr, int kvh,
+                                             int pb, int pe, int L, const bf16x8 (&qf)[4],
+                                             int lane, DecState& st) {
+  const int g = lane >> 4;
   auto load = [&](PageFrag& f, bool& ok, int p) {
     const long long page = btr[p];
     ok = page >= 0 && page < a.pool_pages;
     load_page(f, a.pool + run_offset(ok ? page : 0, kvh), lane);
   };
-  // Four page buffers in registers: page p is processed while p+1..p+3 are in flight
-  // (24 KiB per wave).  The buffers rotate through a 4-way unrolled loop so every index
-  // is static.
+  // Four page buffers in registers: page p is processed while p+1..p+3 are in flight.
+  // The buffers rotate through a 4-way unrolled loop so every index is static.
   PageFrag f0, f1, f2, f3;
   bool k0 = false, k1 = false, k2 = false, k3 = false;
   load(f0, k0, pb);
@@ -179,62 +151,114 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
     if (p + 6 < pe) load(f2, k2, p + 6);
     if (k3) process_page(f3, qf, p + 3, L, g, a.scale_log2, st);
   }
-  float l_run = st.l, m_run = st.m;
-  float4_t* acc = st.acc;
-  l_run += __shfl_xor(l_run, 16, kWave);
-  l_run += __shfl_xor(l_run, 32, kWave);
-  if (n >= kG) return;
-
-  const int pages = (L + kPage - 1) / kPage;
-  if (pb == 0 && pe == pages) {  // the only split of this sequence: final output
-    const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
-    uint16_t* o = a.out + (long long)row * (kHq * kD) + (kvh * kG + n) * kD + g * 4;
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      uint2 v = make_uint2(pack_bf16x2(acc[b][0] * inv, acc[b][1] * inv),
-                           pack_bf16x2(acc[b][2] * inv, acc[b][3] * inv));
-      *reinterpret_cast<uint2*>(o + b * 16) = v;
-    }
-    return;
-  }
-  const long long slot = ((long long)item * kHkv + kvh) * kG + n;
-  if (g == 0) {
-    a.ws_m[slot] = m_run;
-    a.ws_l[slot] = l_run;
-  }
-  float* wa = a.ws_acc + slot * kD + g * 4;
-#pragma unroll
-  for (int b = 0; b < 8; ++b) *reinterpret_cast<float4_t*>(wa + b * 16) = acc[b];
 }
 
-// Log-sum-exp merge of a sequence's split partials (attn_cute.cu:225-238): one wave per
-// (decode sequence, query head), lane -> 2 dims; splits are folded with an online
-// max so the loop carries no second pass and its loads can run ahead.
+// One wavefront per share of the stream-K plan.  A share walks consecutive streams:
+// the first may start mid-stream, the last may end mid-stream, the ones between are
+// whole.  Whole streams are written as bf16 output; a cut stream leaves its partial in
+// slot 2w (the share's first stream) or 2w+1 (its last).
+__global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel(DecArgs a) {
+  const int w = blockIdx.x * kDecWavesPerBlock + (threadIdx.x >> 6);
+  if (w >= a.meta[FQA_META_DEC_WAVES]) return;
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15, g = lane >> 4;
+  const int4 desc = *reinterpret_cast<const int4*>(a.waves + 4 * (long long)w);
+  int di = desc.x, kvh = desc.y, page = desc.z, left = desc.w;
+  for (int seg = 0; left > 0; ++seg) {
+    const int4 sq = *reinterpret_cast<const int4*>(a.seqs + 4 * (long long)di);
+    const int r = sq.x, row = sq.y, L = sq.z;
+    const int pages = (L + kPage - 1) / kPage;
+    const int cnt = min(pages - page, left);
+
+    // Q^T as the B operand: column n = head (kvh*4 + n) for n < 4, zeros elsewhere.
+    bf16x8 qf[4];
+    if (n < kG) {
+      const uint16_t* q = a.qkv + (long long)row * a.stride + (kvh * kG + n) * kD + g * 8;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(q + ks * 32);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qf[ks][i] = (__bf16)0.0f;
+    }
+    DecState st;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) st.acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
+    st.m = -1e30f;
+    st.l = 0.f;
+    stream_pages(a, a.bt + (long long)r * a.max_blocks, kvh, page, page + cnt, L, qf, lane, st);
+    float l_run = st.l;
+    l_run += __shfl_xor(l_run, 16, kWave);
+    l_run += __shfl_xor(l_run, 32, kWave);
+
+    if (n < kG) {
+      if (page == 0 && cnt == pages) {  // whole stream: final output
+        const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
+        uint16_t* o = a.out + (long long)row * (kHq * kD) + (kvh * kG + n) * kD + g * 4;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+          uint2 v = make_uint2(pack_bf16x2(st.acc[b][0] * inv, st.acc[b][1] * inv),
+                               pack_bf16x2(st.acc[b][2] * inv, st.acc[b][3] * inv));
+          *reinterpret_cast<uint2*>(o + b * 16) = v;
+        }
+      } else {
+        const long long slot = (2LL * w + (seg > 0)) * kG + n;
+        if (g == 0) {
+          a.ws_m[slot] = st.m;
+          a.ws_l[slot] = l_run;
+        }
+        float* wa = a.ws_acc + slot * kD + g * 4;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) *reinterpret_cast<float4_t*>(wa + b * 16) = st.acc[b];
+      }
+    }
+    left -= cnt;
+    page = 0;
+    if (++kvh == kHkv) {
+      kvh = 0;
+      ++di;
+    }
+  }
+}
+
+// Log-sum-exp merge of a cut stream's partials (attn_cute.cu:225-238): one wave per
+// (decode sequence, kv head) stream, lane -> (head = lane/16, 8 dims).  The shares that
+// cut stream s = [S0, S1) are w_first..w_last (share w = [w*W/G, (w+1)*W/G)); the
+// stream is the last of w_first's streams (slot 2w+1), or its first (slot 2w) when
+// w_first's share starts exactly at S0, and the first of every later share (slot 2w).
 __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_combine_kernel(DecArgs a) {
   const int wave = blockIdx.x * kDecWavesPerBlock + (threadIdx.x >> 6);
-  const int di = wave / kHq, h = wave % kHq;
+  const int di = wave >> 3, kvh = wave & 7;
   if (di >= a.meta[FQA_META_N_DECODE]) return;
-  const int i0 = a.item_start[di], i1 = a.item_start[di + 1];
-  if (i1 - i0 <= 1) return;
+  const long long G = a.meta[FQA_META_DEC_WAVES];
+  const long long W = 8LL * a.meta[FQA_META_DEC_PAGES];
+  const int4 sq = *reinterpret_cast<const int4*>(a.seqs + 4 * (long long)di);
+  const int pages = (sq.z + kPage - 1) / kPage;
+  const long long S0 = sq.w + (long long)kvh * pages, S1 = S0 + pages;
+  const long long wf = ((S0 + 1) * G - 1) / W, wl = (S1 * G - 1) / W;
+  if (wf == wl) return;  // finished by one wavefront
   const int lane = threadIdx.x & 63;
-  const int kvh = h / kG, hh = h % kG;
-  float gm = -1e30f, gl = 0.f, a0 = 0.f, a1 = 0.f;
-#pragma unroll 4
-  for (int it = i0; it < i1; ++it) {
-    const long long slot = ((long long)it * kHkv + kvh) * kG + hh;
+  const int h = lane >> 4, d0 = (lane & 15) * 8;
+  float gm = -1e30f, gl = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (long long w = wf; w <= wl; ++w) {
+    const long long sl = (w == wf && wf * W / G != S0) ? 2 * w + 1 : 2 * w;
+    const long long slot = sl * kG + h;
     const float m = a.ws_m[slot], l = a.ws_l[slot];
-    const float2 x = *reinterpret_cast<const float2*>(a.ws_acc + slot * kD + 2 * lane);
+    const float4* src = reinterpret_cast<const float4*>(a.ws_acc + slot * kD + d0);
+    const float4 x0 = src[0], x1 = src[1];
     const float mn = fmaxf(gm, m);
     const float co = exp2f(gm - mn), cn = exp2f(m - mn);
     gl = gl * co + l * cn;
-    a0 = a0 * co + x.x * cn;
-    a1 = a1 * co + x.y * cn;
+    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = acc[i] * co + xs[i] * cn;
     gm = mn;
   }
   const float inv = gl > 0.f ? 1.0f / gl : 0.f;
-  const int row = a.cu[a.decode_rids[di]];
-  *reinterpret_cast<uint32_t*>(a.out + (long long)row * (kHq * kD) + h * kD + 2 * lane) =
-      pack_bf16x2(a0 * inv, a1 * inv);
+  uint4 v = make_uint4(pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv),
+                       pack_bf16x2(acc[4] * inv, acc[5] * inv), pack_bf16x2(acc[6] * inv, acc[7] * inv));
+  *reinterpret_cast<uint4*>(a.out + (long long)sq.y * (kHq * kD) + (kvh * kG + h) * kD + d0) = v;
 }
 
 bool dims_ok(const fqa_dims* d) {
@@ -249,36 +273,33 @@ using namespace fqa;
 
 extern "C" {
 
-int64_t fqa_decode_workspace_bytes(const fqa_dims* dims, int32_t dec_item_cap) {
+int64_t fqa_decode_workspace_bytes(const fqa_dims* dims, int32_t dec_wave_cap) {
   (void)dims;
-  if (dec_item_cap < 0) return 0;
-  return (int64_t)dec_item_cap * kHkv * kG * (2 + kD) * (int64_t)sizeof(float);
+  if (dec_wave_cap < 0) return 0;
+  return 2LL * dec_wave_cap * kG * (2 + kD) * (int64_t)sizeof(float);
 }
 
 int fqa_decode(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
                int64_t pool_pages, const int32_t* block_tables, int32_t max_blocks,
-               const int32_t* cu_seqlens, const int32_t* positions, const int32_t* dec_items,
-               const int32_t* dec_item_start, const int32_t* decode_rids, const int32_t* meta,
-               int32_t dec_item_cap, int32_t n_reqs_bound, void* workspace, uint16_t* out,
+               const int32_t* dec_waves, const int32_t* dec_seqs, const int32_t* meta,
+               int32_t dec_wave_cap, int32_t n_reqs_bound, void* workspace, uint16_t* out,
                void* stream) {
   if (!dims) return FQA_EINVAL;
   if (!dims_ok(dims)) return FQA_EUNSUPPORTED;
-  if (dec_item_cap < 0 || n_reqs_bound < 0 || n_reqs_bound > FQA_MAX_REQS || max_blocks < 1 ||
+  if (dec_wave_cap < 0 || n_reqs_bound < 0 || n_reqs_bound > FQA_MAX_REQS || max_blocks < 1 ||
       pool_pages < 1 || !meta)
     return FQA_EINVAL;
-  if (dec_item_cap == 0 || n_reqs_bound == 0) return FQA_OK;
-  if (!qkv || !pool || !block_tables || !cu_seqlens || !positions || !dec_items ||
-      !dec_item_start || !decode_rids || !workspace || !out)
+  if (dec_wave_cap == 0 || n_reqs_bound == 0) return FQA_OK;
+  if (!qkv || !pool || !block_tables || !dec_waves || !dec_seqs || !workspace || !out)
     return FQA_EINVAL;
-  const long long slots = (long long)dec_item_cap * kHkv * kG;
+  const long long slots = 2LL * dec_wave_cap * kG;
   float* ws = static_cast<float*>(workspace);
-  DecArgs a{qkv, pool, pool_pages, block_tables, max_blocks, cu_seqlens, positions, dec_items,
-            dec_item_start, decode_rids, meta, ws, ws + slots, ws + 2 * slots, out,
-            dims->qkv_stride, dims->scale * kLog2e};
-  const int waves1 = dec_item_cap * kHkv;
-  hipLaunchKernelGGL(decode_split_kernel, dim3((waves1 + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
+  DecArgs a{qkv, pool, pool_pages, block_tables, max_blocks, dec_waves, dec_seqs, meta, ws,
+            ws + slots, ws + 2 * slots, out, dims->qkv_stride, dims->scale * kLog2e};
+  hipLaunchKernelGGL(decode_split_kernel,
+                     dim3((dec_wave_cap + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
                      dim3(kDecWavesPerBlock * kWave), 0, (hipStream_t)stream, a);
-  const int waves2 = n_reqs_bound * kHq;
+  const int waves2 = n_reqs_bound * kHkv;
   hipLaunchKernelGGL(decode_combine_kernel,
                      dim3((waves2 + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
                      dim3(kDecWavesPerBlock * kWave), 0, (hipStream_t)stream, a);

@@ -169,7 +169,9 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   __shared__ int s_btoff[FQA_MAX_REQS + 1];
   __shared__ int s_decidx[FQA_MAX_REQS + 1];
   __shared__ int s_preidx[FQA_MAX_REQS + 1];
-  __shared__ int s_decit[FQA_MAX_REQS + 1];
+  __shared__ int s_decit[FQA_MAX_REQS + 1];  // exclusive prefix of decode pages
+  __shared__ int s_dstart[FQA_MAX_REQS + 1];  // by decode index: 8 * page prefix
+  __shared__ int s_dpages[FQA_MAX_REQS];      // by decode index: pages
   __shared__ int s_preit[FQA_MAX_REQS + 1];
   __shared__ Stats s_stats[kPackWaves];
   __shared__ Counts s_counts[kPackWaves];
@@ -219,13 +221,12 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   }
   const int T = rows;
 
-  // decode split size (pages per work item)
-  int S;
-  if (a.c.dec_target_items <= 0) S = dmax > 0 ? dmax : 1;
-  else {
-    int mins = a.c.dec_min_split > 0 ? a.c.dec_min_split : 1;
-    long long s = (dpages + a.c.dec_target_items - 1) / a.c.dec_target_items;
-    S = s > mins ? (int)s : mins;
+  // decode plan: W page runs (8 kv heads x pages) cut into G equal shares
+  const long long W = 8LL * dpages;
+  int G = 0;
+  if (W > 0) {
+    const int minp = a.c.dec_min_pages > 0 ? a.c.dec_min_pages : 1;
+    G = (int)min((long long)a.c.dec_grid_waves, (W + minp - 1) / minp);
   }
 
   // ---- pass 2: exclusive scans over requests ------------------------------------
@@ -239,7 +240,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
         v.v[0] = n;
         v.v[1] = n == 1;
         v.v[2] = n != 1;
-        v.v[3] = n == 1 ? (s_comp[r] / kPage + S) / S : 0;  // ceil(pages / S)
+        v.v[3] = n == 1 ? s_comp[r] / kPage + 1 : 0;  // pages of a decode stream
         v.v[4] = n != 1 ? (n + QT - 1) / QT : 0;
       }
       Counts tot;
@@ -264,13 +265,20 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     __syncthreads();
   }
   const int nd = s_decidx[R], np = s_preidx[R];
-  const int ndi = s_decit[R], npi = s_preit[R];
-  if (ndi > a.c.dec_item_cap || npi > a.c.pre_item_cap) {
+  const int npi = s_preit[R];
+  if (G > a.c.dec_wave_cap || npi > a.c.pre_item_cap || dpages > INT_MAX / 8) {
     if (blockIdx.x == 0 && tid < FQA_META_LEN)
       a.o.meta[tid] = tid == FQA_META_STATUS ? FQA_PACK_ITEMS : (tid == FQA_META_REQS ? R : 0);
     return;
   }
-
+  // decode streams by decode index: start of (di, kv head 0) and pages
+  for (int r = tid; r < R; r += kPackThreads)
+    if (s_n[r] == 1) {
+      s_dstart[s_decidx[r]] = 8 * s_decit[r];
+      s_dpages[s_decidx[r]] = s_comp[r] / kPage + 1;
+    }
+  if (tid == 0) s_dstart[nd] = (int)W;
+  __syncthreads();
   const int gtid = blockIdx.x * kPackThreads + tid;
   const int gsz = gridDim.x * kPackThreads;
 
@@ -292,17 +300,18 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       a.o.block_tables[e] = g < nb ? a.b.bt_pages[s_btoff[r] + g] : -1;
     }
   }
-  // ---- decode items: one thread per decode sequence ------------------------------
-  for (int r = gtid; r < R; r += gsz) {
-    if (s_n[r] != 1) continue;
-    int pages = s_comp[r] / kPage + 1;
-    int it = s_decit[r];
-    for (int s = 0; s * S < pages; ++s, ++it) {
-      int pe = (s + 1) * S < pages ? (s + 1) * S : pages;
-      int4 v = make_int4(r, s, s * S, pe);
-      *reinterpret_cast<int4*>(a.o.dec_items + 4 * (long long)it) = v;
-    }
+  // ---- decode wave shares: where share w = [w*W/G, (w+1)*W/G) starts ----------------
+  for (int w = gtid; w < G; w += gsz) {
+    const long long g0 = (long long)w * W / G, g1 = (long long)(w + 1) * W / G;
+    const int di = upper_index(s_dstart, nd, (int)g0);
+    const int rem = (int)g0 - s_dstart[di], pg = s_dpages[di];
+    *reinterpret_cast<int4*>(a.o.dec_waves + 4 * (long long)w) =
+        make_int4(di, rem / pg, rem % pg, (int)(g1 - g0));
   }
+  for (int r = gtid; r < R; r += gsz)
+    if (s_n[r] == 1)
+      *reinterpret_cast<int4*>(a.o.dec_seqs + 4 * (long long)s_decidx[r]) =
+          make_int4(r, s_qstart[r], s_comp[r] + 1, 8 * s_decit[r]);
   // ---- prefill items, sorted by key count descending (stable) --------------------
   // Tile t of prefill request r covers rows [t*QT, min((t+1)*QT, n)) and needs
   // c + min((t+1)*QT, n) keys, so per request the number of tiles with more keys than X
@@ -338,16 +347,11 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       // decode / prefill lists: slot i holds the i-th request of the class
       if (n == 1) a.o.decode_rids[s_decidx[r]] = r;
       else a.o.prefill_rids[s_preidx[r]] = r;
-      if (n == 1) a.o.dec_item_start[s_decidx[r]] = s_decit[r];
     }
   }
   for (int i = tid; i < R; i += kPackThreads) {
     if (i >= nd) a.o.decode_rids[i] = -1;
     if (i >= np) a.o.prefill_rids[i] = -1;
-  }
-  for (int i = tid; i <= R; i += kPackThreads) {
-    if (i == nd) a.o.dec_item_start[i] = ndi;
-    else if (i > nd) a.o.dec_item_start[i] = -1;
   }
   // page-id range check over the concatenated tables: 16-byte loads, 4 in flight per
   // thread (the scalar head and tail are the at most 3 ids on either side of alignment)
@@ -381,9 +385,9 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       case FQA_META_N_DECODE: v = nd; break;
       case FQA_META_N_PREFILL: v = np; break;
       case FQA_META_MAX_QLEN: v = qmax; break;
-      case FQA_META_DEC_ITEMS: v = ndi; break;
+      case FQA_META_DEC_WAVES: v = G; break;
       case FQA_META_PRE_ITEMS: v = npi; break;
-      case FQA_META_SPLIT_PAGES: v = S; break;
+      case FQA_META_DEC_WAVE_PAGES: v = G ? (int)((W + G - 1) / G) : 0; break;
       case FQA_META_STATUS: v = bad ? FQA_PACK_PAGE_RANGE : FQA_PACK_OK; break;
       case FQA_META_REQS: v = R; break;
       case FQA_META_DEC_PAGES: v = (int)dpages; break;
@@ -565,17 +569,17 @@ int fqa_pack(const fqa_batch* batch, const fqa_pack_cfg* cfg, const fqa_pack_out
   const int R = batch->n_reqs;
   if (R < 0 || R > FQA_MAX_REQS) return FQA_EINVAL;
   if (cfg->max_rows < 0 || cfg->max_blocks < 1 || cfg->pool_pages < 1 ||
-      cfg->dec_item_cap < 0 || cfg->pre_item_cap < 0)
+      cfg->dec_wave_cap < 0 || cfg->pre_item_cap < 0 || cfg->dec_grid_waves < 1)
     return FQA_EINVAL;
   if (cfg->pre_tile_q != 32 && cfg->pre_tile_q != 64 && cfg->pre_tile_q != 128)
     return FQA_EINVAL;
-  if (!batch->bt_off || !out->meta || !out->cu_seqlens || !out->dec_item_start) return FQA_EINVAL;
+  if (!batch->bt_off || !out->meta || !out->cu_seqlens || !out->dec_seqs) return FQA_EINVAL;
   if (R > 0 && (!batch->computed || !batch->n_new || !batch->bt_pages || !out->qlen ||
                 !out->block_tables || !out->decode_rids || !out->prefill_rids))
     return FQA_EINVAL;
   if (cfg->max_rows > 0 && (!out->positions || !out->row_req || !out->slot_mapping))
     return FQA_EINVAL;
-  if ((cfg->dec_item_cap > 0 && !out->dec_items) || (cfg->pre_item_cap > 0 && !out->pre_items))
+  if ((cfg->dec_wave_cap > 0 && !out->dec_waves) || (cfg->pre_item_cap > 0 && !out->pre_items))
     return FQA_EINVAL;
   long long work = (long long)R * cfg->max_blocks;
   if (cfg->max_rows > work) work = cfg->max_rows;
@@ -587,9 +591,17 @@ int fqa_pack(const fqa_batch* batch, const fqa_pack_cfg* cfg, const fqa_pack_out
   return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
 }
 
-int32_t fqa_dec_item_bound(int32_t n_reqs, int32_t dec_target_items) {
-  if (n_reqs < 0) return 0;
-  return dec_target_items > 0 ? dec_target_items + n_reqs : n_reqs;
+int32_t fqa_dec_wave_bound(int32_t n_reqs, int32_t dec_grid_waves) {
+  (void)n_reqs;
+  return dec_grid_waves > 0 ? dec_grid_waves : 0;
+}
+
+int32_t fqa_dec_default_waves(int32_t device) {
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      cus <= 0)
+    return 0;
+  return cus * 8;  // 2 decode wavefronts per SIMD (the kernel's register budget), 4 SIMDs
 }
 
 int32_t fqa_pre_item_bound(int32_t n_reqs, int32_t max_rows, int32_t pre_tile_q) {

@@ -62,7 +62,7 @@ class AttnStep:
     """Per-step context + per-layer launches of the attention path (one GPU, one stream)."""
 
     def __init__(self, *, max_rows: int, max_reqs: int, max_ctx: int, pool_pages: int,
-                 device="cuda", dec_target_items: int = 1024, dec_min_split: int = 8,
+                 device="cuda", dec_grid_waves: int | None = None, dec_min_pages: int = 8,
                  pre_tile_q: int = 64, max_bt_pages: int | None = None):
         self.lib = _lib.load()
         if max_reqs > _lib.FQA_MAX_REQS:
@@ -73,10 +73,13 @@ class AttnStep:
         self.pool_pages = pool_pages
         self.max_blocks = -(-max_ctx // PAGE)
         self.pre_tile_q = pre_tile_q
-        self.dec_cap = int(self.lib.fqa_dec_item_bound(max_reqs, dec_target_items))
+        if dec_grid_waves is None:  # fill the device: CUs x resident decode waves per CU
+            dec_grid_waves = int(self.lib.fqa_dec_default_waves(self.device.index or 0)) or 2048
+        self.dec_grid_waves = dec_grid_waves
+        self.dec_wave_cap = int(self.lib.fqa_dec_wave_bound(max_reqs, dec_grid_waves))
         self.pre_cap = int(self.lib.fqa_pre_item_bound(max_reqs, max_rows, pre_tile_q))
-        self.cfg = FqaPackCfg(max_rows, self.max_blocks, pool_pages, dec_target_items,
-                              dec_min_split, self.dec_cap, pre_tile_q, self.pre_cap)
+        self.cfg = FqaPackCfg(max_rows, self.max_blocks, pool_pages, dec_grid_waves,
+                              dec_min_pages, self.dec_wave_cap, pre_tile_q, self.pre_cap)
         i32 = dict(dtype=torch.int32, device=self.device)
         R = max_reqs
         self.cu_seqlens = torch.zeros(R + 1, **i32)
@@ -87,11 +90,11 @@ class AttnStep:
         self.block_tables = torch.full((R, self.max_blocks), -1, **i32)
         self.decode_rids = torch.zeros(R, **i32)
         self.prefill_rids = torch.zeros(R, **i32)
-        self.dec_item_start = torch.zeros(R + 1, **i32)
-        self.dec_items = torch.zeros((max(self.dec_cap, 1), 4), **i32)
+        self.dec_seqs = torch.zeros((max(R, 1), 4), **i32)
+        self.dec_waves = torch.zeros((max(self.dec_wave_cap, 1), 4), **i32)
         self.pre_items = torch.zeros((max(self.pre_cap, 1), 4), **i32)
         self.meta = torch.zeros(_lib.META_LEN, **i32)
-        ws = int(self.lib.fqa_decode_workspace_bytes(C.byref(self.dims), self.dec_cap))
+        ws = int(self.lib.fqa_decode_workspace_bytes(C.byref(self.dims), self.dec_wave_cap))
         self.workspace = torch.empty(max(ws, 16), dtype=torch.uint8, device=self.device)
         cos, sin = rope_tables(max_ctx)
         self.cos = torch.from_numpy(cos).to(self.device)
@@ -99,7 +102,7 @@ class AttnStep:
         self.out_struct = FqaPackOut(*[
             _ptr(t) for t in (self.cu_seqlens, self.qlen, self.positions, self.row_req,
                               self.slot_mapping, self.block_tables, self.decode_rids,
-                              self.prefill_rids, self.dec_item_start, self.dec_items,
+                              self.prefill_rids, self.dec_seqs, self.dec_waves,
                               self.pre_items, self.meta)])
         # device-side selection buffers (schedule_and_prepare)
         self.max_bt_pages = max_bt_pages if max_bt_pages is not None else R * self.max_blocks
@@ -161,9 +164,8 @@ class AttnStep:
         """LaunchAttnDecodeCute: split-K decode + combine."""
         check(self.lib.fqa_decode(
             C.byref(self.dims), _ptr(qkv), _ptr(pool_layer), self.pool_pages,
-            _ptr(self.block_tables), self.max_blocks, _ptr(self.cu_seqlens),
-            _ptr(self.positions), _ptr(self.dec_items), _ptr(self.dec_item_start),
-            _ptr(self.decode_rids), _ptr(self.meta), self.dec_cap, self.n_reqs_bound,
+            _ptr(self.block_tables), self.max_blocks, _ptr(self.dec_waves),
+            _ptr(self.dec_seqs), _ptr(self.meta), self.dec_wave_cap, self.n_reqs_bound,
             _ptr(self.workspace), _ptr(out), self.stream), "fqa_decode")
 
     def attn_prefill(self, qkv, pool_layer, out):

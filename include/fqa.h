@@ -59,9 +59,9 @@ enum {
   FQA_META_N_DECODE = 1,     /* requests with qlen == 1                        */
   FQA_META_N_PREFILL = 2,    /* requests with qlen != 1                        */
   FQA_META_MAX_QLEN = 3,     /* max(1, max prefill qlen) (model_runtime.cu:82) */
-  FQA_META_DEC_ITEMS = 4,    /* decode work items (sequence, page range)      */
+  FQA_META_DEC_WAVES = 4,    /* decode wavefronts with work this step         */
   FQA_META_PRE_ITEMS = 5,    /* prefill work items (request, query tile)      */
-  FQA_META_SPLIT_PAGES = 6,  /* pages per decode split chosen this step       */
+  FQA_META_DEC_WAVE_PAGES = 6, /* max page runs one decode wavefront streams */
   FQA_META_STATUS = 7,       /* 0 or an FQA_PACK_* code                       */
   FQA_META_REQS = 8,         /* R                                             */
   FQA_META_DEC_PAGES = 9,    /* sum over decode sequences of their pages      */
@@ -78,7 +78,7 @@ enum {
   FQA_PACK_ROWS = 3,        /* sum of n over requests > max_rows                */
   FQA_PACK_PAGE_RANGE = 4,  /* a page id outside [0, pool_pages)                */
   FQA_PACK_NEGATIVE = 5,    /* negative computed or n                           */
-  FQA_PACK_ITEMS = 6        /* work items would exceed the plan capacity        */
+  FQA_PACK_ITEMS = 6        /* prefill items or decode waves exceed capacity    */
 };
 
 typedef struct fqa_dims {
@@ -105,7 +105,18 @@ typedef struct fqa_batch {
   int32_t n_reqs;
 } fqa_batch;
 
-/* Everything the pack writes (device arrays, caller-allocated at capacity). */
+/* Everything the pack writes (device arrays, caller-allocated at capacity).
+ *
+ * Decode plan (stream-K): the decode requests' (sequence, kv head) page streams are laid
+ * end to end, stream (di, kvh) covering P[di]*8 + kvh*pages[di] .. + pages[di], where
+ * pages = ceil(n_keys/16) and P is the exclusive prefix of pages over decode indices.
+ * The W = 8*sum(pages) page runs are cut into G = min(dec_grid_waves,
+ * ceil(W/dec_min_pages)) equal contiguous shares, share w = [floor(w*W/G),
+ * floor((w+1)*W/G)), one per decode wavefront; dec_waves[w] = {di, kvh, page, n_runs}
+ * is where share w starts and how long it is.  dec_seqs[di] = {r, row = qstart[r],
+ * n_keys = computed[r]+1, 8*P[di]}.  Prefill plan: one item per pre_tile_q query rows
+ * of each prefill request, pre_items[i] = {r, q0, q1, n_keys = computed + q1}, ordered
+ * by n_keys descending (stable). */
 typedef struct fqa_pack_out {
   int32_t* cu_seqlens;     /* [R+1]  qstart = cu_seqlens[r]                   */
   int32_t* qlen;           /* [R]                                             */
@@ -115,8 +126,8 @@ typedef struct fqa_pack_out {
   int32_t* block_tables;   /* [R * max_blocks], tail padded with -1           */
   int32_t* decode_rids;    /* [R] qlen==1 requests, increasing; pad -1        */
   int32_t* prefill_rids;   /* [R] the others, increasing; pad -1              */
-  int32_t* dec_item_start; /* [R+1] first item of decode index di; pad -1     */
-  int32_t* dec_items;      /* [dec_cap][4] {r, split, page_begin, page_end}   */
+  int32_t* dec_seqs;       /* [R][4] per decode index: {r, row, n_keys, 8*P}  */
+  int32_t* dec_waves;      /* [dec_wave_cap][4] {di, kvh, page, n_runs}      */
   int32_t* pre_items;      /* [pre_cap][4] {r, q0, q1, n_keys}                */
   int32_t* meta;           /* [FQA_META_LEN]                                  */
 } fqa_pack_out;
@@ -125,9 +136,9 @@ typedef struct fqa_pack_cfg {
   int32_t max_rows;          /* capacity of the per-row arrays             */
   int32_t max_blocks;        /* block table stride                         */
   int64_t pool_pages;        /* pages in the per-layer pool                */
-  int32_t dec_target_items;  /* aim for this many decode splits (0: one per sequence) */
-  int32_t dec_min_split;     /* never split finer than this many pages     */
-  int32_t dec_item_cap;      /* capacity of dec_items                      */
+  int32_t dec_grid_waves;    /* decode wavefronts to spread the work over (>= 1) */
+  int32_t dec_min_pages;     /* give no wavefront fewer page runs than this   */
+  int32_t dec_wave_cap;      /* capacity of dec_waves (>= dec_grid_waves)  */
   int32_t pre_tile_q;        /* query rows per prefill item: 32, 64 or 128 */
   int32_t pre_item_cap;      /* capacity of pre_items                      */
 } fqa_pack_cfg;
@@ -144,11 +155,14 @@ int fqa_rope_tables(int32_t max_pos, int32_t head_dim, float theta, float* cos_t
 int64_t fqa_pool_bytes(const fqa_dims* dims, int64_t pages);
 
 /* Upper bounds for plan capacities and launch grids, from host-known sizes. */
-int32_t fqa_dec_item_bound(int32_t n_reqs, int32_t dec_target_items);
+int32_t fqa_dec_wave_bound(int32_t n_reqs, int32_t dec_grid_waves);
+
+/* A decode grid that fills the device: CUs x resident decode wavefronts per CU. */
+int32_t fqa_dec_default_waves(int32_t device);
 int32_t fqa_pre_item_bound(int32_t n_reqs, int32_t max_rows, int32_t pre_tile_q);
 
-/* Bytes of the decode workspace fqa_decode needs for `dec_item_cap` items. */
-int64_t fqa_decode_workspace_bytes(const fqa_dims* dims, int32_t dec_item_cap);
+/* Bytes of the decode workspace fqa_decode needs for `dec_wave_cap` wavefronts. */
+int64_t fqa_decode_workspace_bytes(const fqa_dims* dims, int32_t dec_wave_cap);
 
 /* --- device entry points (stream-ordered launches) -------------------------------- */
 
@@ -192,17 +206,19 @@ int fqa_qknorm_rope_append(const fqa_dims* dims, uint16_t* qkv, const float* q_n
                            const int32_t* meta, int32_t rows_bound, uint16_t* pool,
                            int64_t pool_pages, int32_t write_k_inplace, void* stream);
 
-/* GQA-shared split-K flash decoding over the pack's decode plan: one wavefront per
- * (work item, kv head) streams its page range once for all 4 query heads; sequences
- * with more than one split are merged by a log-sum-exp combine.  Output rows
- * out[cu_seqlens[r]] ([n_q_heads][head_dim] bf16, row stride n_q_heads*head_dim).
- * `workspace` must hold fqa_decode_workspace_bytes(dims, dec_item_cap) bytes. */
+/* GQA-shared split-K flash decoding over the pack's stream-K decode plan: wavefront w
+ * streams its share of page runs; each (page, kv head) run is read once for all 4 query
+ * heads of the kv head.  A stream that lies inside one share is finished by that
+ * wavefront; a stream cut by share boundaries leaves fp32 partials (m, l, acc) that a
+ * log-sum-exp combine merges.  Output rows out[row] ([n_q_heads][head_dim] bf16, row
+ * stride n_q_heads*head_dim).  `workspace` must hold
+ * fqa_decode_workspace_bytes(dims, dec_wave_cap) bytes; n_reqs_bound bounds the
+ * decode requests (combine grid). */
 int fqa_decode(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
                int64_t pool_pages, const int32_t* block_tables, int32_t max_blocks,
-               const int32_t* cu_seqlens, const int32_t* positions,
-               const int32_t* dec_items, const int32_t* dec_item_start,
-               const int32_t* decode_rids, const int32_t* meta, int32_t dec_item_cap,
-               int32_t n_reqs_bound, void* workspace, uint16_t* out, void* stream);
+               const int32_t* dec_waves, const int32_t* dec_seqs, const int32_t* meta,
+               int32_t dec_wave_cap, int32_t n_reqs_bound, void* workspace, uint16_t* out,
+               void* stream);
 
 /* Varlen causal FlashAttention-2 prefill on bf16 MFMA over the pack's prefill plan:
  * one workgroup per (query tile, kv head) computes all 4 query heads of the kv head

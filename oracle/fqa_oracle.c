@@ -114,11 +114,11 @@ static int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
  * StoreKvKernel (kv_store.cu:56-60) and this library's decode/prefill work plans. */
 int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t* bt_off,
              const int32_t* bt_pages, int max_rows, int max_blocks, int64_t pool_pages,
-             int dec_target_items, int dec_min_split, int dec_item_cap, int pre_tile_q,
+             int dec_grid_waves, int dec_min_pages, int dec_wave_cap, int pre_tile_q,
              int pre_item_cap, int32_t* cu_seqlens, int32_t* qlen, int32_t* positions,
              int32_t* row_req, int32_t* slot_mapping, int32_t* block_tables,
-             int32_t* decode_rids, int32_t* prefill_rids, int32_t* dec_item_start,
-             int32_t* dec_items, int32_t* pre_items, int32_t* meta) {
+             int32_t* decode_rids, int32_t* prefill_rids, int32_t* dec_seqs,
+             int32_t* dec_waves, int32_t* pre_items, int32_t* meta) {
   for (int i = 0; i < 16; ++i) meta[i] = 0;
   meta[8] = R;
   /* structural checks: the smallest violated code wins */
@@ -179,48 +179,54 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
     }
   }
 
-  /* decode plan: split size S pages, ceil(pages / S) items per sequence */
+  /* decode plan (stream-K): the (decode sequence, kv head) page streams end to end,
+   * W = 8 * total pages runs cut into G equal shares [w*W/G, (w+1)*W/G) */
   int64_t total = 0;
-  int maxpages = 0;
-  for (int di = 0; di < nd; ++di) {
-    int pages = computed[decode_rids[di]] / PAGE + 1;
-    total += pages;
-    if (pages > maxpages) maxpages = pages;
+  for (int di = 0; di < nd; ++di) total += computed[decode_rids[di]] / PAGE + 1;
+  int64_t W = 8 * total;
+  int minp = dec_min_pages > 0 ? dec_min_pages : 1;
+  int G = 0;
+  if (W > 0) {
+    int64_t gmax = (W + minp - 1) / minp;
+    G = (int)(dec_grid_waves < gmax ? dec_grid_waves : gmax);
   }
-  int minsplit = dec_min_split > 0 ? dec_min_split : 1;
-  int S;
-  if (dec_target_items <= 0) S = maxpages > 0 ? maxpages : 1;
-  else {
-    int64_t s = (total + dec_target_items - 1) / dec_target_items;
-    S = s > minsplit ? (int)s : minsplit;
-  }
-  int nitems = 0;
-  for (int di = 0; di < nd; ++di) {
-    dec_item_start[di] = nitems;
-    nitems += ceil_div(computed[decode_rids[di]] / PAGE + 1, S);
-  }
-  dec_item_start[nd] = nitems;
-  for (int i = nd + 1; i <= R; ++i) dec_item_start[i] = -1;
-
   /* prefill plan: query tiles of pre_tile_q rows, ordered by key count descending
    * (longest first), ties by (prefill index, tile) ascending */
   int npi = 0;
   for (int pi = 0; pi < np; ++pi) npi += ceil_div(n_new[prefill_rids[pi]], pre_tile_q);
 
-  if (nitems > dec_item_cap || npi > pre_item_cap) {
+  if (G > dec_wave_cap || npi > pre_item_cap || total > 0x7fffffff / 8) {
     for (int i = 0; i < 16; ++i) meta[i] = 0;
     meta[8] = R;
     meta[7] = 6;
     return 6;
   }
-  for (int di = 0; di < nd; ++di) {
-    int r = decode_rids[di], pages = computed[r] / PAGE + 1;
-    for (int s = 0, it = dec_item_start[di]; s * S < pages; ++s, ++it) {
-      int pe = (s + 1) * S < pages ? (s + 1) * S : pages;
-      dec_items[4 * it + 0] = r;
-      dec_items[4 * it + 1] = s;
-      dec_items[4 * it + 2] = s * S;
-      dec_items[4 * it + 3] = pe;
+  {
+    int64_t P = 0; /* page prefix over decode indices */
+    for (int di = 0; di < nd; ++di) {
+      int r = decode_rids[di], pages = computed[r] / PAGE + 1;
+      dec_seqs[4 * di + 0] = r;
+      dec_seqs[4 * di + 1] = cu_seqlens[r];
+      dec_seqs[4 * di + 2] = computed[r] + 1;
+      dec_seqs[4 * di + 3] = (int32_t)(8 * P);
+      P += pages;
+    }
+    /* share w starts at global run g0: find its stream by walking the sequences */
+    int di = 0;
+    int64_t start = 0; /* 8 * P[di] */
+    for (int w = 0; w < G; ++w) {
+      int64_t g0 = (int64_t)w * W / G, g1 = (int64_t)(w + 1) * W / G;
+      int pages = computed[decode_rids[di]] / PAGE + 1;
+      while (g0 >= start + 8 * (int64_t)pages) {
+        start += 8 * (int64_t)pages;
+        ++di;
+        pages = computed[decode_rids[di]] / PAGE + 1;
+      }
+      int64_t rem = g0 - start;
+      dec_waves[4 * w + 0] = di;
+      dec_waves[4 * w + 1] = (int32_t)(rem / pages);
+      dec_waves[4 * w + 2] = (int32_t)(rem % pages);
+      dec_waves[4 * w + 3] = (int32_t)(g1 - g0);
     }
   }
   {
@@ -251,9 +257,9 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
   meta[1] = nd;
   meta[2] = np;
   meta[3] = maxq;
-  meta[4] = nitems;
+  meta[4] = G;
   meta[5] = npi;
-  meta[6] = S;
+  meta[6] = G ? (int32_t)((W + G - 1) / G) : 0;
   meta[7] = bad_page ? 4 : 0;
   meta[9] = (int32_t)total;
   return meta[7];

@@ -69,7 +69,7 @@ def schedule(num_tokens, computed, token_budget: int, prefill_chunk: int):
 
 
 def pack(computed, n_new, bt_off, bt_pages, *, max_rows, max_blocks, pool_pages,
-         dec_target_items, dec_min_split, dec_item_cap, pre_tile_q, pre_item_cap) -> dict:
+         dec_grid_waves, dec_min_pages, dec_wave_cap, pre_tile_q, pre_item_cap) -> dict:
     computed, n_new, bt_off = i32(computed), i32(n_new), i32(bt_off)
     bt_pages = i32(bt_pages) if len(bt_pages) else np.zeros(1, np.int32)
     R = computed.shape[0]
@@ -80,16 +80,16 @@ def pack(computed, n_new, bt_off, bt_pages, *, max_rows, max_blocks, pool_pages,
         slot_mapping=np.zeros(max(max_rows, 1), np.int32),
         block_tables=np.zeros(max(R * max_blocks, 1), np.int32),
         decode_rids=np.zeros(max(R, 1), np.int32), prefill_rids=np.zeros(max(R, 1), np.int32),
-        dec_item_start=np.zeros(R + 1, np.int32),
-        dec_items=np.zeros((max(dec_item_cap, 1), 4), np.int32),
+        dec_seqs=np.zeros((max(R, 1), 4), np.int32),
+        dec_waves=np.zeros((max(dec_wave_cap, 1), 4), np.int32),
         pre_items=np.zeros((max(pre_item_cap, 1), 4), np.int32),
         meta=np.zeros(16, np.int32))
     status = load().fqo_pack(
         R, _p(computed), _p(n_new), _p(bt_off), _p(bt_pages), max_rows, max_blocks,
-        C.c_int64(pool_pages), dec_target_items, dec_min_split, dec_item_cap, pre_tile_q,
+        C.c_int64(pool_pages), dec_grid_waves, dec_min_pages, dec_wave_cap, pre_tile_q,
         pre_item_cap, *[_p(out[k]) for k in (
             "cu_seqlens", "qlen", "positions", "row_req", "slot_mapping", "block_tables",
-            "decode_rids", "prefill_rids", "dec_item_start", "dec_items", "pre_items", "meta")])
+            "decode_rids", "prefill_rids", "dec_seqs", "dec_waves", "pre_items", "meta")])
     out["status"] = status
     return out
 

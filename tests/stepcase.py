@@ -13,17 +13,16 @@ ATT_MAX_ABS = 2e-2
 ATT_MEAN_ABS = 2e-3
 
 
-def pack_kwargs(cfg: synth.StepConfig, max_rows=None, dec_target_items=1024, dec_min_split=8,
+def pack_kwargs(cfg: synth.StepConfig, max_rows=None, dec_grid_waves=2048, dec_min_pages=8,
                 pre_tile_q=64, max_reqs=None):
     from oracle import oracle as orc  # noqa: F401  (tests only)
 
     R = cfg.n_reqs if max_reqs is None else max_reqs
     max_rows = max(cfg.rows, 1) if max_rows is None else max_rows
-    dec_cap = dec_target_items + R if dec_target_items > 0 else R
     pre_cap = max_rows // pre_tile_q + R
     return dict(max_rows=max_rows, max_blocks=cfg.max_blocks, pool_pages=cfg.pool_pages,
-                dec_target_items=dec_target_items, dec_min_split=dec_min_split,
-                dec_item_cap=dec_cap, pre_tile_q=pre_tile_q, pre_item_cap=pre_cap)
+                dec_grid_waves=dec_grid_waves, dec_min_pages=dec_min_pages,
+                dec_wave_cap=dec_grid_waves, pre_tile_q=pre_tile_q, pre_item_cap=pre_cap)
 
 
 def pool_elems(pages: int) -> int:

@@ -39,7 +39,7 @@ def rand_batch(rng, R, max_ctx=4096, pool_pages=4096, share=False):
 
 
 def run_both(gpu, comp, nnew, tabs, *, max_rows=None, max_ctx=4096, pool_pages=4096,
-             dec_target_items=64, dec_min_split=2, pre_tile_q=64, max_reqs=None):
+             dec_grid_waves=64, dec_min_pages=2, pre_tile_q=64, max_reqs=None):
     import torch
 
     from flashqwen_amd.step import AttnStep
@@ -50,11 +50,11 @@ def run_both(gpu, comp, nnew, tabs, *, max_rows=None, max_ctx=4096, pool_pages=4
     max_reqs = max(R, 1) if max_reqs is None else max_reqs
     max_rows = max(int(np.sum(nnew)) if R else 0, 1) if max_rows is None else max_rows
     step = AttnStep(max_rows=max_rows, max_reqs=max_reqs, max_ctx=max_ctx, pool_pages=pool_pages,
-                    device=gpu, dec_target_items=dec_target_items, dec_min_split=dec_min_split,
+                    device=gpu, dec_grid_waves=dec_grid_waves, dec_min_pages=dec_min_pages,
                     pre_tile_q=pre_tile_q)
     kw = dict(max_rows=max_rows, max_blocks=cfg.max_blocks, pool_pages=pool_pages,
-              dec_target_items=dec_target_items, dec_min_split=dec_min_split,
-              dec_item_cap=step.dec_cap, pre_tile_q=pre_tile_q, pre_item_cap=step.pre_cap)
+              dec_grid_waves=dec_grid_waves, dec_min_pages=dec_min_pages,
+              dec_wave_cap=step.dec_wave_cap, pre_tile_q=pre_tile_q, pre_item_cap=step.pre_cap)
     ref = orc.pack(cfg.computed, cfg.n_new, cfg.bt_off, cfg.bt_pages, **kw)
     t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(gpu)  # noqa: E731
     pages = cfg.bt_pages if len(cfg.bt_pages) else np.zeros(1, np.int32)
@@ -71,8 +71,9 @@ def assert_pack_equal(step, ref, R, kw):
     if meta[7] not in (0, 4):
         return
     T = int(meta[0])
-    for k in ("cu_seqlens", "dec_item_start"):
-        assert np.array_equal(getattr(step, k).cpu().numpy()[: R + 1], ref[k][: R + 1]), k
+    assert np.array_equal(step.cu_seqlens.cpu().numpy()[: R + 1], ref["cu_seqlens"][: R + 1])
+    nd_seq = int(meta[1])
+    assert np.array_equal(step.dec_seqs.cpu().numpy()[:nd_seq], ref["dec_seqs"][:nd_seq])
     for k in ("qlen", "decode_rids", "prefill_rids"):
         assert np.array_equal(getattr(step, k).cpu().numpy()[:R], ref[k][:R]), k
     for k in ("positions", "row_req", "slot_mapping"):
@@ -81,7 +82,7 @@ def assert_pack_equal(step, ref, R, kw):
     assert np.array_equal(step.block_tables.cpu().numpy().reshape(-1)[: R * mb],
                           ref["block_tables"][: R * mb])
     nd, npi = int(meta[4]), int(meta[5])
-    assert np.array_equal(step.dec_items.cpu().numpy()[:nd], ref["dec_items"][:nd])
+    assert np.array_equal(step.dec_waves.cpu().numpy()[:nd], ref["dec_waves"][:nd])
     assert np.array_equal(step.pre_items.cpu().numpy()[:npi], ref["pre_items"][:npi])
 
 
@@ -92,10 +93,10 @@ def test_pack_random(gpu, seed):
     R = int(rng.choice([1, 3, 17, 64, 250, 700]))
     comp, nnew, tabs = rand_batch(rng, R, share=seed % 2 == 0)
     tile = int(rng.choice([32, 64, 128]))
-    target = int(rng.choice([0, 1, 50, 1024]))
+    target = int(rng.choice([1, 7, 50, 2048]))
     print(f"[test_pack_random] seed={seed} R={R} tile={tile} target={target}", flush=True)
-    step, ref, R, kw = run_both(gpu, comp, nnew, tabs, pre_tile_q=tile, dec_target_items=target,
-                                dec_min_split=int(rng.choice([0, 1, 8])))
+    step, ref, R, kw = run_both(gpu, comp, nnew, tabs, pre_tile_q=tile, dec_grid_waves=target,
+                                dec_min_pages=int(rng.choice([0, 1, 8])))
     assert ref["status"] == 0
     assert_pack_equal(step, ref, R, kw)
 
@@ -149,15 +150,15 @@ def test_pack_status(gpu, case):
         comp = [4000] * 2
         nnew = [1, 1]
         tabs = [np.arange(251, dtype=np.int32)] * 2
-        kwargs.update(dec_target_items=1, dec_min_split=1)
+        kwargs.update(dec_grid_waves=8, dec_min_pages=1)
     step, ref, R, kw = run_both(gpu, comp, nnew, tabs, **kwargs)
     code = {"short": 1, "wide": 2, "rows": 3, "negative": 5, "page": 4, "items": 6}[case]
     if case == "items":
         # capacity is sized by the bound; force overflow through a smaller cap
         from flashqwen_amd import _lib
 
-        step.cfg.dec_item_cap = 1
-        kw["dec_item_cap"] = 1
+        step.cfg.dec_wave_cap = 1
+        kw["dec_wave_cap"] = 1
         from oracle import oracle as orc
 
         cfg = synth._assemble("x", comp, nnew, tabs, 4096, 4096)
@@ -204,7 +205,7 @@ def test_schedule_gather_pack(gpu, seed):
     T = int(sel_n.sum())
     max_rows = max(T, 1)
     step = AttnStep(max_rows=max_rows, max_reqs=len(comp), max_ctx=8192, pool_pages=pool,
-                    device=gpu, dec_target_items=128, dec_min_split=4)
+                    device=gpu, dec_grid_waves=128, dec_min_pages=4)
     t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(gpu)  # noqa: E731
     step.schedule_and_prepare(t(ntok), t(comp), t(run.bt_off), t(run.bt_pages), budget, chunk)
     torch.cuda.synchronize()
@@ -216,7 +217,7 @@ def test_schedule_gather_pack(gpu, seed):
     assert np.array_equal(step.b_bt_off.cpu().numpy()[: Rb + 1], sub.bt_off)
     assert np.array_equal(step.b_bt_pages.cpu().numpy()[: len(sub.bt_pages)], sub.bt_pages)
     kw = dict(max_rows=max_rows, max_blocks=sub.max_blocks, pool_pages=pool,
-              dec_target_items=128, dec_min_split=4, dec_item_cap=step.dec_cap, pre_tile_q=64,
+              dec_grid_waves=128, dec_min_pages=4, dec_wave_cap=step.dec_wave_cap, pre_tile_q=64,
               pre_item_cap=step.pre_cap)
     ref = orc.pack(sub.computed, sub.n_new, sub.bt_off, sub.bt_pages, **kw)
     ref["meta"][8] = Rb

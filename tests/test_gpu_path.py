@@ -9,7 +9,7 @@ from flashqwen_amd import synth
 from flashqwen_amd.synth import HEAD_DIM, N_Q, PAGE, QKV_STRIDE
 from tests import stepcase as sc
 
-PACK_KEYS_R = ("cu_seqlens", "qlen", "decode_rids", "prefill_rids", "dec_item_start")
+PACK_KEYS_R = ("cu_seqlens", "qlen", "decode_rids", "prefill_rids")
 
 
 def _t(x, dev):
@@ -48,7 +48,7 @@ def gpu_chain(cfg, qkv_host, pool, wq, wk, dev, kw, schedule=False):
 
     step = AttnStep(max_rows=kw["max_rows"], max_reqs=cfg.n_reqs, max_ctx=cfg.max_ctx,
                     pool_pages=cfg.pool_pages, device=dev,
-                    dec_target_items=kw["dec_target_items"], dec_min_split=kw["dec_min_split"],
+                    dec_grid_waves=kw["dec_grid_waves"], dec_min_pages=kw["dec_min_pages"],
                     pre_tile_q=kw["pre_tile_q"])
     qkv = _t(qkv_host.view(np.int16), dev).view(torch.bfloat16)
     out = torch.zeros((kw["max_rows"], N_Q * HEAD_DIM), dtype=torch.bfloat16, device=dev)
@@ -69,14 +69,15 @@ def check_pack(step, ref_pk, R, T, kw):
     assert np.array_equal(meta, ref_pk["meta"]), (meta, ref_pk["meta"])
     for k in PACK_KEYS_R:
         got = getattr(step, k).cpu().numpy()
-        n = R + 1 if k in ("cu_seqlens", "dec_item_start") else R
+        n = R + 1 if k == "cu_seqlens" else R
         assert np.array_equal(got[:n], ref_pk[k][:n]), k
     for k in ("positions", "row_req", "slot_mapping"):
         assert np.array_equal(getattr(step, k).cpu().numpy()[:T], ref_pk[k][:T]), k
     bt = step.block_tables.cpu().numpy().reshape(-1)[: R * kw["max_blocks"]]
     assert np.array_equal(bt, ref_pk["block_tables"][: R * kw["max_blocks"]])
+    assert np.array_equal(step.dec_seqs.cpu().numpy()[: meta[1]], ref_pk["dec_seqs"][: meta[1]])
     nd, npi = int(meta[4]), int(meta[5])
-    assert np.array_equal(step.dec_items.cpu().numpy()[:nd], ref_pk["dec_items"][:nd])
+    assert np.array_equal(step.dec_waves.cpu().numpy()[:nd], ref_pk["dec_waves"][:nd])
     assert np.array_equal(step.pre_items.cpu().numpy()[:npi], ref_pk["pre_items"][:npi])
 
 
@@ -89,7 +90,7 @@ def test_step_parity(gpu, cfgno):
     cfg = synth.CONFIGS[cfgno]()
     rng = np.random.default_rng(100 + cfgno)
     T, R = cfg.rows, cfg.n_reqs
-    kw = sc.pack_kwargs(cfg, dec_target_items=256 if cfgno == 1 else 1024, dec_min_split=2)
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=256 if cfgno == 1 else 2048, dec_min_pages=2)
     qkv_h = synth.rand_bf16(rng, (T, QKV_STRIDE))
     wq, wk = synth.norm_weights()
     pool = make_pool(cfg.pool_pages, 1000 + cfgno, gpu)
