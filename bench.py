@@ -44,6 +44,7 @@ def parse():
     ap.add_argument("--dec-grid-waves", type=int, default=None,
                     help="decode wavefronts (default: CUs x 8)")
     ap.add_argument("--dec-min-pages", type=int, default=8)
+    ap.add_argument("--pre-tile-q", type=int, default=32, choices=[32])
     ap.add_argument("--layers", type=int, default=None, help="config 5 only (default 36)")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only run the per-kernel graphs (for rocprofv3 passes)")
@@ -104,7 +105,8 @@ def main():
 
     step = AttnStep(max_rows=T, max_reqs=cfg.n_reqs, max_ctx=cfg.max_ctx,
                     pool_pages=cfg.pool_pages, device=dev,
-                    dec_grid_waves=args.dec_grid_waves, dec_min_pages=args.dec_min_pages)
+                    dec_grid_waves=args.dec_grid_waves, dec_min_pages=args.dec_min_pages,
+                    pre_tile_q=args.pre_tile_q)
     d_computed, d_n_new = t(cfg.computed), t(cfg.n_new)
     d_off, d_pages = t(cfg.bt_off), t(cfg.bt_pages)
     d_ntok = t(cfg.num_tokens) if scheduled else None

@@ -7,31 +7,39 @@
 // fp32 accumulation; output bf16, 0 when l == 0.
 //
 // MI355X design:
-//  * One 256-thread workgroup per (query tile of 64 rows, kv head): the 4 query heads
-//    of the kv head share every K/V tile, which is staged into LDS once (the reference
-//    runs one block per query head and re-reads K/V 4x, attn_cute.cu:157).
-//    Wave w takes rows (w/2)*32 .. +32 and heads 2*(w%2), 2*(w%2)+1.
+//  * One 256-thread workgroup per (32 query rows, kv head); wave w owns query head w of
+//    the kv head.  The 4 heads share every K/V tile, staged into LDS once (the
+//    reference runs one block per query head and re-reads K/V 4x, attn_cute.cu:157).
+//    At 212 VGPRs two workgroups share a CU, so one wave's MFMAs overlap another's
+//    softmax on every SIMD.
 //  * Transposed FA-2 on v_mfma_f32_32x32x16_bf16:
-//        S^T[32 keys x 32 rows] = K[32 x 128] . Q^T[128 x 32]   (8 MFMAs per head)
-//        O^T[128 x 32 rows]    += V^T[128 x 32 keys] . P^T      (8 MFMAs per head)
+//        S^T[32 keys x 32 rows] = K[32 x 128] . Q^T[128 x 32]   (8 MFMAs per 32 keys)
+//        O^T[128 x 32 rows]    += V^T[128 x 16 keys] . P^T      (4 MFMAs per 16 keys)
 //    With rows as accumulator columns every lane owns one query row: the softmax row
 //    max / sum is 16 in-lane values plus one exchange with lane^32, the rescale of O is
 //    a per-lane scalar, and the S^T accumulator registers are already the P^T operand
 //    (the key order inside the contraction is chosen to match, V^T is read to suit).
-//    Each K or V^T fragment read from LDS feeds both heads of the wave.
-//  * K/V tiles are 32 keys = 2 pages = two contiguous 8 KiB runs, double-buffered in
-//    LDS with XOR swizzles that make the fragment reads bank-conflict free; the next
-//    tile's global loads are in flight during the current tile's MFMAs.
+//  * Softmax VALU work per score, not MFMA, is the limit on CDNA (a wave64 VALU op
+//    issues in 4 cycles, exp in more): scores are maxed raw, scaled inside the exp2
+//    FMA, converted with v_cvt_pk_bf16_f32, and O is rescaled lazily (only when the
+//    row max grows by more than 2^8).
+//  * K/V tiles are 64 keys = 4 pages = four contiguous 8 KiB runs, double-buffered in
+//    LDS (2 x 32 KiB) with XOR swizzles that make every fragment read bank-conflict
+//    free and every fragment one 16-byte read; the next tile's global loads are in
+//    flight during the current tile's MFMAs.
 //  * Work items come from the pack sorted by key count, longest first.
 #include "fqa_common.h"
 
 namespace fqa {
 namespace {
 
-constexpr int kQT = 64;           // query rows per workgroup
-constexpr int kKT = 32;           // keys per LDS tile (2 pages)
-constexpr int kStageBytes = 2 * kRunElems * 2;  // 16 KiB
+constexpr int kQT = 32;        // query rows per workgroup
+constexpr int kKT = 64;        // keys per LDS tile (4 pages)
+constexpr int kPagesPerTile = kKT / kPage;
+constexpr int kRunBytes = kRunElems * 2;                 // 8 KiB
+constexpr int kStageBytes = kPagesPerTile * kRunBytes;   // 32 KiB
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kRescale = 8.0f;  // lazy-rescale threshold (log2 units)
 
 struct PreArgs {
   const uint16_t* qkv;
@@ -48,27 +56,29 @@ struct PreArgs {
   float scale_log2;
 };
 
-// LDS byte offset of K chunk (16 B) `c` of token `t` in page slot `ps` of a stage.
+// LDS byte offset of K chunk (16 B = 8 dims) `c` of token `t` in page slot `ps`.
 __device__ __forceinline__ int lds_k(int ps, int t, int c) {
-  return ps * (kRunElems * 2) + t * 256 + ((c ^ t) << 4);
+  return ps * kRunBytes + t * 256 + ((c ^ t) << 4);
 }
-// LDS byte offset of V^T unit (8 B = 4 tokens) `u` of dim row `d` in page slot `ps`.
-__device__ __forceinline__ int lds_v(int ps, int d, int u) {
-  return ps * (kRunElems * 2) + kVOff * 2 + d * 32 + ((u ^ ((d >> 3) & 3)) << 3);
+// LDS byte offset of V^T chunk `h` of dim row `d` in page slot `ps`.  A row's 16 tokens
+// are stored as chunk 0 = tokens {0-3, 8-11}, chunk 1 = tokens {4-7, 12-15}: exactly the
+// 8 keys one lane half contributes to a 16-key PV step.
+__device__ __forceinline__ int lds_v(int ps, int d, int h) {
+  return ps * kRunBytes + kVOff * 2 + d * 32 + ((h ^ ((d >> 2) & 1)) << 4);
 }
 
-__device__ __forceinline__ uint4 zero_tokens(uint4 v, int first_bad) {
-  // v holds 8 consecutive tokens (bf16) of one V^T row; clear tokens >= first_bad
-  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+// Keep the first `valid` (0..16) tokens of 8 bf16 tokens t0.. of one V^T row.
+__device__ __forceinline__ uint2 keep_tokens(uint2 v, int t0, int valid) {
+  uint32_t w[2] = {v.x, v.y};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if (2 * i >= first_bad) w[i] &= 0xffff0000u;
-    if (2 * i + 1 >= first_bad) w[i] &= 0x0000ffffu;
+  for (int i = 0; i < 2; ++i) {
+    const int ta = t0 + 2 * i;
+    w[i] &= (ta < valid ? 0x0000ffffu : 0u) | (ta + 1 < valid ? 0xffff0000u : 0u);
   }
-  return make_uint4(w[0], w[1], w[2], w[3]);
+  return make_uint2(w[0], w[1]);
 }
 
-__global__ void __launch_bounds__(256) prefill_kernel(PreArgs a) {
+__global__ void __launch_bounds__(256, 2) prefill_kernel(PreArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[2 * kStageBytes];
 
   const int item = blockIdx.x >> 3, kvh = blockIdx.x & 7;
@@ -80,81 +90,80 @@ __global__ void __launch_bounds__(256) prefill_kernel(PreArgs a) {
   const int32_t* btr = a.bt + (long long)r * a.max_blocks;
   const int nkb = (nkeys + kKT - 1) / kKT;
 
-  // ---- this wave's rows and heads ---------------------------------------------------
   const int col = lane & 31, hf = lane >> 5;
-  const int i_row = q0 + (w >> 1) * 32 + col;  // row within the request
+  const int i_row = q0 + col;  // row within the request
   const bool row_ok = i_row < q1;
   const int qpos = row_ok ? a.pos[qs + i_row] : -1;
-  const int h0 = kvh * kG + (w & 1) * 2;
-  const int wave_first = q0 + (w >> 1) * 32;
-  const bool wave_live = wave_first < q1;
-  // key blocks this wave needs: keys up to the last valid row's position
-  const int wave_last = min(wave_first + 31, q1 - 1);
-  const int wave_nkb = wave_live ? (a.pos[qs + wave_last] + kKT) / kKT : 0;
-  const int wave_min_pos = wave_live ? a.pos[qs + wave_first] : 0;
+  const int min_pos = a.pos[qs + q0];  // first row: smallest position of the tile
+  const int h = kvh * kG + w;
 
-  bf16x8 qf[2][8];
-#pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
-    const uint16_t* q = a.qkv + (long long)(qs + i_row) * a.stride + (h0 + hh) * kD + hf * 8;
+  bf16x8 qf[8];
+  {
+    const uint16_t* q = a.qkv + (long long)(qs + (row_ok ? i_row : q0)) * a.stride + h * kD + hf * 8;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-      if (row_ok) qf[hh][ks] = *reinterpret_cast<const bf16x8*>(q + ks * 16);
-      else
+      qf[ks] = *reinterpret_cast<const bf16x8*>(q + ks * 16);
+      if (!row_ok)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) qf[hh][ks][i] = (__bf16)0.0f;
+        for (int i = 0; i < 8; ++i) qf[ks][i] = (__bf16)0.0f;
     }
   }
 
-  float16_t o[2][4];
+  float16_t o[4];
 #pragma unroll
-  for (int hh = 0; hh < 2; ++hh)
+  for (int db = 0; db < 4; ++db)
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) o[hh][db][i] = 0.f;
-  float m_run[2] = {-1e30f, -1e30f}, l_run[2] = {0.f, 0.f};
+    for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
+  float m_run = -1e30f, l_run = 0.f;
 
-  // ---- staging: 1024 chunks of 16 B per tile, 4 per thread ----------------------------
-  uint4 stg[4];
+  // ---- staging: per tile each thread moves 4 K chunks (16 B) and 2 V^T rows (32 B) ----
+  // K chunk i of thread t: page slot i, token t/16, dims (t%16)*8..; V^T row j: page slot
+  // 2j + t/128, dim t%128.
+  uint4 sk[4];
+  uint4 sv[2][2];
   auto stage_load = [&](int kb) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + i * 256, ps = c >> 9, e = c & 511;
-      const int pidx = kb * 2 + ps;
-      const int key_base = pidx * kPage;
-      stg[i] = make_uint4(0, 0, 0, 0);
-      if (key_base < nkeys) {
-        const long long page = btr[pidx];
-        if (page >= 0 && page < a.pool_pages) {
-          const uint16_t* run = a.pool + run_offset(page, kvh);
-          uint4 v = *reinterpret_cast<const uint4*>(run + e * 8);
-          const int valid = nkeys - key_base;  // tokens of this page that exist
-          if (valid < kPage) {
-            if (e < 256) {
-              if ((e >> 4) >= valid) v = make_uint4(0, 0, 0, 0);
-            } else {
-              v = zero_tokens(v, valid - ((e - 256) & 1) * 8);
-            }
-          }
-          stg[i] = v;
+    for (int ps = 0; ps < kPagesPerTile; ++ps) {
+      const int pidx = kb * kPagesPerTile + ps;
+      const int valid = nkeys - pidx * kPage;  // tokens of this page that exist (may be <= 0)
+      const long long page = valid > 0 ? btr[pidx] : -1;
+      const bool ok = page >= 0 && page < a.pool_pages;
+      const uint16_t* run = a.pool + run_offset(ok ? page : 0, kvh);
+      const int tk = tid >> 4;
+      uint4 v = *reinterpret_cast<const uint4*>(run + tid * 8);
+      const bool keep = ok && tk < valid;
+      sk[ps] = keep ? v : make_uint4(0, 0, 0, 0);
+      if ((ps >> 1) * 2 + (tid >> 7) == ps) {  // this thread's V^T row lives in page ps
+        const int j = ps >> 1, d = tid & 127;
+        const uint16_t* vr = run + kVOff + d * kPage;
+        uint4 lo = *reinterpret_cast<const uint4*>(vr);
+        uint4 hi = *reinterpret_cast<const uint4*>(vr + 8);
+        if (!ok) lo = hi = make_uint4(0, 0, 0, 0);
+        if (valid < kPage) {
+          uint2 a0 = keep_tokens(make_uint2(lo.x, lo.y), 0, valid);
+          uint2 a1 = keep_tokens(make_uint2(lo.z, lo.w), 4, valid);
+          uint2 b0 = keep_tokens(make_uint2(hi.x, hi.y), 8, valid);
+          uint2 b1 = keep_tokens(make_uint2(hi.z, hi.w), 12, valid);
+          lo = make_uint4(a0.x, a0.y, a1.x, a1.y);
+          hi = make_uint4(b0.x, b0.y, b1.x, b1.y);
         }
+        // chunk 0 = tokens {0-3, 8-11}, chunk 1 = tokens {4-7, 12-15}
+        sv[j][0] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        sv[j][1] = make_uint4(lo.z, lo.w, hi.z, hi.w);
       }
     }
   };
   auto stage_store = [&](int buf) {
     char* base = lds + buf * kStageBytes;
+    const int tk = tid >> 4, cc = tid & 15;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + i * 256, ps = c >> 9, e = c & 511;
-      if (e < 256) {
-        const int t = e >> 4, cc = e & 15;
-        *reinterpret_cast<uint4*>(base + lds_k(ps, t, cc)) = stg[i];
-      } else {
-        const int e2 = e - 256, d = e2 >> 1, u = (e2 & 1) * 2;
-        *reinterpret_cast<uint2*>(base + lds_v(ps, d, u)) = make_uint2(stg[i].x, stg[i].y);
-        *reinterpret_cast<uint2*>(base + lds_v(ps, d, u + 1)) = make_uint2(stg[i].z, stg[i].w);
-      }
+    for (int ps = 0; ps < kPagesPerTile; ++ps)
+      *reinterpret_cast<uint4*>(base + lds_k(ps, tk, cc)) = sk[ps];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int ps = 2 * j + (tid >> 7), d = tid & 127;
+      *reinterpret_cast<uint4*>(base + lds_v(ps, d, 0)) = sv[j][0];
+      *reinterpret_cast<uint4*>(base + lds_v(ps, d, 1)) = sv[j][1];
     }
   };
 
@@ -165,68 +174,66 @@ __global__ void __launch_bounds__(256) prefill_kernel(PreArgs a) {
   for (int kb = 0; kb < nkb; ++kb) {
     const int buf = kb & 1;
     if (kb + 1 < nkb) stage_load(kb + 1);
-    if (kb < wave_nkb) {
-      const char* base = lds + buf * kStageBytes;
-      // S^T = K Q^T for both heads
-      float16_t s[2];
+    const char* base = lds + buf * kStageBytes;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) { s[0][i] = 0.f; s[1][i] = 0.f; }
+    for (int j = 0; j < 2; ++j) {  // two 32-key halves of the tile
+      const int key0 = kb * kKT + j * 32;
+      if (key0 >= nkeys) continue;  // past the last row's position (wave-uniform)
+      // S^T = K Q^T
+      float16_t s;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[i] = 0.f;
       {
-        const int key = col, ps = key >> 4, t = key & 15;
+        const int ps = j * 2 + (col >> 4), t = col & 15;
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
           const bf16x8 kf = *reinterpret_cast<const bf16x8*>(base + lds_k(ps, t, ks * 2 + hf));
-          s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[0][ks], s[0], 0, 0, 0);
-          s[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[1][ks], s[1], 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s, 0, 0, 0);
         }
       }
-      const bool need_mask = (kb + 1) * kKT - 1 > wave_min_pos;
-      bf16x8 pt[2][2];
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        float mx = -INFINITY;
+      // online softmax over this lane's query row
+      float mx = -INFINITY;
+      if (key0 + 31 > min_pos) {  // the causal diagonal crosses these keys
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          float x = s[hh][v] * a.scale_log2;
-          if (need_mask) {
-            const int key = kb * kKT + (v >> 2) * 8 + hf * 4 + (v & 3);
-            if (key > qpos) x = -INFINITY;
-          }
-          s[hh][v] = x;
-          mx = fmaxf(mx, x);
+          const int key = key0 + (v >> 2) * 8 + hf * 4 + (v & 3);
+          if (key > qpos) s[v] = -INFINITY;
+          mx = fmaxf(mx, s[v]);
         }
-        mx = wave_max_xor(mx, 32);
-        const float m_new = fmaxf(m_run[hh], mx);
-        const float corr = exp2f(m_run[hh] - m_new);
-        float psum = 0.f;
+      } else {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float p = exp2f(s[hh][v] - m_new);
-          s[hh][v] = p;
-          psum += p;
-        }
-        l_run[hh] = l_run[hh] * corr + psum;
-        m_run[hh] = m_new;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) o[hh][db] *= corr;
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc)
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-            pt[hh][kc][j] = __builtin_bit_cast(__bf16, f32_to_bf16_bits(s[hh][kc * 8 + j]));
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[v]);
       }
-      // O^T += V^T P^T
+      mx = wave_max_xor(mx, 32);
+      // Lazy rescale: the reference max only moves when the row max grows by more than
+      // 2^kRescale, so P = exp2(s*scale - m) stays <= 2^kRescale and O, l are rescaled
+      // on few tiles instead of every tile.
+      const float m_new = fmaxf(m_run, mx * a.scale_log2);
+      if (m_new > m_run + kRescale) {
+        const float corr = exp2f(m_run - m_new);
+        l_run *= corr;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const int d = db * 32 + col;
+        for (int db = 0; db < 4; ++db) o[db] *= corr;
+        m_run = m_new;
+      }
+      bf16x8 pt[2];
+      float psum = 0.f;
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-          const uint2 lo = *reinterpret_cast<const uint2*>(base + lds_v(kc, d, hf));
-          const uint2 hi = *reinterpret_cast<const uint2*>(base + lds_v(kc, d, 2 + hf));
-          const uint4 vv = make_uint4(lo.x, lo.y, hi.x, hi.y);
-          const bf16x8 vf = __builtin_bit_cast(bf16x8, vv);
-          o[0][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pt[0][kc], o[0][db], 0, 0, 0);
-          o[1][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pt[1][kc], o[1][db], 0, 0, 0);
+      for (int v = 0; v < 16; ++v) {
+        const float p = exp2f(fmaf(s[v], a.scale_log2, -m_run));
+        psum += p;
+        pt[v >> 3][v & 7] = (__bf16)p;
+      }
+      l_run += psum;
+      // O^T += V^T P^T over the two pages (16 keys each) of this half
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const int ps = j * 2 + kc;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const bf16x8 vf =
+              *reinterpret_cast<const bf16x8*>(base + lds_v(ps, db * 32 + col, hf));
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pt[kc], o[db], 0, 0, 0);
         }
       }
     }
@@ -235,21 +242,17 @@ __global__ void __launch_bounds__(256) prefill_kernel(PreArgs a) {
   }
 
   if (!row_ok) return;
+  const float l = l_run + __shfl_xor(l_run, 32, kWave);
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  uint16_t* dst = a.out + (long long)(qs + i_row) * (kHq * kD) + h * kD + hf * 4;
 #pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
-    float l = l_run[hh] + __shfl_xor(l_run[hh], 32, kWave);
-    const float inv = l > 0.f ? 1.0f / l : 0.f;
-    uint16_t* dst = a.out + (long long)(qs + i_row) * (kHq * kD) + (h0 + hh) * kD + hf * 4;
+  for (int db = 0; db < 4; ++db)
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float16_t& v = o[hh][db];
-        uint2 pk = make_uint2(pack_bf16x2(v[i * 4] * inv, v[i * 4 + 1] * inv),
-                              pack_bf16x2(v[i * 4 + 2] * inv, v[i * 4 + 3] * inv));
-        *reinterpret_cast<uint2*>(dst + db * 32 + i * 8) = pk;
-      }
-  }
+    for (int i = 0; i < 4; ++i) {
+      const uint2 pk = make_uint2(pack_bf16x2(o[db][i * 4] * inv, o[db][i * 4 + 1] * inv),
+                                  pack_bf16x2(o[db][i * 4 + 2] * inv, o[db][i * 4 + 3] * inv));
+      *reinterpret_cast<uint2*>(dst + db * 32 + i * 8) = pk;
+    }
 }
 
 bool dims_ok(const fqa_dims* d) {
@@ -276,7 +279,7 @@ extern "C" int fqa_prefill(const fqa_dims* dims, const uint16_t* qkv, const uint
     return FQA_EINVAL;
   PreArgs a{qkv, pool, pool_pages, block_tables, max_blocks, cu_seqlens, positions, pre_items,
             meta, out, dims->qkv_stride, dims->scale * kLog2e};
-  hipLaunchKernelGGL(prefill_kernel, dim3(pre_item_cap * kHkv), dim3(256), 0, (hipStream_t)stream,
-                     a);
+  hipLaunchKernelGGL(prefill_kernel, dim3(pre_item_cap * kHkv), dim3(256), 0,
+                     (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
 }

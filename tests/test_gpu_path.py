@@ -82,15 +82,16 @@ def check_pack(step, ref_pk, R, T, kw):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("cfgno", [1, 2, 3])
-def test_step_parity(gpu, cfgno):
+@pytest.mark.parametrize("cfgno,tile", [(1, 32), (2, 32), (3, 32)])
+def test_step_parity(gpu, cfgno, tile):
     from oracle import oracle as orc
 
-    print(f"[test_step_parity] config{cfgno}", flush=True)
+    print(f"[test_step_parity] config{cfgno} tile{tile}", flush=True)
     cfg = synth.CONFIGS[cfgno]()
     rng = np.random.default_rng(100 + cfgno)
     T, R = cfg.rows, cfg.n_reqs
-    kw = sc.pack_kwargs(cfg, dec_grid_waves=256 if cfgno == 1 else 2048, dec_min_pages=2)
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=256 if cfgno == 1 else 2048, dec_min_pages=2,
+                        pre_tile_q=tile)
     qkv_h = synth.rand_bf16(rng, (T, QKV_STRIDE))
     wq, wk = synth.norm_weights()
     pool = make_pool(cfg.pool_pages, 1000 + cfgno, gpu)
