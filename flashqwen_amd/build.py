@@ -51,5 +51,15 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+def build_cpp_driver() -> Path:
+    """tests/cpp/step_cpp: a C++ program driving the path through include/fqa_step.hpp."""
+    root = PKG.parent
+    src = root / "tests" / "cpp" / "step_cpp.cpp"
+    exe = src.with_suffix("")
+    _run([HIPCC, "-O2", "-std=c++17", "-o", str(exe), str(src), f"-L{PKG}", "-lfqa",
+          "-Wl,-rpath,$ORIGIN/../../flashqwen_amd"])
+    return exe
+
+
 if __name__ == "__main__":
     build(verbose=True)

@@ -1,0 +1,186 @@
+// fqa_step.hpp — C++ host-side mirror of the reference engine's per-step attention
+// interface, over the C ABI of fqa.h.  Header-only; link with libfqa.so and amdhip64.
+//
+// Reference interface it mirrors (engine/src/):
+//   StepContext::StepContext(max_rows, slots, max_ctx)      model_runtime.h:119-136
+//   StepContext::PrepareInputs(ForwardInput, rng, stream)   model_runtime.cu:295-302
+//   LaunchHeadNormRope(...) + KvStore::StoreKV(...)          kernels.cuh:28-31, kv_store.h:29-31
+//   LaunchAttnDecodeCute(...)                                attn_cute.h:14-20
+//   LaunchAttnPrefillCute(...)                               attn_cute.h:7-12
+//
+// Differences a caller sees: PrepareInputs takes the batch as plain host vectors (the
+// reference's ForwardInput rows are derived on the device from computed/n per request),
+// and errors throw std::runtime_error with the FQA_E* code instead of exit(1).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "fqa.h"
+
+namespace fqa {
+
+inline void Check(int rc, const char* what) {
+  if (rc != FQA_OK) throw std::runtime_error(std::string(what) + " failed: " + std::to_string(rc));
+}
+inline void HipCheck(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Owning device buffer (the reference's DeviceBuffer, cuda_helpers.h:38-78).
+template <class T>
+class DeviceBuffer {
+ public:
+  DeviceBuffer() = default;
+  explicit DeviceBuffer(size_t n) : n_(n) {
+    if (n) HipCheck(hipMalloc(&p_, n * sizeof(T)), "hipMalloc");
+  }
+  DeviceBuffer(DeviceBuffer&& o) noexcept : p_(o.p_), n_(o.n_) { o.p_ = nullptr; o.n_ = 0; }
+  DeviceBuffer& operator=(DeviceBuffer&& o) noexcept {
+    if (this != &o) { Free(); p_ = o.p_; n_ = o.n_; o.p_ = nullptr; o.n_ = 0; }
+    return *this;
+  }
+  ~DeviceBuffer() { Free(); }
+  T* D() const { return p_; }
+  size_t Size() const { return n_; }
+  void Upload(const T* h, size_t n, hipStream_t s) {
+    HipCheck(hipMemcpyAsync(p_, h, n * sizeof(T), hipMemcpyHostToDevice, s), "upload");
+  }
+
+ private:
+  void Free() { if (p_) (void)hipFree(p_); p_ = nullptr; }
+  T* p_ = nullptr;
+  size_t n_ = 0;
+};
+
+// One step's batch as the scheduler hands it over (Request::EmitChunk, scheduler.h:66-72):
+// request r adds n_new[r] rows at positions computed[r]..; block_tables[r] are its pages.
+struct BatchInput {
+  std::vector<int32_t> computed, n_new;
+  std::vector<std::vector<int32_t>> block_tables;
+};
+
+class StepContext {
+ public:
+  StepContext(int max_rows, int slots, int max_ctx, int64_t pool_pages, int device = 0,
+              int dec_grid_waves = 0, int dec_min_pages = 8)
+      : max_rows_(max_rows), slots_(slots), max_ctx_(max_ctx), pool_pages_(pool_pages) {
+    if (slots > FQA_MAX_REQS) throw std::runtime_error("slots > FQA_MAX_REQS");
+    max_blocks_ = (max_ctx + FQA_PAGE_TOKENS - 1) / FQA_PAGE_TOKENS;
+    dims_ = {32, 8, 128, FQA_PAGE_TOKENS, 6144, 1e-6f, 1.0f / std::sqrt(128.0f)};
+    if (dec_grid_waves <= 0) dec_grid_waves = fqa_dec_default_waves(device);
+    if (dec_grid_waves <= 0) dec_grid_waves = 2048;
+    dec_cap_ = fqa_dec_wave_bound(slots, dec_grid_waves);
+    pre_cap_ = fqa_pre_item_bound(slots, max_rows, 32);
+    cfg_ = {max_rows, max_blocks_, pool_pages, dec_grid_waves, dec_min_pages, dec_cap_, 32,
+            pre_cap_};
+    computed_ = DeviceBuffer<int32_t>(slots);
+    n_new_ = DeviceBuffer<int32_t>(slots);
+    bt_off_ = DeviceBuffer<int32_t>(slots + 1);
+    bt_pages_ = DeviceBuffer<int32_t>((size_t)slots * max_blocks_);
+    cu_ = DeviceBuffer<int32_t>(slots + 1);
+    qlen_ = DeviceBuffer<int32_t>(slots);
+    pos_ = DeviceBuffer<int32_t>(max_rows);
+    req_ = DeviceBuffer<int32_t>(max_rows);
+    slot_ = DeviceBuffer<int32_t>(max_rows);
+    bt_ = DeviceBuffer<int32_t>((size_t)slots * max_blocks_);
+    drids_ = DeviceBuffer<int32_t>(slots);
+    prids_ = DeviceBuffer<int32_t>(slots);
+    dseqs_ = DeviceBuffer<int32_t>((size_t)slots * 4);
+    dwaves_ = DeviceBuffer<int32_t>((size_t)dec_cap_ * 4);
+    items_ = DeviceBuffer<int32_t>((size_t)pre_cap_ * 4);
+    meta_ = DeviceBuffer<int32_t>(FQA_META_LEN);
+    ws_ = DeviceBuffer<unsigned char>((size_t)fqa_decode_workspace_bytes(&dims_, dec_cap_));
+    std::vector<float> c((size_t)max_ctx * 64), s((size_t)max_ctx * 64);
+    Check(fqa_rope_tables(max_ctx, 128, 1.0e6f, c.data(), s.data()), "fqa_rope_tables");
+    cos_ = DeviceBuffer<float>(c.size());
+    sin_ = DeviceBuffer<float>(s.size());
+    cos_.Upload(c.data(), c.size(), nullptr);
+    sin_.Upload(s.data(), s.size(), nullptr);
+    HipCheck(hipDeviceSynchronize(), "rope upload");
+  }
+
+  // StepContext::PrepareInputs: upload the per-request batch and pack it on the GPU.
+  void PrepareInputs(const BatchInput& in, hipStream_t stream) {
+    const int R = (int)in.computed.size();
+    if (R > slots_) throw std::runtime_error("batch larger than slots");
+    h_off_.assign(R + 1, 0);
+    h_pages_.clear();
+    rows_ = 0;
+    for (int r = 0; r < R; ++r) {
+      h_pages_.insert(h_pages_.end(), in.block_tables[r].begin(), in.block_tables[r].end());
+      h_off_[r + 1] = (int32_t)h_pages_.size();
+      rows_ += in.n_new[r];
+    }
+    if (h_pages_.size() > bt_pages_.Size()) throw std::runtime_error("block tables too long");
+    if (R) {
+      computed_.Upload(in.computed.data(), R, stream);
+      n_new_.Upload(in.n_new.data(), R, stream);
+    }
+    bt_off_.Upload(h_off_.data(), R + 1, stream);
+    if (!h_pages_.empty()) bt_pages_.Upload(h_pages_.data(), h_pages_.size(), stream);
+    fqa_batch b{computed_.D(), n_new_.D(), bt_off_.D(), bt_pages_.D(), nullptr, R};
+    fqa_pack_out o{cu_.D(), qlen_.D(), pos_.D(), req_.D(), slot_.D(), bt_.D(), drids_.D(),
+                   prids_.D(), dseqs_.D(), dwaves_.D(), items_.D(), meta_.D()};
+    Check(fqa_pack(&b, &cfg_, &o, stream), "fqa_pack");
+    n_reqs_ = R;
+    has_decode_ = has_prefill_ = false;
+    for (int r = 0; r < R; ++r) (in.n_new[r] == 1 ? has_decode_ : has_prefill_) = true;
+  }
+
+  // LaunchHeadNormRope + KvStore::StoreKV for one layer (fused).
+  void HeadNormRopeStoreKV(uint16_t* qkv, const float* q_norm, const float* k_norm,
+                           uint16_t* pool_layer, hipStream_t stream) const {
+    Check(fqa_qknorm_rope_append(&dims_, qkv, q_norm, k_norm, cos_.D(), sin_.D(), max_ctx_,
+                                 pos_.D(), slot_.D(), meta_.D(), rows_, pool_layer, pool_pages_,
+                                 0, stream),
+          "fqa_qknorm_rope_append");
+  }
+  // LaunchAttnDecodeCute.
+  void AttnDecode(const uint16_t* qkv, const uint16_t* pool_layer, uint16_t* out,
+                  hipStream_t stream) const {
+    if (!has_decode_) return;
+    Check(fqa_decode(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_, dwaves_.D(),
+                     dseqs_.D(), meta_.D(), dec_cap_, n_reqs_, ws_.D(), out, stream),
+          "fqa_decode");
+  }
+  // LaunchAttnPrefillCute.
+  void AttnPrefill(const uint16_t* qkv, const uint16_t* pool_layer, uint16_t* out,
+                   hipStream_t stream) const {
+    if (!has_prefill_) return;
+    Check(fqa_prefill(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_, cu_.D(),
+                      pos_.D(), items_.D(), meta_.D(), 32, pre_cap_, out, stream),
+          "fqa_prefill");
+  }
+  // The attention block of one layer (model_runtime.cu:263-278).
+  void RunLayer(uint16_t* qkv, const float* q_norm, const float* k_norm, uint16_t* pool_layer,
+                uint16_t* out, hipStream_t stream) const {
+    HeadNormRopeStoreKV(qkv, q_norm, k_norm, pool_layer, stream);
+    AttnDecode(qkv, pool_layer, out, stream);
+    AttnPrefill(qkv, pool_layer, out, stream);
+  }
+
+  const int32_t* Meta() const { return meta_.D(); }
+  int Rows() const { return rows_; }
+
+ private:
+  int max_rows_, slots_, max_ctx_, max_blocks_ = 0;
+  int64_t pool_pages_;
+  int dec_cap_ = 0, pre_cap_ = 0, n_reqs_ = 0, rows_ = 0;
+  bool has_decode_ = false, has_prefill_ = false;
+  fqa_dims dims_{};
+  fqa_pack_cfg cfg_{};
+  std::vector<int32_t> h_off_, h_pages_;
+  DeviceBuffer<int32_t> computed_, n_new_, bt_off_, bt_pages_;
+  DeviceBuffer<int32_t> cu_, qlen_, pos_, req_, slot_, bt_, drids_, prids_, dseqs_, dwaves_, items_,
+      meta_;
+  DeviceBuffer<unsigned char> ws_;
+  DeviceBuffer<float> cos_, sin_;
+};
+
+}  // namespace fqa

@@ -1,0 +1,123 @@
+"""Independent pure-Python restatements used to pin the C oracle (tests only).
+
+Written per row / per request from the reference's definitions, deliberately in a
+different shape from oracle/fqa_oracle.c (dicts and per-row loops instead of scans), so a
+shared mistake is unlikely:
+
+  build_batch   Scheduler::BuildBatch (engine/src/scheduler.cc:116-143): the greedy loop
+                over running requests stably sorted by Remaining().
+  pack          EmitChunk rows (scheduler.h:66-72), PackBlockTables + SplitDecodePrefill
+                (model_runtime.cu:54-91), slot = bt[p/16]*16 + p%16 (kv_store.cu:56-60),
+                plus this library's decode/prefill plans as documented in include/fqa.h.
+"""
+from __future__ import annotations
+
+PAGE = 16
+
+
+def build_batch(num_tokens, computed, budget, chunk):
+    order = sorted(range(len(num_tokens)), key=lambda i: (num_tokens[i] - computed[i], i))
+    out = []
+    for i in order:
+        if budget <= 0:
+            break
+        rem = num_tokens[i] - computed[i]
+        if rem <= 0:
+            continue
+        n = min(rem, budget)
+        if rem > 1:
+            n = min(n, chunk)
+        out.append((i, n))
+        budget -= n
+    return out
+
+
+def _cdiv(a, b):
+    return -(-a // b)
+
+
+def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_waves,
+         dec_min_pages, dec_wave_cap, pre_tile_q, pre_item_cap):
+    R = len(computed)
+    meta = [0] * 16
+    meta[8] = R
+    codes = []
+    rows_total = 0
+    for c, n, t in zip(computed, n_new, tables):
+        if c < 0 or n < 0:
+            codes.append(5)
+            continue
+        if len(t) < _cdiv(c + n, PAGE):
+            codes.append(1)
+        elif len(t) > max_blocks:
+            codes.append(2)
+        rows_total += n
+    if rows_total > max_rows:
+        codes.append(3)
+    if codes:
+        meta[7] = min(codes)
+        return {"meta": meta}
+
+    res = {"positions": [], "row_req": [], "slot_mapping": [], "cu_seqlens": [],
+           "qlen": list(n_new)}
+    for r in range(R):
+        res["cu_seqlens"].append(len(res["positions"]))
+        for k in range(n_new[r]):
+            p = computed[r] + k
+            res["positions"].append(p)
+            res["row_req"].append(r)
+            res["slot_mapping"].append(tables[r][p // PAGE] * PAGE + p % PAGE)
+    res["cu_seqlens"].append(len(res["positions"]))
+    dec = [r for r in range(R) if n_new[r] == 1]
+    pre = [r for r in range(R) if n_new[r] != 1]
+    res["decode_rids"] = dec + [-1] * (R - len(dec))
+    res["prefill_rids"] = pre + [-1] * (R - len(pre))
+    bt = []
+    bad = False
+    for t in tables:
+        row = list(t) + [-1] * (max_blocks - len(t))
+        bad |= any(not (0 <= v < pool_pages) for v in t)
+        bt.extend(row)
+    res["block_tables"] = bt
+
+    # decode stream-K plan: concatenate streams (di, kvh), cut into G equal shares
+    runs = []  # (di, kvh, page) for every page run, in order
+    seqs = []
+    P = 0
+    for di, r in enumerate(dec):
+        pages = computed[r] // PAGE + 1
+        seqs.append([r, res["cu_seqlens"][r], computed[r] + 1, 8 * P])
+        for kvh in range(8):
+            for pg in range(pages):
+                runs.append((di, kvh, pg))
+        P += pages
+    W = len(runs)
+    G = min(dec_grid_waves, _cdiv(W, max(1, dec_min_pages))) if W else 0
+    waves = []
+    for w in range(G):
+        g0, g1 = w * W // G, (w + 1) * W // G
+        waves.append([*runs[g0], g1 - g0])
+    # prefill items: tiles sorted by key count descending, stable
+    tiles = []
+    for r in pre:
+        q = n_new[r]
+        for q0 in range(0, q, pre_tile_q):
+            q1 = min(q0 + pre_tile_q, q)
+            tiles.append([r, q0, q1, computed[r] + q1])
+    items = sorted(tiles, key=lambda x: -x[3])  # Python's sort is stable
+    if G > dec_wave_cap or len(items) > pre_item_cap:
+        meta = [0] * 16
+        meta[8], meta[7] = R, 6
+        return {"meta": meta}
+    res["dec_seqs"] = seqs
+    res["dec_waves"] = waves
+    res["pre_items"] = items
+    meta[0] = rows_total
+    meta[1], meta[2] = len(dec), len(pre)
+    meta[3] = max([1] + [n_new[r] for r in pre])
+    meta[4], meta[5] = G, len(items)
+    meta[6] = _cdiv(W, G) if G else 0
+    meta[7] = 4 if bad else 0
+    meta[9] = P
+    res["meta"] = meta
+    return res

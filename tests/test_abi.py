@@ -1,0 +1,111 @@
+"""The C ABI without a GPU: libfqa.so loads, exports every function include/fqa.h declares,
+its host-side helpers are exact, and rejected calls return error codes before any launch."""
+from __future__ import annotations
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from flashqwen_amd import _lib
+from flashqwen_amd.step import make_dims
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "fqa.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(fqa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib.SIGNATURES), "ctypes table and header disagree"
+    assert lib.fqa_version().startswith(b"fqa")
+
+
+def test_rope_tables_bit_identical_to_oracle():
+    from oracle import oracle as orc
+
+    lib = _lib.load()
+    for max_pos in (1, 17, 4096):
+        cos = np.empty((max_pos, 64), np.float32)
+        sin = np.empty_like(cos)
+        assert lib.fqa_rope_tables(max_pos, 128, 1e6, cos.ctypes.data, sin.ctypes.data) == 0
+        oc, os_ = orc.rope_tables(max_pos)
+        assert np.array_equal(cos.view(np.uint32), oc.view(np.uint32))
+        assert np.array_equal(sin.view(np.uint32), os_.view(np.uint32))
+
+
+def test_sizes_and_bounds():
+    lib = _lib.load()
+    d = make_dims()
+    assert lib.fqa_pool_bytes(C.byref(d), 12500) == 12500 * 64 * 1024
+    assert lib.fqa_pool_bytes(C.byref(d), 84771) == 84771 * 65536  # > 2^31 elements ok
+    assert lib.fqa_dec_wave_bound(64, 2048) == 2048
+    assert lib.fqa_pre_item_bound(16, 8192, 32) == 8192 // 32 + 16
+    assert lib.fqa_decode_workspace_bytes(C.byref(d), 2048) == 2 * 2048 * 4 * 130 * 4
+
+
+def test_rejected_calls_return_codes_without_launching():
+    lib = _lib.load()
+    d = make_dims()
+    bad = make_dims()
+    bad.head_dim = 64
+    null = None
+    # pack: null structs, too many requests, bad tile, zero grid waves
+    assert lib.fqa_pack(null, null, null, null) == _lib.FQA_EINVAL
+    b = _lib.FqaBatch(null, null, null, null, null, _lib.FQA_MAX_REQS + 1)
+    cfg = _lib.FqaPackCfg(8, 8, 8, 16, 1, 16, 32, 8)
+    out = _lib.FqaPackOut()
+    assert lib.fqa_pack(C.byref(b), C.byref(cfg), C.byref(out), null) == _lib.FQA_EINVAL
+    b.n_reqs = 1
+    cfg.pre_tile_q = 48
+    assert lib.fqa_pack(C.byref(b), C.byref(cfg), C.byref(out), null) == _lib.FQA_EINVAL
+    cfg.pre_tile_q = 32
+    cfg.dec_grid_waves = 0
+    assert lib.fqa_pack(C.byref(b), C.byref(cfg), C.byref(out), null) == _lib.FQA_EINVAL
+    # shapes other than Qwen3-8B's are refused
+    assert lib.fqa_decode(C.byref(bad), null, null, 1, null, 1, null, null, null, 4, 4, null,
+                          null, null) == _lib.FQA_EUNSUPPORTED
+    assert lib.fqa_prefill(C.byref(bad), null, null, 1, null, 1, null, null, null, null, 32, 1,
+                           null, null) == _lib.FQA_EUNSUPPORTED
+    assert lib.fqa_qknorm_rope_append(C.byref(bad), *([null] * 5 + [1] + [null] * 3 + [1, null, 1,
+                                                        0, null])) == _lib.FQA_EUNSUPPORTED
+    # unsupported prefill tile; null pointers with work to do
+    assert lib.fqa_prefill(C.byref(d), null, null, 1, null, 1, null, null, null, null, 64, 1, null,
+                           null) == _lib.FQA_EUNSUPPORTED
+    assert lib.fqa_decode(C.byref(d), null, null, 1, null, 1, null, null, null, 4, 4, null, null,
+                          null) == _lib.FQA_EINVAL
+    assert lib.fqa_schedule(null, null, _lib.FQA_MAX_REQS + 1, 1, 1, null, null, null,
+                            null) == _lib.FQA_EINVAL
+    assert lib.fqa_schedule(null, null, 4, 1, 0, null, null, null, null) == _lib.FQA_EINVAL
+    assert lib.fqa_rope_tables(4, 127, 1e6, null, null) == _lib.FQA_EINVAL
+
+
+@pytest.mark.parametrize("name", ["fqa_pack", "fqa_decode", "fqa_prefill",
+                                  "fqa_qknorm_rope_append", "fqa_schedule"])
+def test_zero_work_is_ok(name):
+    """Zero-size calls are no-ops that succeed (the reference's launchers return early on
+    R <= 0 / n_decode <= 0, attn_cute.cu:155,247)."""
+    lib = _lib.load()
+    d = make_dims()
+    meta = (C.c_int32 * 16)()
+    if name == "fqa_decode":
+        rc = lib.fqa_decode(C.byref(d), None, None, 1, None, 1, None, None, meta, 0, 0, None,
+                            None, None)
+    elif name == "fqa_prefill":
+        rc = lib.fqa_prefill(C.byref(d), None, None, 1, None, 1, None, None, None, meta, 32, 0,
+                             None, None)
+    elif name == "fqa_qknorm_rope_append":
+        rc = lib.fqa_qknorm_rope_append(C.byref(d), None, None, None, None, None, 8, None, None,
+                                        meta, 0, None, 1, 0, None)
+    else:
+        pytest.skip("launches a kernel even for empty input (covered on the GPU)")
+    assert rc == _lib.FQA_OK

@@ -217,7 +217,8 @@ def test_schedule_gather_pack(gpu, seed):
     assert np.array_equal(step.b_bt_off.cpu().numpy()[: Rb + 1], sub.bt_off)
     assert np.array_equal(step.b_bt_pages.cpu().numpy()[: len(sub.bt_pages)], sub.bt_pages)
     kw = dict(max_rows=max_rows, max_blocks=sub.max_blocks, pool_pages=pool,
-              dec_grid_waves=128, dec_min_pages=4, dec_wave_cap=step.dec_wave_cap, pre_tile_q=64,
+              dec_grid_waves=128, dec_min_pages=4, dec_wave_cap=step.dec_wave_cap,
+              pre_tile_q=step.pre_tile_q,
               pre_item_cap=step.pre_cap)
     ref = orc.pack(sub.computed, sub.n_new, sub.bt_off, sub.bt_pages, **kw)
     ref["meta"][8] = Rb

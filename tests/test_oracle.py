@@ -1,0 +1,412 @@
+"""Pins the CPU oracle (oracle/fqa_oracle.c) before anything is checked against it.
+
+The reference ships no tests or golden vectors for this path (its only tests are Go
+text-tier tests), so each oracle function is pinned by library routines and closed forms
+chosen so that a plausible mistake (dropped term, wrong sign or index, transposed
+operand, off-by-one mask) fails:
+
+  bf16 rounding        torch's float32 -> bfloat16 cast (RNE)
+  RoPE tables          float64 cos/sin of the float32 angle; p = 0 gives cos 1, sin 0
+  RMSNorm + RoPE       torch fp64 rms_norm + rotate-half; p = 0 identity; constant input;
+                       pair-norm preservation; relative-position invariance of q.k
+  append               exact placement of k and raw v at the slot; nothing else written
+  attention            torch fp64 scaled_dot_product_attention (GQA, causal offset);
+                       single key -> V; identical keys -> mean(V); first causal row ->
+                       V[0]; page-permutation invariance (bit-exact)
+  pack / plans         an independent Python restatement (tests/pyref.py) on random
+                       batches, hand-built known answers, every status code
+  selection            the reference's greedy loop restated in Python; config 4's known
+                       batch (261 requests, 6464 rows)
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from flashqwen_amd import synth
+from flashqwen_amd.synth import HEAD_DIM, N_KV, N_Q, PAGE, QKV_STRIDE
+from oracle import oracle as orc
+from tests import pyref
+from tests import stepcase as sc
+
+F32 = np.float32
+
+
+def bf(x: np.ndarray) -> np.ndarray:
+    """float -> bf16 bits via torch (RNE) — the library routine the oracle must match."""
+    t = torch.from_numpy(np.ascontiguousarray(x, dtype=F32)).to(torch.bfloat16)
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+def f32(b: np.ndarray) -> np.ndarray:
+    return synth.bf16_to_f32(b)
+
+
+# ---------------------------------------------------------------------------------------
+def test_bf16_rounding_matches_torch():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(20000).astype(F32) * 10 ** rng.uniform(-40, 38, 20000).astype(F32),
+                        np.array([0.0, -0.0, np.inf, -np.inf, 1e-45, 3.0e38, 1.00390625, 1.01171875], F32)])
+    x = x[np.isfinite(x) | np.isinf(x)]
+    lib = orc.load()
+    got = np.array([lib.fqo_f32_to_bf16(float(v)) for v in x], np.uint16)
+    assert np.array_equal(got, bf(x))
+    # ties go to even
+    assert lib.fqo_f32_to_bf16(1.00390625) == 0x3F80
+    assert lib.fqo_f32_to_bf16(1.01171875) == 0x3F82
+
+
+def test_rope_tables():
+    cos, sin = orc.rope_tables(4096)
+    assert np.all(cos[0] == 1.0) and np.all(sin[0] == 0.0)
+    # fp64 truth of angle p * theta^(-2i/128): the tables compute the angle in float32,
+    # so they may differ by the float32 rounding of the angle (a few ulps of p * inv)
+    i = np.arange(64)
+    ang = np.arange(4096, dtype=np.float64)[:, None] * np.power(1e6, -2.0 * i / 128)[None, :]
+    tol = 4 * 2.0 ** -24 * np.maximum(ang, 1.0) + 2e-7
+    assert np.all(np.abs(cos - np.cos(ang)) <= tol)
+    assert np.all(np.abs(sin - np.sin(ang)) <= tol)
+    # a dropped factor 2 or a wrong sign in the exponent would be far outside tol
+    wrong = np.arange(4096.0)[:, None] * np.power(1e6, -1.0 * i / 128)[None, :]
+    assert np.abs(cos - np.cos(wrong)).max() > 0.1
+
+
+# ---------------------------------------------------------------------------------------
+def _norm_case(rows=12, seed=0, positions=None):
+    rng = np.random.default_rng(seed)
+    qkv = synth.rand_bf16(rng, (rows, QKV_STRIDE))
+    wq, wk = synth.norm_weights(seed + 1)
+    pos = np.arange(rows, dtype=np.int32) * 37 if positions is None else np.asarray(positions, np.int32)
+    pool_pages = 64
+    slots = (rng.permutation(pool_pages * PAGE)[:rows]).astype(np.int32)
+    pool = np.zeros(sc.pool_elems(pool_pages), np.uint16)
+    return qkv, wq, wk, pos, slots, pool, pool_pages
+
+
+def _torch_norm_rope(x_bits, w, pos, cos, sin):
+    x = torch.from_numpy(f32(x_bits).astype(np.float64))
+    wt = torch.from_numpy(w.astype(np.float64))
+    y = torch.nn.functional.rms_norm(x, (HEAD_DIM,), wt, eps=1e-6)
+    c = torch.from_numpy(cos[pos].astype(np.float64))
+    s = torch.from_numpy(sin[pos].astype(np.float64))
+    y1, y2 = y[..., :64], y[..., 64:]
+    return torch.cat([y1 * c - y2 * s, y2 * c + y1 * s], -1).numpy()
+
+
+def test_qknorm_rope_against_torch_fp64():
+    qkv, wq, wk, pos, slots, pool, pp = _norm_case()
+    cos, sin = orc.rope_tables(4096)
+    q = qkv.copy()
+    orc.qknorm_rope_append(q, wq, wk, cos, sin, pos, slots, len(pos), pool, pp)
+    for head in range(N_Q + N_KV):
+        w = wq if head < N_Q else wk
+        src = qkv[:, head * HEAD_DIM:(head + 1) * HEAD_DIM]
+        ref = _torch_norm_rope(src, w, pos[:, None].repeat(1, 0)[:, 0], cos, sin)
+        if head < N_Q:
+            got = f32(q[:, head * HEAD_DIM:(head + 1) * HEAD_DIM]).astype(np.float64)
+        else:
+            kvh = head - N_Q
+            pg, tk = slots // PAGE, slots % PAGE
+            got = np.stack([f32(pool[[orc.pool_offset(int(pg[t]), kvh, 0, int(tk[t]), d)
+                                      for d in range(HEAD_DIM)]]) for t in range(len(pos))])
+        # one bf16 rounding of the fp32 result + fp32 vs fp64 evaluation
+        assert np.all(np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref) + 2e-5), head
+
+
+def test_qknorm_rope_closed_forms():
+    cos, sin = orc.rope_tables(4096)
+    qkv, wq, wk, pos, slots, pool, pp = _norm_case(rows=4, positions=[0, 0, 0, 0])
+    # constant input: rms_norm(c * 1) = sign(c) (eps negligible), times w; pos 0 = identity
+    qkv[0, :] = bf(np.full(QKV_STRIDE, 2.5, F32))
+    qkv[1, :] = bf(np.full(QKV_STRIDE, -0.75, F32))
+    q = qkv.copy()
+    orc.qknorm_rope_append(q, wq, wk, cos, sin, pos, slots, 4, pool, pp)
+    assert np.array_equal(q[0, :HEAD_DIM], bf(wq))
+    assert np.array_equal(q[1, :HEAD_DIM], bf(-wq))
+    # pos 0 is the identity: output = bf16(x / rms * w)
+    x = f32(qkv[2, :HEAD_DIM]).astype(np.float64)
+    y = x / np.sqrt(np.mean(x * x) + 1e-6) * wq
+    assert np.all(np.abs(f32(q[2, :HEAD_DIM]) - y) <= 2.0 ** -8 * np.abs(y) + 1e-6)
+
+    # rotation: pair norms preserved, and q.k depends only on the position difference
+    qkv, wq, wk, _, slots, pool, pp = _norm_case(rows=4, seed=3)
+    qkv[2] = qkv[0]
+    qkv[3] = qkv[1]
+    pos = np.array([5, 3, 1005, 1003], np.int32)
+    q = qkv.copy()
+    orc.qknorm_rope_append(q, wq, wk, cos, sin, pos, slots, 4, pool, pp)
+    ref0 = orc.rope_tables(1)  # noqa: F841  (tables for p=0 are identity, checked above)
+    q0 = qkv.copy()
+    orc.qknorm_rope_append(q0, wq, wk, cos, sin, np.zeros(4, np.int32), slots, 4,
+                           np.zeros_like(pool), pp)
+    a, b = f32(q[:, :HEAD_DIM]).astype(np.float64), f32(q0[:, :HEAD_DIM]).astype(np.float64)
+    pn = lambda v: v[:, :64] ** 2 + v[:, 64:] ** 2  # noqa: E731
+    assert np.allclose(pn(a), pn(b), rtol=2e-2, atol=1e-3)
+    d1 = np.dot(a[0], a[1])
+    d2 = np.dot(a[2], a[3])
+    assert abs(d1 - d2) <= 2e-2 * (abs(d1) + 1.0)
+    assert abs(d1 - np.dot(b[0], b[1])) > 1e-3  # rotation is not a no-op
+
+
+def test_append_placement_and_bounds():
+    cos, sin = orc.rope_tables(64)
+    qkv, wq, wk, pos, slots, pool, pp = _norm_case(rows=5, positions=[1, 2, 3, 63, 64])
+    slots[2] = pp * PAGE + 3  # page out of range: nothing written for this row
+    q = qkv.copy()
+    orc.qknorm_rope_append(q, wq, wk, cos, sin, pos, slots, 5, pool, pp, write_k=True)
+    # row 4 has no table row (pos 64 >= 64): untouched
+    assert np.array_equal(q[4], qkv[4])
+    written = set()
+    for t in (0, 1, 3):
+        pg, tk = int(slots[t] // PAGE), int(slots[t] % PAGE)
+        for kvh in range(N_KV):
+            for d in range(HEAD_DIM):
+                ko = orc.pool_offset(pg, kvh, 0, tk, d)
+                vo = orc.pool_offset(pg, kvh, 1, tk, d)
+                assert pool[ko] == q[t, (N_Q + kvh) * HEAD_DIM + d]  # normed k (write_k)
+                assert pool[vo] == qkv[t, (N_Q + N_KV + kvh) * HEAD_DIM + d]  # raw v
+                written.update((ko, vo))
+    mask = np.ones(pool.size, bool)
+    mask[list(written)] = False
+    assert not pool[mask].any()
+
+
+# ---------------------------------------------------------------------------------------
+def _attn_case(seed, lens, computed, pool_pages=128, perm_seed=None):
+    """Random q/pool for requests with given new rows (lens) and cached prefixes."""
+    rng = np.random.default_rng(seed)
+    tables = []
+    perm = np.random.default_rng(perm_seed if perm_seed is not None else seed).permutation(pool_pages)
+    o = 0
+    for n, c in zip(lens, computed):
+        k = synth.cdiv(n + c, PAGE)
+        tables.append(perm[o:o + k].astype(np.int32))
+        o += k
+    cfg = synth._assemble("t", computed, lens, tables, pool_pages, 4096)
+    T = cfg.rows
+    qkv = synth.rand_bf16(rng, (T, QKV_STRIDE))
+    pool = synth.rand_bf16(np.random.default_rng(seed + 1000), sc.pool_elems(pool_pages))
+    kw = sc.pack_kwargs(cfg)
+    pk = orc.pack(cfg.computed, cfg.n_new, cfg.bt_off, cfg.bt_pages, **kw)
+    return cfg, qkv, pool, pk, kw
+
+
+def _run_attn(cfg, qkv, pool, pk, kw):
+    T = cfg.rows
+    out = np.zeros((T, N_Q * HEAD_DIM), np.uint16)
+    orc.decode(qkv, pool, cfg.pool_pages, pk["block_tables"], kw["max_blocks"], pk["cu_seqlens"],
+               pk["positions"], pk["decode_rids"], int(pk["meta"][1]), out)
+    orc.prefill(qkv, pool, cfg.pool_pages, pk["block_tables"], kw["max_blocks"],
+                pk["cu_seqlens"], pk["positions"], pk["prefill_rids"], int(pk["meta"][2]), out)
+    return out
+
+
+def _logical_kv(cfg, pool, r, nkeys):
+    """[nkeys, 8, 128] K and V of request r read through its block table."""
+    K = np.zeros((nkeys, N_KV, HEAD_DIM))
+    V = np.zeros_like(K)
+    t = cfg.tables()[r]
+    d = np.arange(HEAD_DIM)
+    for kp in range(nkeys):
+        pg, tk = int(t[kp // PAGE]), kp % PAGE
+        for kvh in range(N_KV):
+            base = ((pg * N_KV + kvh) * 2) * PAGE * HEAD_DIM
+            K[kp, kvh] = f32(pool[base + tk * HEAD_DIM + d])
+            V[kp, kvh] = f32(pool[base + PAGE * HEAD_DIM + d * PAGE + tk])
+    return K, V
+
+
+@pytest.mark.parametrize("lens,computed", [([1, 1, 1], [0, 40, 300]), ([37, 1, 20], [0, 90, 50])])
+def test_attention_against_torch_sdpa(lens, computed):
+    cfg, qkv, pool, pk, kw = _attn_case(7, lens, computed)
+    out = _run_attn(cfg, qkv, pool, pk, kw)
+    for r, (n, c) in enumerate(zip(lens, computed)):
+        K, V = _logical_kv(cfg, pool, r, n + c)
+        q0 = pk["cu_seqlens"][r]
+        Q = f32(qkv[q0:q0 + n, :N_Q * HEAD_DIM]).reshape(n, N_Q, HEAD_DIM).astype(np.float64)
+        Qt = torch.from_numpy(Q).transpose(0, 1)  # [H, n, D]
+        Kt = torch.from_numpy(K).transpose(0, 1).repeat_interleave(4, 0)  # GQA: h -> h//4
+        Vt = torch.from_numpy(V).transpose(0, 1).repeat_interleave(4, 0)
+        mask = torch.arange(n + c)[None, :] <= (c + torch.arange(n))[:, None]
+        ref = torch.nn.functional.scaled_dot_product_attention(Qt, Kt, Vt, attn_mask=mask)
+        ref = ref.transpose(0, 1).reshape(n, -1).numpy()
+        got = f32(out[q0:q0 + n]).astype(np.float64)
+        assert np.abs(got - ref).max() <= 2e-2
+        assert np.abs(got - ref).mean() <= 2e-3
+
+
+def test_attention_closed_forms():
+    # single key: decode at context 1 returns V[0] exactly; first row of a fresh prompt too
+    cfg, qkv, pool, pk, kw = _attn_case(3, [1, 9], [0, 0])
+    out = _run_attn(cfg, qkv, pool, pk, kw)
+    for r in range(2):
+        K, V = _logical_kv(cfg, pool, r, 1)
+        row = pk["cu_seqlens"][r]
+        want = bf(np.repeat(V[0], 4, axis=0).reshape(-1).astype(F32))
+        assert np.array_equal(out[row], want)
+    # identical keys: softmax is uniform, output = mean of V
+    cfg, qkv, pool, pk, kw = _attn_case(4, [1], [40])
+    t = cfg.tables()[0]
+    k_src = pool[((int(t[0]) * N_KV) * 2) * PAGE * HEAD_DIM:][:HEAD_DIM].copy()
+    for kp in range(41):
+        pg, tk = int(t[kp // PAGE]), kp % PAGE
+        for kvh in range(N_KV):
+            base = ((pg * N_KV + kvh) * 2) * PAGE * HEAD_DIM
+            pool[base + tk * HEAD_DIM: base + (tk + 1) * HEAD_DIM] = k_src
+    out = _run_attn(cfg, qkv, pool, pk, kw)
+    K, V = _logical_kv(cfg, pool, 0, 41)
+    want = np.repeat(V.mean(0), 4, axis=0).reshape(-1)
+    assert np.abs(f32(out[0]) - want).max() <= 2.0 ** -7 * np.abs(want).max() + 1e-6
+
+
+def test_attention_page_permutation_invariance():
+    lens, comp = [1, 23, 1], [77, 10, 5]
+    a = _attn_case(9, lens, comp, perm_seed=1)
+    b = _attn_case(9, lens, comp, perm_seed=2)
+    # same logical K/V in both pools: copy a's pages into b's placement
+    cfg_a, qkv, pool_a, pk_a, kw = a
+    cfg_b, _, pool_b, pk_b, _ = b
+    run = 2 * N_KV * PAGE * HEAD_DIM
+    for ta, tb in zip(cfg_a.tables(), cfg_b.tables()):
+        for pa, pb in zip(ta, tb):
+            pool_b[int(pb) * run:(int(pb) + 1) * run] = pool_a[int(pa) * run:(int(pa) + 1) * run]
+    oa = _run_attn(cfg_a, qkv, pool_a, pk_a, kw)
+    ob = _run_attn(cfg_b, qkv, pool_b, pk_b, kw)
+    assert np.array_equal(oa, ob)
+
+
+# ---------------------------------------------------------------------------------------
+def _kw(R, max_rows=4096, **over):
+    kw = dict(max_rows=max_rows, max_blocks=256, pool_pages=4096, dec_grid_waves=64,
+              dec_min_pages=2, dec_wave_cap=64, pre_tile_q=32, pre_item_cap=max_rows // 32 + R)
+    kw.update(over)
+    return kw
+
+
+def _compare_pack(comp, nnew, tabs, kw):
+    cfg = synth._assemble("p", comp, nnew, tabs, kw["pool_pages"], 4096)
+    got = orc.pack(cfg.computed, cfg.n_new, cfg.bt_off, cfg.bt_pages, **kw)
+    ref = pyref.pack(list(comp), list(nnew), [list(t) for t in tabs], **kw)
+    assert list(got["meta"]) == ref["meta"]
+    if ref["meta"][7] not in (0, 4):
+        return got, ref
+    R, T = len(comp), ref["meta"][0]
+    assert list(got["cu_seqlens"][:R + 1]) == ref["cu_seqlens"]
+    for k in ("positions", "row_req", "slot_mapping"):
+        assert list(got[k][:T]) == ref[k], k
+    for k in ("decode_rids", "prefill_rids", "qlen"):
+        assert list(got[k][:R]) == list(ref[k]), k
+    assert list(got["block_tables"][:R * kw["max_blocks"]]) == ref["block_tables"]
+    nd, G, npi = ref["meta"][1], ref["meta"][4], ref["meta"][5]
+    assert got["dec_seqs"][:nd].tolist() == ref["dec_seqs"]
+    assert got["dec_waves"][:G].tolist() == ref["dec_waves"]
+    assert got["pre_items"][:npi].tolist() == ref["pre_items"]
+    return got, ref
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_pack_against_python_restatement(seed):
+    from tests.test_gpu_pack import rand_batch
+
+    rng = np.random.default_rng(seed)
+    R = int(rng.choice([0, 1, 5, 40, 200]))
+    comp, nnew, tabs = rand_batch(rng, R, share=True)
+    kw = _kw(R, max_rows=max(1, int(np.sum(nnew)) if R else 1),
+             dec_grid_waves=int(rng.choice([1, 3, 64, 2048])),
+             dec_min_pages=int(rng.choice([0, 1, 8])), pre_tile_q=int(rng.choice([32, 64, 128])))
+    kw["dec_wave_cap"] = kw["dec_grid_waves"]
+    kw["pre_item_cap"] = kw["max_rows"] // kw["pre_tile_q"] + R
+    _compare_pack(comp, nnew, tabs, kw)
+
+
+def test_pack_known_answer():
+    # request 0: decode at context 18 (pages 5,9); request 1: 3-row chunk on a 15-token
+    # prefix (pages 2,7); request 2: 1-token fresh prompt = a decode; request 3: n = 0
+    comp, nnew = [17, 15, 0, 4], [1, 3, 1, 0]
+    tabs = [[5, 9], [2, 7], [11], [4]]
+    kw = _kw(4, max_rows=8, max_blocks=3, dec_grid_waves=5, dec_min_pages=1, dec_wave_cap=5,
+             pre_tile_q=32, pre_item_cap=4)
+    got, _ = _compare_pack(comp, nnew, tabs, kw)
+    assert got["cu_seqlens"][:5].tolist() == [0, 1, 4, 5, 5]
+    assert got["positions"][:5].tolist() == [17, 15, 16, 17, 0]
+    assert got["row_req"][:5].tolist() == [0, 1, 1, 1, 2]
+    assert got["slot_mapping"][:5].tolist() == [9 * 16 + 1, 2 * 16 + 15, 7 * 16 + 0, 7 * 16 + 1,
+                                                11 * 16]
+    assert got["block_tables"][:12].tolist() == [5, 9, -1, 2, 7, -1, 11, -1, -1, 4, -1, -1]
+    assert got["decode_rids"][:4].tolist() == [0, 2, -1, -1]
+    assert got["prefill_rids"][:4].tolist() == [1, 3, -1, -1]
+    assert got["meta"][:10].tolist() == [5, 2, 2, 3, 5, 1, 5, 0, 4, 3]
+    # W = 8*(2+1) = 24 page runs over 5 waves: shares 4,5,5,5,5
+    assert got["dec_seqs"][:2].tolist() == [[0, 0, 18, 0], [2, 4, 1, 16]]
+    assert got["dec_waves"][:5].tolist() == [[0, 0, 0, 4], [0, 2, 0, 5], [0, 4, 1, 5],
+                                             [0, 7, 0, 5], [1, 3, 0, 5]]
+    assert got["pre_items"][:1].tolist() == [[1, 0, 3, 18]]
+
+
+@pytest.mark.parametrize("case,code", [("short", 1), ("wide", 2), ("rows", 3), ("page", 4),
+                                       ("negative", 5), ("items", 6)])
+def test_pack_status_codes(case, code):
+    comp, nnew, tabs = [10, 0], [1, 40], [[1], [2, 3, 4]]
+    kw = _kw(2, max_rows=64, max_blocks=8)
+    if case == "short":
+        tabs[1] = [2, 3]
+    elif case == "wide":
+        tabs[0] = list(range(9))
+    elif case == "rows":
+        kw["max_rows"] = 20
+    elif case == "page":
+        tabs[1] = [2, 5000, 4]
+    elif case == "negative":
+        nnew[0] = -1
+    elif case == "items":
+        kw["dec_wave_cap"] = 0
+    got, ref = _compare_pack(comp, nnew, tabs, kw)
+    assert got["status"] == code
+
+
+def test_dec_waves_cover_every_run_once():
+    rng = np.random.default_rng(5)
+    comp = list(rng.integers(0, 3000, 37))
+    tabs = [list(range(c // 16 + 1)) for c in comp]
+    kw = _kw(37, max_rows=37, dec_grid_waves=61, dec_min_pages=1, dec_wave_cap=61)
+    got = orc.pack(comp, [1] * 37, synth._assemble("x", comp, [1] * 37, [np.array(t) for t in tabs], 4096, 4096).bt_off,
+                   np.concatenate(tabs), **kw)
+    seen = []
+    for di, kvh, page, n in got["dec_waves"][: got["meta"][4]]:
+        while n > 0:
+            pages = comp[got["dec_seqs"][di][0]] // 16 + 1
+            take = min(n, pages - page)
+            seen += [(di, kvh, p) for p in range(page, page + take)]
+            n -= take
+            page = 0
+            kvh += 1
+            if kvh == 8:
+                kvh, di = 0, di + 1
+    expect = [(di, kvh, p) for di in range(37) for kvh in range(8) for p in range(comp[di] // 16 + 1)]
+    assert seen == expect
+
+
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("seed", range(6))
+def test_schedule_against_python_restatement(seed):
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(0, 300))
+    comp = rng.integers(0, 3000, n).astype(np.int32)
+    rem = np.where(rng.random(n) < 0.5, rng.integers(-2, 2, n), rng.integers(2, 900, n))
+    ntok = (comp + rem).astype(np.int32)
+    budget = int(rng.choice([-5, 0, 1, 512, 8192]))
+    chunk = int(rng.choice([1, 64, 2048]))
+    req, nn = orc.schedule(ntok, comp, budget, chunk)
+    ref = pyref.build_batch(ntok.tolist(), comp.tolist(), budget, chunk)
+    assert list(zip(req.tolist(), nn.tolist())) == ref
+
+
+def test_schedule_config4_known_batch():
+    cfg = synth.config4()
+    req, nn = orc.schedule(cfg.num_tokens, cfg.computed, cfg.token_budget, cfg.prefill_chunk)
+    assert len(req) == 261 and int(nn.sum()) == 6464
+    rem = cfg.num_tokens[req] - cfg.computed[req]
+    assert list(nn[:256]) == [1] * 256  # decodes first
+    assert sorted(nn[256:259].tolist()) == [512, 700, 900]
+    assert nn[259:].tolist() == [2048, 2048] and list(rem[259:]) == [4096, 4096]
