@@ -212,7 +212,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   if (tid == 0) s_btoff[R] = a.b.bt_off[R];
   st = block_reduce_stats(st, s_stats);
   int code = st.v[0];
-  const int rows = st.v[1], dpages = st.v[2], dmax = st.v[3], qmax = st.v[4];
+  const int rows = st.v[1], dpages = st.v[2], qmax = st.v[4];
   if (rows > a.c.max_rows && code > FQA_PACK_ROWS) code = FQA_PACK_ROWS;
   if (code != INT_MAX) {
     if (blockIdx.x == 0 && tid < FQA_META_LEN)

@@ -4,23 +4,27 @@
 // StoreKvKernel (engine/src/kv_store.cu:48-75), which the reference runs as two
 // launches with one 128-thread block per (row, head) and one bf16 element per thread.
 //
-// Here one 16-lane group owns one head of one row: lane j holds dims [4j, 4j+4) and
-// [64+4j, 64+4j+4), so both halves of every rotate-half pair sit in the same lane and
-// RoPE needs no data exchange; the sum of squares is a 16-lane butterfly.  A 256-thread
-// workgroup covers 16 heads, three workgroups cover one row's 32 q + 8 k + 8 v heads.
+// W = 10/HPG wavefronts per row (HPG = heads per 16-lane group, a template parameter the
+// host picks from the row count: few rows want many waves, many rows want each wave to
+// amortise its load latency over more heads).  The 4 16-lane groups of wave s take heads
+// g + 4*(s*HPG + i), i < HPG, with every load issued before any math and cos/sin and the
+// norm weights loaded once: lane j holds dims [4j, 4j+4) and [64+4j, 64+4j+4), so both
+// halves of every rotate-half pair sit in one lane and RoPE needs no data exchange; the
+// sum of squares is a 16-lane butterfly.  q is written back in place, k into its page.
+// The row's 8 v heads are split over the W waves and copied into the V^T
+// [dim][16 tokens] rows of the page.  Those are 2-byte writes, so the 16 rows of a page
+// must meet in one L2 before the line goes to HBM: workgroup b runs on XCD b % 8, and
+// rows are dealt to XCDs in contiguous ranges, so a page's rows (except where a range
+// ends) go through the same XCD's L2.  (Dealing rows round-robin spread each page over
+// all 8 L2s and more than doubled the bytes written to HBM.)
 // Memory-bound: per row 12 KiB read, 8 KiB (q) + 4 KiB (k, v) written.
 //
-// Semantics (kernels.cu:113-129): y = x * rsqrt(mean(x^2) + eps) * w in fp32, then
-// y1' = y1*cos - y2*sin, y2' = y2*cos + y1*sin with no intermediate bf16 rounding,
-// one RNE rounding to bf16 at the end.  V is copied unchanged.
 #include "fqa_common.h"
 
 namespace fqa {
 namespace {
 
-constexpr int kHeadsPerRow = kHq + 2 * kHkv;  // 48
-constexpr int kHeadsPerBlock = 16;
-constexpr int kBlocksPerRow = kHeadsPerRow / kHeadsPerBlock;  // 3
+constexpr int kWavesPerBlock = 4;
 
 struct AppendArgs {
   uint16_t* qkv;
@@ -37,6 +41,7 @@ struct AppendArgs {
   int stride;
   float eps;
   int write_k;
+  int blocks_per_xcd;
 };
 
 __device__ __forceinline__ void unpack4(uint2 v, float* f) {
@@ -46,74 +51,92 @@ __device__ __forceinline__ void unpack4(uint2 v, float* f) {
   f[3] = __uint_as_float(v.y & 0xffff0000u);
 }
 
+template <int HPG>
 __global__ void __launch_bounds__(256) qknorm_rope_append_kernel(AppendArgs a) {
-  const int row = blockIdx.x / kBlocksPerRow;
-  if (row >= a.meta[FQA_META_ROWS]) return;
-  const int head = (blockIdx.x % kBlocksPerRow) * kHeadsPerBlock + (threadIdx.x >> 4);
-  const int j = threadIdx.x & 15;
-
+  constexpr int W = 10 / HPG;                  // waves per row
+  constexpr int NKV = (kHkv + W - 1) / W;      // v heads per wave
+  const int T = a.meta[FQA_META_ROWS];
+  const int b = blockIdx.x;
+  const int wid = ((b & 7) * a.blocks_per_xcd + (b >> 3)) * kWavesPerBlock + (threadIdx.x >> 6);
+  const int row = wid / W, sw = wid % W;
+  if (row >= T) return;
   const int pos = a.positions[row];
-  if (pos < 0 || pos >= a.rope_max_pos) return;
-  uint16_t* src = a.qkv + (long long)row * a.stride + head * kD;
-  uint2 lo = *reinterpret_cast<const uint2*>(src + 4 * j);
-  uint2 hi = *reinterpret_cast<const uint2*>(src + 64 + 4 * j);
-
+  if (pos < 0 || pos >= a.rope_max_pos) return;  // no table row: leave the row untouched
   const int slot = a.slots[row];
   const long long page = slot / kPage;
-  const int tok = slot % kPage;
   const bool page_ok = slot >= 0 && page < a.pool_pages;
+  const int tok = slot % kPage;
+  const int lane = threadIdx.x & 63, g = lane >> 4, j = lane & 15;
+  uint16_t* src = a.qkv + (long long)row * a.stride;
 
-  if (head >= kHq + kHkv) {  // v head: copy into V^T [d][16 tokens]
-    if (!page_ok) return;
-    const int kvh = head - kHq - kHkv;
-    uint16_t* vt = a.pool + run_offset(page, kvh) + kVOff + tok;
-    const uint16_t l4[4] = {(uint16_t)lo.x, (uint16_t)(lo.x >> 16), (uint16_t)lo.y,
-                            (uint16_t)(lo.y >> 16)};
-    const uint16_t h4[4] = {(uint16_t)hi.x, (uint16_t)(hi.x >> 16), (uint16_t)hi.y,
-                            (uint16_t)(hi.y >> 16)};
+  // ---- q/k heads g + 4*(sw*HPG + i) ----------------------------------------------------
+  uint2 lo[HPG], hi[HPG];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      vt[(4 * j + i) * kPage] = l4[i];
-      vt[(64 + 4 * j + i) * kPage] = h4[i];
-    }
-    return;
+  for (int i = 0; i < HPG; ++i) {
+    const uint16_t* hs = src + (g + 4 * (sw * HPG + i)) * kD;
+    lo[i] = *reinterpret_cast<const uint2*>(hs + 4 * j);
+    hi[i] = *reinterpret_cast<const uint2*>(hs + 64 + 4 * j);
   }
-
-  float x1[4], x2[4];
-  unpack4(lo, x1);
-  unpack4(hi, x2);
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
-#pragma unroll
-  for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, kWave);
-  const float inv = 1.0f / sqrtf(ss / (float)kD + a.eps);
-
-  const float* w = head < kHq ? a.wq : a.wk;
-  const float4 w1 = *reinterpret_cast<const float4*>(w + 4 * j);
-  const float4 w2 = *reinterpret_cast<const float4*>(w + 64 + 4 * j);
   const float4 c4 = *reinterpret_cast<const float4*>(a.cos_tab + (long long)pos * 64 + 4 * j);
   const float4 s4 = *reinterpret_cast<const float4*>(a.sin_tab + (long long)pos * 64 + 4 * j);
-  const float wa[4] = {w1.x, w1.y, w1.z, w1.w}, wb[4] = {w2.x, w2.y, w2.z, w2.w};
+  const float4 q1 = *reinterpret_cast<const float4*>(a.wq + 4 * j);
+  const float4 q2 = *reinterpret_cast<const float4*>(a.wq + 64 + 4 * j);
+  const float4 k1 = *reinterpret_cast<const float4*>(a.wk + 4 * j);
+  const float4 k2 = *reinterpret_cast<const float4*>(a.wk + 64 + 4 * j);
   const float cs[4] = {c4.x, c4.y, c4.z, c4.w}, sn[4] = {s4.x, s4.y, s4.z, s4.w};
-  float o1[4], o2[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float y1 = x1[i] * inv * wa[i];
-    float y2 = x2[i] * inv * wb[i];
-    o1[i] = y1 * cs[i] - y2 * sn[i];
-    o2[i] = y2 * cs[i] + y1 * sn[i];
+  for (int i = 0; i < HPG; ++i) {
+    const int head = g + 4 * (sw * HPG + i);
+    const bool is_k = head >= kHq;  // heads 32..39: only i >= 8
+    float x1[4], x2[4];
+    unpack4(lo[i], x1);
+    unpack4(hi[i], x2);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ss += x1[e] * x1[e] + x2[e] * x2[e];
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, kWave);
+    const float inv = 1.0f / sqrtf(ss / (float)kD + a.eps);
+    const float wa[4] = {is_k ? k1.x : q1.x, is_k ? k1.y : q1.y, is_k ? k1.z : q1.z,
+                         is_k ? k1.w : q1.w};
+    const float wb[4] = {is_k ? k2.x : q2.x, is_k ? k2.y : q2.y, is_k ? k2.z : q2.z,
+                         is_k ? k2.w : q2.w};
+    float o1[4], o2[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float y1 = x1[e] * inv * wa[e];
+      const float y2 = x2[e] * inv * wb[e];
+      o1[e] = y1 * cs[e] - y2 * sn[e];
+      o2[e] = y2 * cs[e] + y1 * sn[e];
+    }
+    const uint2 olo = make_uint2(pack_bf16x2(o1[0], o1[1]), pack_bf16x2(o1[2], o1[3]));
+    const uint2 ohi = make_uint2(pack_bf16x2(o2[0], o2[1]), pack_bf16x2(o2[2], o2[3]));
+    uint16_t* hs = src + head * kD;
+    if (!is_k || a.write_k) {
+      *reinterpret_cast<uint2*>(hs + 4 * j) = olo;
+      *reinterpret_cast<uint2*>(hs + 64 + 4 * j) = ohi;
+    }
+    if (is_k && page_ok) {  // K [16 tokens][128] of the row's page
+      uint16_t* kd = a.pool + run_offset(page, head - kHq) + tok * kD;
+      *reinterpret_cast<uint2*>(kd + 4 * j) = olo;
+      *reinterpret_cast<uint2*>(kd + 64 + 4 * j) = ohi;
+    }
   }
-  uint2 olo = make_uint2(pack_bf16x2(o1[0], o1[1]), pack_bf16x2(o1[2], o1[3]));
-  uint2 ohi = make_uint2(pack_bf16x2(o2[0], o2[1]), pack_bf16x2(o2[2], o2[3]));
-  if (head < kHq || a.write_k) {
-    *reinterpret_cast<uint2*>(src + 4 * j) = olo;
-    *reinterpret_cast<uint2*>(src + 64 + 4 * j) = ohi;
-  }
-  if (head >= kHq && page_ok) {  // k head: K [16 tokens][128]
-    uint16_t* kd = a.pool + run_offset(page, head - kHq) + tok * kD;
-    *reinterpret_cast<uint2*>(kd + 4 * j) = olo;
-    *reinterpret_cast<uint2*>(kd + 64 + 4 * j) = ohi;
+
+  // ---- v heads sw*NKV .. : lane -> (kv head, DPL consecutive dims) --------------------
+  constexpr int LPK = kWave / NKV;   // lanes per v head
+  constexpr int DPL = kD / LPK;      // dims per lane (2, 4 or 16)
+  const int kvh = sw * NKV + lane / LPK, d0 = (lane % LPK) * DPL;
+  if (!page_ok || kvh >= kHkv) return;
+  const uint16_t* vs = src + (kHq + kHkv + kvh) * kD + d0;
+  uint32_t wv[DPL / 2];
+#pragma unroll
+  for (int e = 0; e < DPL / 2; ++e) wv[e] = reinterpret_cast<const uint32_t*>(vs)[e];
+  uint16_t* vt = a.pool + run_offset(page, kvh) + kVOff + d0 * kPage + tok;
+#pragma unroll
+  for (int e = 0; e < DPL / 2; ++e) {
+    vt[(2 * e) * kPage] = (uint16_t)wv[e];
+    vt[(2 * e + 1) * kPage] = (uint16_t)(wv[e] >> 16);
   }
 }
 
@@ -141,9 +164,21 @@ extern "C" int fqa_qknorm_rope_append(const fqa_dims* dims, uint16_t* qkv, const
   if (!qkv || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !positions || !slot_mapping ||
       !pool)
     return FQA_EINVAL;
-  AppendArgs a{qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, rope_max_pos, positions, slot_mapping, meta, pool,
-               pool_pages, dims->qkv_stride, dims->eps, write_k_inplace};
-  hipLaunchKernelGGL(qknorm_rope_append_kernel, dim3(rows_bound * kBlocksPerRow), dim3(256), 0,
-                     (hipStream_t)stream, a);
+  // Heads per lane group: 1 (10 waves per row) for decode-sized steps, 10 (one wave per
+  // row) for prefill-sized ones; measured crossover between.
+  const int hpg = rows_bound <= 512 ? 1 : (rows_bound <= 2048 ? 2 : 10);
+  const long long waves = (long long)rows_bound * (10 / hpg);
+  const int blocks = (int)((waves + kWavesPerBlock - 1) / kWavesPerBlock);
+  const int blocks_per_xcd = (blocks + 7) / 8;
+  AppendArgs a{qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, rope_max_pos, positions, slot_mapping,
+               meta, pool, pool_pages, dims->qkv_stride, dims->eps, write_k_inplace,
+               blocks_per_xcd};
+  const dim3 grid(8 * blocks_per_xcd), block(256);
+  if (hpg == 1)
+    hipLaunchKernelGGL(qknorm_rope_append_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
+  else if (hpg == 2)
+    hipLaunchKernelGGL(qknorm_rope_append_kernel<2>, grid, block, 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(qknorm_rope_append_kernel<10>, grid, block, 0, (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
 }
