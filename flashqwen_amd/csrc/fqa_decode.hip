@@ -99,14 +99,13 @@ __device__ __forceinline__ void process_page(PageFrag& f, const bf16x8 (&qf)[4],
       for (int j = 0; j < 4; ++j)
         if (key0 + j >= L) f.v[b][j] = 0;
   }
-  mx = wave_max_xor(mx, 16);
-  mx = wave_max_xor(mx, 32);
+  mx = max_xor32(max_xor16(mx));
   const float m_new = fmaxf(st.m, mx);
-  const float corr = exp2f(st.m - m_new);
+  const float corr = __builtin_amdgcn_exp2f(st.m - m_new);
   float pj[4], psum = 0.f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    pj[j] = exp2f(sv[j] - m_new);
+    pj[j] = __builtin_amdgcn_exp2f(sv[j] - m_new);
     psum += pj[j];
   }
   st.l = st.l * corr + psum;
@@ -188,9 +187,7 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
     st.m = -1e30f;
     st.l = 0.f;
     stream_pages(a, a.bt + (long long)r * a.max_blocks, kvh, page, page + cnt, L, qf, lane, st);
-    float l_run = st.l;
-    l_run += __shfl_xor(l_run, 16, kWave);
-    l_run += __shfl_xor(l_run, 32, kWave);
+    const float l_run = sum_rows4(st.l);
 
     if (n < kG) {
       if (page == 0 && cnt == pages) {  // whole stream: final output
@@ -241,19 +238,32 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_combine_kern
   const int lane = threadIdx.x & 63;
   const int h = lane >> 4, d0 = (lane & 15) * 8;
   float gm = -1e30f, gl = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (long long w = wf; w <= wl; ++w) {
-    const long long sl = (w == wf && wf * W / G != S0) ? 2 * w + 1 : 2 * w;
-    const long long slot = sl * kG + h;
-    const float m = a.ws_m[slot], l = a.ws_l[slot];
-    const float4* src = reinterpret_cast<const float4*>(a.ws_acc + slot * kD + d0);
-    const float4 x0 = src[0], x1 = src[1];
-    const float mn = fmaxf(gm, m);
-    const float co = exp2f(gm - mn), cn = exp2f(m - mn);
-    gl = gl * co + l * cn;
-    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+  // partials in batches of 4: all loads of a batch are issued before any is used
+  for (long long w0 = wf; w0 <= wl; w0 += 4) {
+    float m[4], l[4];
+    float4 x0[4], x1[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = acc[i] * co + xs[i] * cn;
-    gm = mn;
+    for (int k = 0; k < 4; ++k) {
+      const long long w = w0 + k;
+      const long long sl = (w == wf && wf * W / G != S0) ? 2 * w + 1 : 2 * w;
+      const long long slot = (w <= wl ? sl : 2 * wf) * kG + h;  // beyond wl: harmless reread
+      m[k] = a.ws_m[slot];
+      l[k] = a.ws_l[slot];
+      const float4* src = reinterpret_cast<const float4*>(a.ws_acc + slot * kD + d0);
+      x0[k] = src[0];
+      x1[k] = src[1];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (w0 + k > wl) break;
+      const float mn = fmaxf(gm, m[k]);
+      const float co = exp2f(gm - mn), cn = exp2f(m[k] - mn);
+      gl = gl * co + l[k] * cn;
+      const float xs[8] = {x0[k].x, x0[k].y, x0[k].z, x0[k].w, x1[k].x, x1[k].y, x1[k].z, x1[k].w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = acc[i] * co + xs[i] * cn;
+      gm = mn;
+    }
   }
   const float inv = gl > 0.f ? 1.0f / gl : 0.f;
   uint4 v = make_uint4(pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv),

@@ -121,7 +121,36 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PreArgs a) {
   // 2j + t/128, dim t%128.
   uint4 sk[4];
   uint4 sv[2][2];
+  // Fast path: every page of the tile is full and in range (all but a workgroup's last
+  // tile, checked on scalar registers): plain loads, no masks.  Otherwise each page is
+  // loaded only if it exists and is in range, and tokens past n_keys are zeroed (their
+  // P is 0, and 0 x garbage must not become NaN in PV).
   auto stage_load = [&](int kb) {
+    long long pg[kPagesPerTile];
+    bool fast = (kb + 1) * kKT <= nkeys;
+#pragma unroll
+    for (int ps = 0; ps < kPagesPerTile; ++ps) {
+      pg[ps] = fast ? btr[kb * kPagesPerTile + ps] : -1;
+      fast = fast && pg[ps] >= 0 && pg[ps] < a.pool_pages;
+    }
+    if (fast) {
+#pragma unroll
+      for (int ps = 0; ps < kPagesPerTile; ++ps) {
+        const uint16_t* run = a.pool + run_offset(pg[ps], kvh);
+        sk[ps] = *reinterpret_cast<const uint4*>(run + tid * 8);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int d = tid & 127;
+        const uint16_t* src = a.pool + run_offset(pg[2 * j + (tid >> 7)], kvh) + kVOff + d * kPage;
+        const uint4 lo = *reinterpret_cast<const uint4*>(src);
+        const uint4 hi = *reinterpret_cast<const uint4*>(src + 8);
+        // chunk 0 = tokens {0-3, 8-11}, chunk 1 = tokens {4-7, 12-15}
+        sv[j][0] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        sv[j][1] = make_uint4(lo.z, lo.w, hi.z, hi.w);
+      }
+      return;
+    }
 #pragma unroll
     for (int ps = 0; ps < kPagesPerTile; ++ps) {
       const int pidx = kb * kPagesPerTile + ps;
@@ -147,7 +176,6 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PreArgs a) {
           lo = make_uint4(a0.x, a0.y, a1.x, a1.y);
           hi = make_uint4(b0.x, b0.y, b1.x, b1.y);
         }
-        // chunk 0 = tokens {0-3, 8-11}, chunk 1 = tokens {4-7, 12-15}
         sv[j][0] = make_uint4(lo.x, lo.y, hi.x, hi.y);
         sv[j][1] = make_uint4(lo.z, lo.w, hi.z, hi.w);
       }
@@ -204,23 +232,25 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PreArgs a) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[v]);
       }
-      mx = wave_max_xor(mx, 32);
+      mx = max_xor32(mx);
       // Lazy rescale: the reference max only moves when the row max grows by more than
       // 2^kRescale, so P = exp2(s*scale - m) stays <= 2^kRescale and O, l are rescaled
       // on few tiles instead of every tile.
       const float m_new = fmaxf(m_run, mx * a.scale_log2);
-      if (m_new > m_run + kRescale) {
-        const float corr = exp2f(m_run - m_new);
+      const bool grow = m_new > m_run + kRescale;
+      if (__builtin_amdgcn_ballot_w64(grow)) {  // wave-uniform: skipped on most tiles
+        const float corr = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
         l_run *= corr;
 #pragma unroll
         for (int db = 0; db < 4; ++db) o[db] *= corr;
-        m_run = m_new;
+        m_run = grow ? m_new : m_run;
       }
       bf16x8 pt[2];
       float psum = 0.f;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const float p = exp2f(fmaf(s[v], a.scale_log2, -m_run));
+        // raw v_exp_f32: results below 2^-126 flush to 0, which a softmax weight can be
+        const float p = __builtin_amdgcn_exp2f(fmaf(s[v], a.scale_log2, -m_run));
         psum += p;
         pt[v >> 3][v & 7] = (__bf16)p;
       }
@@ -242,7 +272,9 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PreArgs a) {
   }
 
   if (!row_ok) return;
-  const float l = l_run + __shfl_xor(l_run, 32, kWave);
+  const auto lr = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run),
+                                                   false, false);
+  const float l = __uint_as_float(lr[0]) + __uint_as_float(lr[1]);
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   uint16_t* dst = a.out + (long long)(qs + i_row) * (kHq * kD) + h * kD + hf * 4;
 #pragma unroll
