@@ -21,8 +21,8 @@
 //    (the key order inside the contraction is chosen to match, V^T is read to suit).
 //  * Softmax VALU work per score, not MFMA, is the limit on CDNA (a wave64 VALU op
 //    issues in 4 cycles, exp in more): scores are maxed raw, scaled inside the exp2
-//    FMA, converted with v_cvt_pk_bf16_f32, and O is rescaled lazily (only when the
-//    row max grows by more than 2^8).
+//    FMA, converted with v_cvt_pk_bf16_f32, summed two at a time with v_dot2 against
+//    (1, 1), and O is rescaled lazily (only when the row max grows by more than 2^8).
 //  * K/V tiles are 64 keys = 4 pages = four contiguous 8 KiB runs, double-buffered in
 //    LDS (2 x 32 KiB) with XOR swizzles that make every fragment read bank-conflict
 //    free and every fragment one 16-byte read; the next tile's global loads are in
@@ -63,8 +63,10 @@ __device__ __forceinline__ int lds_k(int ps, int t, int c) {
 // LDS byte offset of V^T chunk `h` of dim row `d` in page slot `ps`.  A row's 16 tokens
 // are stored as chunk 0 = tokens {0-3, 8-11}, chunk 1 = tokens {4-7, 12-15}: exactly the
 // 8 keys one lane half contributes to a 16-key PV step.
+// The chunk swizzle h ^ bit2(d) ^ bit3(d) keeps the 16-byte reads of 16 consecutive rows
+// on distinct banks whether the LDS serves 8 lanes from 32 banks or 16 lanes from 64.
 __device__ __forceinline__ int lds_v(int ps, int d, int h) {
-  return ps * kRunBytes + kVOff * 2 + d * 32 + ((h ^ ((d >> 2) & 1)) << 4);
+  return ps * kRunBytes + kVOff * 2 + d * 32 + ((h ^ ((d >> 2) & 1) ^ ((d >> 3) & 1)) << 4);
 }
 
 // Keep the first `valid` (0..16) tokens of 8 bf16 tokens t0.. of one V^T row.
@@ -203,22 +205,27 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PreArgs a) {
     const int buf = kb & 1;
     if (kb + 1 < nkb) stage_load(kb + 1);
     const char* base = lds + buf * kStageBytes;
+    // Both halves' S^T = K Q^T first, so half 0's softmax (VALU) runs while half 1's
+    // MFMAs execute, and half 1's softmax while half 0's PV MFMAs execute.
+    const bool live1 = kb * kKT + 32 < nkeys;  // second half has keys (wave-uniform)
+    float16_t s2[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (j == 1 && !live1) break;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s2[j][i] = 0.f;
+      const int ps = j * 2 + (col >> 4), t = col & 15;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(base + lds_k(ps, t, ks * 2 + hf));
+        s2[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s2[j], 0, 0, 0);
+      }
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {  // two 32-key halves of the tile
+      if (j == 1 && !live1) break;
       const int key0 = kb * kKT + j * 32;
-      if (key0 >= nkeys) continue;  // past the last row's position (wave-uniform)
-      // S^T = K Q^T
-      float16_t s;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[i] = 0.f;
-      {
-        const int ps = j * 2 + (col >> 4), t = col & 15;
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(base + lds_k(ps, t, ks * 2 + hf));
-          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s, 0, 0, 0);
-        }
-      }
+      float16_t& s = s2[j];
       // online softmax over this lane's query row
       float mx = -INFINITY;
       if (key0 + 31 > min_pos) {  // the causal diagonal crosses these keys
@@ -246,15 +253,25 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PreArgs a) {
         m_run = grow ? m_new : m_run;
       }
       bf16x8 pt[2];
-      float psum = 0.f;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         // raw v_exp_f32: results below 2^-126 flush to 0, which a softmax weight can be
         const float p = __builtin_amdgcn_exp2f(fmaf(s[v], a.scale_log2, -m_run));
-        psum += p;
         pt[v >> 3][v & 7] = (__bf16)p;
       }
-      l_run += psum;
+      // l sums the same bf16 P that multiplies V (one v_dot2 per pair instead of one add
+      // per score), so the output weights are normalised exactly
+      {
+        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+        const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const bf16x2_t pr = {pt[kc][2 * e], pt[kc][2 * e + 1]};
+            l_run = __builtin_amdgcn_fdot2_f32_bf16(pr, one, l_run, false);
+          }
+      }
       // O^T += V^T P^T over the two pages (16 keys each) of this half
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) {
