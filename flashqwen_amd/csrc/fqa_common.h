@@ -72,4 +72,43 @@ __device__ __forceinline__ float sum_rows4(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// ---- wave-level integer scans and reductions on DPP ----------------------------------
+// Each step is a VALU op with a lane-shifted operand (row_shr within 16-lane rows, then
+// row_bcast across rows), a few cycles each; __shfl_* goes through ds_bpermute (~100
+// cycles per step).  Bound-control makes shifted-in lanes read 0.
+enum : int {
+  kDppRowShr1 = 0x111,
+  kDppRowShr2 = 0x112,
+  kDppRowShr4 = 0x114,
+  kDppRowShr8 = 0x118,
+  kDppRowBcast15 = 0x142,
+  kDppRowBcast31 = 0x143,
+  kDppWaveShr1 = 0x138,
+};
+
+// Inclusive prefix sum over the 64 lanes of the wave.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, kDppRowShr1, 0xf, 0xf, true);
+  x += __builtin_amdgcn_update_dpp(0, x, kDppRowShr2, 0xf, 0xf, true);
+  x += __builtin_amdgcn_update_dpp(0, x, kDppRowShr4, 0xf, 0xf, true);
+  x += __builtin_amdgcn_update_dpp(0, x, kDppRowShr8, 0xf, 0xf, true);
+  x += __builtin_amdgcn_update_dpp(0, x, kDppRowBcast15, 0xa, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0, x, kDppRowBcast31, 0xc, 0xf, false);
+  return x;
+}
+
+// Max / min over the wave (result in every lane): the scan pattern with max/min, then
+// lane 63 holds the answer.  `id` is the identity (shifted-in lanes read it).
+template <bool kMax>
+__device__ __forceinline__ int wave_extreme(int x, int id) {
+  auto op = [](int a, int b) { return kMax ? (a > b ? a : b) : (a < b ? a : b); };
+  x = op(x, __builtin_amdgcn_update_dpp(id, x, kDppRowShr1, 0xf, 0xf, false));
+  x = op(x, __builtin_amdgcn_update_dpp(id, x, kDppRowShr2, 0xf, 0xf, false));
+  x = op(x, __builtin_amdgcn_update_dpp(id, x, kDppRowShr4, 0xf, 0xf, false));
+  x = op(x, __builtin_amdgcn_update_dpp(id, x, kDppRowShr8, 0xf, 0xf, false));
+  x = op(x, __builtin_amdgcn_update_dpp(id, x, kDppRowBcast15, 0xa, 0xf, false));
+  x = op(x, __builtin_amdgcn_update_dpp(id, x, kDppRowBcast31, 0xc, 0xf, false));
+  return __builtin_amdgcn_readlane(x, 63);
+}
+
 }  // namespace fqa

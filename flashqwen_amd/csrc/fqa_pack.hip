@@ -23,81 +23,61 @@ namespace {
 constexpr int kPackThreads = 1024;
 constexpr int kPackWaves = kPackThreads / 64;
 
-// Exclusive scan of one value per thread over the workgroup; returns the thread's
-// exclusive prefix and the total via *total.  `sh` holds >= kPackWaves values.
-template <typename T>
-__device__ T block_excl_scan(T v, T* sh, T* total) {
+// Exclusive scan of one int per thread over a kPackThreads workgroup (DPP waves + one LDS
+// exchange); the total goes to *total.  `sh` holds >= kPackWaves ints.
+__device__ int block_excl_scan(int v, int* sh, int* total) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
-  T x = v;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    T y = __shfl_up(x, d, kWave);
-    if (lane >= d) x += y;
-  }
-  if (lane == kWave - 1) sh[w] = x;
+  const int incl = wave_incl_scan(v);
+  if (lane == kWave - 1) sh[w] = incl;
   __syncthreads();
-  T base = 0, tot = 0;
-#pragma unroll
-  for (int i = 0; i < kPackThreads / kWave; ++i) {
-    T s = sh[i];
-    if (i < w) base += s;
-    tot += s;
-  }
+  const int sc = wave_incl_scan(lane < kPackWaves ? sh[lane] : 0);
+  *total = __builtin_amdgcn_readlane(sc, kPackWaves - 1);
+  const int below = __builtin_amdgcn_readlane(sc, w == 0 ? 0 : w - 1);
   __syncthreads();
-  *total = tot;
-  return base + x - v;
+  return (w == 0 ? 0 : below) + incl - v;
 }
 
-template <typename T, typename Op>
-__device__ T block_reduce(T v, T* sh, Op op) {
+// Max over the workgroup (every thread gets it).
+__device__ int block_max(int v, int* sh) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) v = op(v, __shfl_xor(v, d, kWave));
+  v = wave_extreme<true>(v, INT_MIN);
   if (lane == 0) sh[w] = v;
   __syncthreads();
-  T r = sh[0];
-#pragma unroll
-  for (int i = 1; i < kPackThreads / kWave; ++i) r = op(r, sh[i]);
+  v = wave_extreme<true>(lane < kPackWaves ? sh[lane] : INT_MIN, INT_MIN);
   __syncthreads();
-  return r;
+  return v;
 }
 
-// The per-request totals of pass 1 (code: min, rows/dpages: saturating sum,
-// dmax/qmax: max) reduced together, and the five exclusive scans of pass 2 done
-// together.  Small kernels here are bound by instruction fetch (the instruction cache
-// starts cold at every dispatch), so these loops are kept rolled: code size, not
-// instruction count, sets their latency.
-__device__ __forceinline__ int sat_add(int a, int b) {
-  long long s = (long long)a + b;
-  return s > INT_MAX ? INT_MAX : (int)s;
-}
+// The per-request totals of pass 1 and the five exclusive scans of pass 2, each done
+// for all values at once with DPP wave primitives (a shuffle-based version spent ~3 us
+// per reduction in ds_bpermute latency chains).  Sums are of values the host bounds
+// (rows <= max_rows <= 2^20, pages <= max_blocks <= 2^19 per request, <= 2 requests per
+// thread); a thread partial that exceeds kPartCap is flagged instead of overflowing.
+constexpr int kPartCap = 1 << 20;
 
 struct Stats {
-  int v[5];  // code, rows, dpages, dmax, qmax
+  int v[6];  // code (min), rows (sum), dpages (sum), dmax (max), qmax (max), overflow (max)
 };
-
-__device__ __forceinline__ void stats_combine(Stats& a, const Stats& b) {
-  a.v[0] = min(a.v[0], b.v[0]);
-  a.v[1] = sat_add(a.v[1], b.v[1]);
-  a.v[2] = sat_add(a.v[2], b.v[2]);
-  a.v[3] = max(a.v[3], b.v[3]);
-  a.v[4] = max(a.v[4], b.v[4]);
-}
 
 __device__ Stats block_reduce_stats(Stats v, Stats* sh) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
-#pragma unroll 1
-  for (int d = 1; d < kWave; d <<= 1) {
-    Stats o;
-#pragma unroll
-    for (int k = 0; k < 5; ++k) o.v[k] = __shfl_xor(v.v[k], d, kWave);
-    stats_combine(v, o);
-  }
-  if (lane == 0) sh[w] = v;
+  Stats r;
+  r.v[0] = wave_extreme<false>(v.v[0], INT_MAX);
+  r.v[1] = __builtin_amdgcn_readlane(wave_incl_scan(v.v[1]), 63);
+  r.v[2] = __builtin_amdgcn_readlane(wave_incl_scan(v.v[2]), 63);
+  r.v[3] = wave_extreme<true>(v.v[3], 0);
+  r.v[4] = wave_extreme<true>(v.v[4], 1);
+  r.v[5] = wave_extreme<true>(v.v[5], 0);
+  if (lane == 0) sh[w] = r;
   __syncthreads();
-  Stats r = sh[0];
-#pragma unroll 1
-  for (int i = 1; i < kPackWaves; ++i) stats_combine(r, sh[i]);
+  const bool have = lane < kPackWaves;
+  const Stats o = sh[have ? lane : 0];
+  r.v[0] = wave_extreme<false>(have ? o.v[0] : INT_MAX, INT_MAX);
+  r.v[1] = __builtin_amdgcn_readlane(wave_incl_scan(have ? o.v[1] : 0), 63);
+  r.v[2] = __builtin_amdgcn_readlane(wave_incl_scan(have ? o.v[2] : 0), 63);
+  r.v[3] = wave_extreme<true>(have ? o.v[3] : 0, 0);
+  r.v[4] = wave_extreme<true>(have ? o.v[4] : 1, 1);
+  r.v[5] = wave_extreme<true>(have ? o.v[5] : 0, 0);
   __syncthreads();
   return r;
 }
@@ -106,43 +86,27 @@ struct Counts {
   int v[5];
 };
 
+// Exclusive scans of 5 values over the workgroup; *total gets the 5 sums.
 __device__ Counts block_excl_scan5(const Counts& in, Counts* sh, Counts* total) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
-  Counts x = in;
-#pragma unroll 1
-  for (int d = 1; d < kWave; d <<= 1) {
-    int y[5];
+  Counts incl;
 #pragma unroll
-    for (int k = 0; k < 5; ++k) y[k] = __shfl_up(x.v[k], d, kWave);
-    if (lane >= d)
-#pragma unroll
-      for (int k = 0; k < 5; ++k) x.v[k] += y[k];
-  }
-  if (lane == kWave - 1) sh[w] = x;
+  for (int k = 0; k < 5; ++k) incl.v[k] = wave_incl_scan(in.v[k]);
+  if (lane == kWave - 1) sh[w] = incl;
   __syncthreads();
-  Counts base = {{0, 0, 0, 0, 0}}, tot = {{0, 0, 0, 0, 0}};
-#pragma unroll 1
-  for (int i = 0; i < kPackWaves; ++i) {
-    const Counts s = sh[i];
-#pragma unroll
-    for (int k = 0; k < 5; ++k) {
-      if (i < w) base.v[k] += s.v[k];
-      tot.v[k] += s.v[k];
-    }
-  }
-  __syncthreads();
-  *total = tot;
+  const bool have = lane < kPackWaves;
+  const Counts o = sh[have ? lane : 0];
   Counts out;
 #pragma unroll
-  for (int k = 0; k < 5; ++k) out.v[k] = base.v[k] + x.v[k] - in.v[k];
+  for (int k = 0; k < 5; ++k) {
+    const int sc = wave_incl_scan(have ? o.v[k] : 0);  // lane i: total of waves 0..i
+    total->v[k] = __builtin_amdgcn_readlane(sc, kPackWaves - 1);
+    const int below = __builtin_amdgcn_readlane(sc, w == 0 ? 0 : w - 1);
+    out.v[k] = (w == 0 ? 0 : below) + incl.v[k] - in.v[k];
+  }
+  __syncthreads();
   return out;
 }
-
-struct MinOp { __device__ int operator()(int a, int b) const { return a < b ? a : b; } };
-struct MaxOp { __device__ int operator()(int a, int b) const { return a > b ? a : b; } };
-struct SumOp64 {
-  __device__ long long operator()(long long a, long long b) const { return a + b; }
-};
 
 __device__ __forceinline__ int cdiv(long long a, long long b) { return (int)((a + b - 1) / b); }
 
@@ -173,7 +137,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   __shared__ int s_dstart[FQA_MAX_REQS + 1];  // by decode index: 8 * page prefix
   __shared__ int s_dpages[FQA_MAX_REQS];      // by decode index: pages
   __shared__ int s_preit[FQA_MAX_REQS + 1];
-  __shared__ Stats s_stats[kPackWaves];
+  __shared__ Stats s_stats[kPackWaves];  // (Stats now has 6 fields)
   __shared__ Counts s_counts[kPackWaves];
   __shared__ int sh32[kPackWaves];
 
@@ -185,7 +149,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   const int maxb = a.c.max_blocks;
 
   // ---- pass 1: load, structural checks, totals ---------------------------------
-  Stats st = {{INT_MAX, 0, 0, 0, 1}};
+  Stats st = {{INT_MAX, 0, 0, 0, 1, 0}};
   for (int r = tid; r < R; r += kPackThreads) {
     const int c = a.b.computed[r], n = a.b.n_new[r];
     const int o0 = a.b.bt_off[r], o1 = a.b.bt_off[r + 1];
@@ -198,10 +162,10 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       const int nb = o1 - o0;
       if (nb < cdiv((long long)c + n, kPage)) cc = FQA_PACK_SHORT_TABLE;
       else if (nb > maxb) cc = FQA_PACK_WIDE_TABLE;
-      st.v[1] = sat_add(st.v[1], n);
+      st.v[1] = min(st.v[1] + min(n, kPartCap), kPartCap + 1);
       if (n == 1) {
         const int pg = c / kPage + 1;
-        st.v[2] = sat_add(st.v[2], pg);
+        st.v[2] = min(st.v[2] + min(pg, kPartCap), kPartCap + 1);
         st.v[3] = max(pg, st.v[3]);
       } else {
         st.v[4] = max(n, st.v[4]);
@@ -209,11 +173,13 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     }
     if (cc) st.v[0] = min(st.v[0], cc);
   }
+  st.v[5] = st.v[2] > kPartCap;
   if (tid == 0) s_btoff[R] = a.b.bt_off[R];
   st = block_reduce_stats(st, s_stats);
   int code = st.v[0];
   const int rows = st.v[1], dpages = st.v[2], qmax = st.v[4];
   if (rows > a.c.max_rows && code > FQA_PACK_ROWS) code = FQA_PACK_ROWS;
+  if (code == INT_MAX && st.v[5]) code = FQA_PACK_ITEMS;  // decode pages beyond the plan's range
   if (code != INT_MAX) {
     if (blockIdx.x == 0 && tid < FQA_META_LEN)
       a.o.meta[tid] = tid == FQA_META_STATUS ? code : (tid == FQA_META_REQS ? R : 0);
@@ -293,9 +259,9 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   }
   // ---- padded block tables -------------------------------------------------------
   {
-    const long long total = (long long)R * maxb;
-    for (long long e = gtid; e < total; e += gsz) {
-      int r = (int)(e / maxb), g = (int)(e % maxb);
+    const int total = R * maxb;  // < 2^31: R <= 2048, max_blocks <= 2^19
+    for (int e = gtid; e < total; e += gsz) {
+      const int r = e / maxb, g = e - r * maxb;
       int nb = s_btoff[r + 1] - s_btoff[r];
       a.o.block_tables[e] = g < nb ? a.b.bt_pages[s_btoff[r] + g] : -1;
     }
@@ -377,7 +343,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       for (int u = 0; u < 4; ++u) bad |= (int)badv(v[u].x) | (int)badv(v[u].y) | (int)badv(v[u].z) | (int)badv(v[u].w);
     }
   }
-  bad = block_reduce(bad, sh32, MaxOp());
+  bad = block_max(bad, sh32);
   if (tid < FQA_META_LEN) {
     int v = 0;
     switch (tid) {
@@ -406,7 +372,7 @@ schedule_kernel(const int32_t* __restrict__ num_tokens, const int32_t* __restric
                 int32_t* n_batch) {
   __shared__ int s_rem[FQA_MAX_REQS];
   __shared__ int s_order[FQA_MAX_REQS];
-  __shared__ long long s_wsum[kSchedThreads / kWave];
+  __shared__ int s_wsum[kSchedThreads / kWave];
   __shared__ int s_wcnt[kSchedThreads / kWave];
   const int tid = threadIdx.x;
   for (int i = tid; i < R; i += kSchedThreads) s_rem[i] = num_tokens[i] - computed[i];
@@ -422,46 +388,44 @@ schedule_kernel(const int32_t* __restrict__ num_tokens, const int32_t* __restric
   }
   __syncthreads();
   // n_k = min(B, S_k) - min(B, S_{k-1}), S = inclusive prefix of per-request caps:
-  // the greedy loop's budget bookkeeping in closed form.
+  // the greedy loop's budget bookkeeping in closed form.  Only min(B, S) matters, so the
+  // prefix is taken with saturating adds at B + 1 (B <= 2^24 keeps every sum in int).
   const int lane = tid & (kWave - 1), w = tid >> 6;
-  long long carry = 0;
+  const int B = budget > 0 ? budget : 0, cap1 = B + 1;
+  auto sat = [cap1](int x, int y) { const int s = x + y; return s < cap1 ? s : cap1; };
+  int carry = 0;
   int ccount = 0;
   for (int base = 0; base < R; base += kSchedThreads) {
-    int k = base + tid;
-    long long cap = 0;
-    int idx = -1;
+    const int k = base + tid;
+    int cap = 0, idx = -1;
     if (k < R) {
       idx = s_order[k];
-      int rem = s_rem[idx];
+      const int rem = s_rem[idx];
       cap = rem <= 0 ? 0 : (rem > 1 && chunk < rem ? chunk : rem);
+      cap = cap < cap1 ? cap : cap1;
     }
-    long long x = cap;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-      long long y = __shfl_up(x, d, kWave);
-      if (lane >= d) x += y;
-    }
+    int x = cap;
+    x = sat(x, __builtin_amdgcn_update_dpp(0, x, kDppRowShr1, 0xf, 0xf, true));
+    x = sat(x, __builtin_amdgcn_update_dpp(0, x, kDppRowShr2, 0xf, 0xf, true));
+    x = sat(x, __builtin_amdgcn_update_dpp(0, x, kDppRowShr4, 0xf, 0xf, true));
+    x = sat(x, __builtin_amdgcn_update_dpp(0, x, kDppRowShr8, 0xf, 0xf, true));
+    x = sat(x, __builtin_amdgcn_update_dpp(0, x, kDppRowBcast15, 0xa, 0xf, false));
+    x = sat(x, __builtin_amdgcn_update_dpp(0, x, kDppRowBcast31, 0xc, 0xf, false));
     if (lane == kWave - 1) s_wsum[w] = x;
     __syncthreads();
-    long long pre = 0, tot = 0;
-    for (int i = 0; i < kSchedThreads / kWave; ++i) {
-      if (i < w) pre += s_wsum[i];
-      tot += s_wsum[i];
-    }
+    int pre = carry;  // saturating prefix of the earlier waves
+    for (int i = 0; i < w; ++i) pre = sat(pre, s_wsum[i]);
+    int tot = carry;
+    for (int i = 0; i < kSchedThreads / kWave; ++i) tot = sat(tot, s_wsum[i]);
     __syncthreads();
-    long long incl = carry + pre + x, excl = incl - cap;
-    long long B = budget;
-    long long hi = incl < B ? incl : B, lo = excl < B ? excl : B;
-    int n = (int)(hi - lo);
-    if (B <= 0) n = 0;
-    int take = n > 0;
+    // exclusive prefix = the previous lane's saturated inclusive prefix (wave_shr:1)
+    const int xe = __builtin_amdgcn_update_dpp(0, x, kDppWaveShr1, 0xf, 0xf, true);
+    const int incl = sat(pre, x), excl = sat(pre, xe);
+    const int hi = incl < B ? incl : B, lo = excl < B ? excl : B;
+    const int n = hi - lo;
+    const int take = n > 0;
     // compact the chosen requests in sorted order
-    int c = take;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-      int y = __shfl_up(c, d, kWave);
-      if (lane >= d) c += y;
-    }
+    const int c = wave_incl_scan(take);
     if (lane == kWave - 1) s_wcnt[w] = c;
     __syncthreads();
     int cpre = 0, ctot = 0;
@@ -471,11 +435,11 @@ schedule_kernel(const int32_t* __restrict__ num_tokens, const int32_t* __restric
     }
     __syncthreads();
     if (take) {
-      int pos = ccount + cpre + c - 1;
+      const int pos = ccount + cpre + c - 1;
       batch_req[pos] = idx;
       batch_n[pos] = n;
     }
-    carry += tot;
+    carry = tot;
     ccount += ctot;
   }
   if (tid == 0) *n_batch = ccount;
@@ -536,7 +500,8 @@ extern "C" {
 int fqa_schedule(const int32_t* num_tokens, const int32_t* computed, int32_t n_running,
                  int32_t token_budget, int32_t prefill_chunk, int32_t* batch_req,
                  int32_t* batch_n, int32_t* n_batch, void* stream) {
-  if (n_running < 0 || n_running > FQA_MAX_REQS || prefill_chunk < 1 || !n_batch)
+  if (n_running < 0 || n_running > FQA_MAX_REQS || prefill_chunk < 1 ||
+      token_budget > (1 << 24) || !n_batch)
     return FQA_EINVAL;
   if (n_running > 0 && (!num_tokens || !computed || !batch_req || !batch_n)) return FQA_EINVAL;
   hipLaunchKernelGGL(schedule_kernel, dim3(1), dim3(kSchedThreads), 0, (hipStream_t)stream,
@@ -568,7 +533,8 @@ int fqa_pack(const fqa_batch* batch, const fqa_pack_cfg* cfg, const fqa_pack_out
   if (!batch || !cfg || !out) return FQA_EINVAL;
   const int R = batch->n_reqs;
   if (R < 0 || R > FQA_MAX_REQS) return FQA_EINVAL;
-  if (cfg->max_rows < 0 || cfg->max_blocks < 1 || cfg->pool_pages < 1 ||
+  if (cfg->max_rows < 0 || cfg->max_rows > (1 << 20) || cfg->max_blocks < 1 ||
+      cfg->max_blocks > (1 << 19) || cfg->pool_pages < 1 ||
       cfg->dec_wave_cap < 0 || cfg->pre_item_cap < 0 || cfg->dec_grid_waves < 1)
     return FQA_EINVAL;
   if (cfg->pre_tile_q != 32 && cfg->pre_tile_q != 64 && cfg->pre_tile_q != 128)

@@ -133,8 +133,8 @@ typedef struct fqa_pack_out {
 } fqa_pack_out;
 
 typedef struct fqa_pack_cfg {
-  int32_t max_rows;          /* capacity of the per-row arrays             */
-  int32_t max_blocks;        /* block table stride                         */
+  int32_t max_rows;          /* capacity of the per-row arrays (<= 2^20)   */
+  int32_t max_blocks;        /* block table stride (<= 2^19)               */
   int64_t pool_pages;        /* pages in the per-layer pool                */
   int32_t dec_grid_waves;    /* decode wavefronts to spread the work over (>= 1) */
   int32_t dec_min_pages;     /* give no wavefront fewer page runs than this   */
@@ -171,7 +171,8 @@ int64_t fqa_decode_workspace_bytes(const fqa_dims* dims, int32_t dec_wave_cap);
  * n = min(remaining, budget left, prefill_chunk if remaining > 1) in that order.
  * Writes batch_req[R] (index into the running arrays), batch_n[R], and *n_batch (R).
  * Block tables must already cover each chosen request's computed + n tokens (the
- * allocator's Grow stays on the host). One workgroup; n_running <= FQA_MAX_REQS. */
+ * allocator's Grow stays on the host). One workgroup; n_running <= FQA_MAX_REQS,
+ * token_budget <= 2^24. */
 int fqa_schedule(const int32_t* num_tokens, const int32_t* computed, int32_t n_running,
                  int32_t token_budget, int32_t prefill_chunk, int32_t* batch_req,
                  int32_t* batch_n, int32_t* n_batch, void* stream);
