@@ -44,7 +44,7 @@ struct DecArgs {
   long long pool_pages;
   const int32_t* bt;
   int max_blocks;
-  const int32_t* waves;  // [G][4] {di, kvh, page, n_runs}
+  const int32_t* waves;  // [G][8] {di, kvh, page, n_runs, r, row, n_keys, first page id}
   const int32_t* seqs;   // [n_decode][4] {r, row, n_keys, 8*P}
   const int32_t* meta;
   float* ws_m;
@@ -123,10 +123,10 @@ __device__ __forceinline__ void process_page(PageFrag& f, const bf16x8 (&qf)[4],
 // Stream pages [pb, pe) of (sequence `seq`, kv head kvh) into `st`.
 __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* btr, int kvh,
                                              int pb, int pe, int L, const bf16x8 (&qf)[4],
-                                             int lane, DecState& st) {
+                                             int lane, DecState& st, int first_page) {
   const int g = lane >> 4;
   auto load = [&](PageFrag& f, bool& ok, int p) {
-    const long long page = btr[p];
+    const long long page = (p == pb && first_page >= 0) ? first_page : btr[p];
     ok = page >= 0 && page < a.pool_pages;
     load_page(f, a.pool + run_offset(ok ? page : 0, kvh), lane);
   };
@@ -161,10 +161,14 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
   if (w >= a.meta[FQA_META_DEC_WAVES]) return;
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
-  const int4 desc = *reinterpret_cast<const int4*>(a.waves + 4 * (long long)w);
+  const int4 desc = *reinterpret_cast<const int4*>(a.waves + 8 * (long long)w);
+  int4 sq = reinterpret_cast<const int4*>(a.waves + 8 * (long long)w)[1];  // {r, row, L, page id}
   int di = desc.x, kvh = desc.y, page = desc.z, left = desc.w;
   for (int seg = 0; left > 0; ++seg) {
-    const int4 sq = *reinterpret_cast<const int4*>(a.seqs + 4 * (long long)di);
+    if (seg > 0) {
+      sq = *reinterpret_cast<const int4*>(a.seqs + 4 * (long long)di);
+      sq.w = -1;  // first page id of a later stream: read from the block table
+    }
     const int r = sq.x, row = sq.y, L = sq.z;
     const int pages = (L + kPage - 1) / kPage;
     const int cnt = min(pages - page, left);
@@ -186,7 +190,8 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
     for (int b = 0; b < 8; ++b) st.acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
     st.m = -1e30f;
     st.l = 0.f;
-    stream_pages(a, a.bt + (long long)r * a.max_blocks, kvh, page, page + cnt, L, qf, lane, st);
+    stream_pages(a, a.bt + (long long)r * a.max_blocks, kvh, page, page + cnt, L, qf, lane, st,
+                 sq.w);
     const float l_run = sum_rows4(st.l);
 
     if (n < kG) {

@@ -136,6 +136,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   __shared__ int s_decit[FQA_MAX_REQS + 1];  // exclusive prefix of decode pages
   __shared__ int s_dstart[FQA_MAX_REQS + 1];  // by decode index: 8 * page prefix
   __shared__ int s_dpages[FQA_MAX_REQS];      // by decode index: pages
+  __shared__ int s_drid[FQA_MAX_REQS];        // by decode index: request
   __shared__ int s_preit[FQA_MAX_REQS + 1];
   __shared__ Stats s_stats[kPackWaves];  // (Stats now has 6 fields)
   __shared__ Counts s_counts[kPackWaves];
@@ -242,6 +243,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     if (s_n[r] == 1) {
       s_dstart[s_decidx[r]] = 8 * s_decit[r];
       s_dpages[s_decidx[r]] = s_comp[r] / kPage + 1;
+      s_drid[s_decidx[r]] = r;
     }
   if (tid == 0) s_dstart[nd] = (int)W;
   __syncthreads();
@@ -271,8 +273,10 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     const long long g0 = (long long)w * W / G, g1 = (long long)(w + 1) * W / G;
     const int di = upper_index(s_dstart, nd, (int)g0);
     const int rem = (int)g0 - s_dstart[di], pg = s_dpages[di];
-    *reinterpret_cast<int4*>(a.o.dec_waves + 4 * (long long)w) =
-        make_int4(di, rem / pg, rem % pg, (int)(g1 - g0));
+    const int kvh = rem / pg, page = rem % pg, r = s_drid[di];
+    int4* dst = reinterpret_cast<int4*>(a.o.dec_waves + 8 * (long long)w);
+    dst[0] = make_int4(di, kvh, page, (int)(g1 - g0));
+    dst[1] = make_int4(r, s_qstart[r], s_comp[r] + 1, a.b.bt_pages[s_btoff[r] + page]);
   }
   for (int r = gtid; r < R; r += gsz)
     if (s_n[r] == 1)

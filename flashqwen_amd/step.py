@@ -91,7 +91,7 @@ class AttnStep:
         self.decode_rids = torch.zeros(R, **i32)
         self.prefill_rids = torch.zeros(R, **i32)
         self.dec_seqs = torch.zeros((max(R, 1), 4), **i32)
-        self.dec_waves = torch.zeros((max(self.dec_wave_cap, 1), 4), **i32)
+        self.dec_waves = torch.zeros((max(self.dec_wave_cap, 1), 8), **i32)
         self.pre_items = torch.zeros((max(self.pre_cap, 1), 4), **i32)
         self.meta = torch.zeros(_lib.META_LEN, **i32)
         ws = int(self.lib.fqa_decode_workspace_bytes(C.byref(self.dims), self.dec_wave_cap))

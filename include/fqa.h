@@ -112,8 +112,10 @@ typedef struct fqa_batch {
  * pages = ceil(n_keys/16) and P is the exclusive prefix of pages over decode indices.
  * The W = 8*sum(pages) page runs are cut into G = min(dec_grid_waves,
  * ceil(W/dec_min_pages)) equal contiguous shares, share w = [floor(w*W/G),
- * floor((w+1)*W/G)), one per decode wavefront; dec_waves[w] = {di, kvh, page, n_runs}
- * is where share w starts and how long it is.  dec_seqs[di] = {r, row = qstart[r],
+ * floor((w+1)*W/G)), one per decode wavefront; dec_waves[w] = {di, kvh, page, n_runs,
+ * r, row, n_keys, page id} is where share w starts, how long it is, the first stream's
+ * request, row and key count, and its first page (so a wavefront's first loads need no
+ * further lookups).  dec_seqs[di] = {r, row = qstart[r],
  * n_keys = computed[r]+1, 8*P[di]}.  Prefill plan: one item per pre_tile_q query rows
  * of each prefill request, pre_items[i] = {r, q0, q1, n_keys = computed + q1}, ordered
  * by n_keys descending (stable). */
@@ -127,7 +129,7 @@ typedef struct fqa_pack_out {
   int32_t* decode_rids;    /* [R] qlen==1 requests, increasing; pad -1        */
   int32_t* prefill_rids;   /* [R] the others, increasing; pad -1              */
   int32_t* dec_seqs;       /* [R][4] per decode index: {r, row, n_keys, 8*P}  */
-  int32_t* dec_waves;      /* [dec_wave_cap][4] {di, kvh, page, n_runs}      */
+  int32_t* dec_waves;      /* [dec_wave_cap][8] see the decode plan above     */
   int32_t* pre_items;      /* [pre_cap][4] {r, q0, q1, n_keys}                */
   int32_t* meta;           /* [FQA_META_LEN]                                  */
 } fqa_pack_out;

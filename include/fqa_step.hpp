@@ -92,7 +92,7 @@ class StepContext {
     drids_ = DeviceBuffer<int32_t>(slots);
     prids_ = DeviceBuffer<int32_t>(slots);
     dseqs_ = DeviceBuffer<int32_t>((size_t)slots * 4);
-    dwaves_ = DeviceBuffer<int32_t>((size_t)dec_cap_ * 4);
+    dwaves_ = DeviceBuffer<int32_t>((size_t)dec_cap_ * 8);
     items_ = DeviceBuffer<int32_t>((size_t)pre_cap_ * 4);
     meta_ = DeviceBuffer<int32_t>(FQA_META_LEN);
     ws_ = DeviceBuffer<unsigned char>((size_t)fqa_decode_workspace_bytes(&dims_, dec_cap_));

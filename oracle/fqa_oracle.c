@@ -223,10 +223,15 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
         pages = computed[decode_rids[di]] / PAGE + 1;
       }
       int64_t rem = g0 - start;
-      dec_waves[4 * w + 0] = di;
-      dec_waves[4 * w + 1] = (int32_t)(rem / pages);
-      dec_waves[4 * w + 2] = (int32_t)(rem % pages);
-      dec_waves[4 * w + 3] = (int32_t)(g1 - g0);
+      int r = decode_rids[di], page = (int)(rem % pages);
+      dec_waves[8 * w + 0] = di;
+      dec_waves[8 * w + 1] = (int32_t)(rem / pages);
+      dec_waves[8 * w + 2] = page;
+      dec_waves[8 * w + 3] = (int32_t)(g1 - g0);
+      dec_waves[8 * w + 4] = r;
+      dec_waves[8 * w + 5] = cu_seqlens[r];
+      dec_waves[8 * w + 6] = computed[r] + 1;
+      dec_waves[8 * w + 7] = bt_pages[bt_off[r] + page];
     }
   }
   {

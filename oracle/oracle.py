@@ -81,7 +81,7 @@ def pack(computed, n_new, bt_off, bt_pages, *, max_rows, max_blocks, pool_pages,
         block_tables=np.zeros(max(R * max_blocks, 1), np.int32),
         decode_rids=np.zeros(max(R, 1), np.int32), prefill_rids=np.zeros(max(R, 1), np.int32),
         dec_seqs=np.zeros((max(R, 1), 4), np.int32),
-        dec_waves=np.zeros((max(dec_wave_cap, 1), 4), np.int32),
+        dec_waves=np.zeros((max(dec_wave_cap, 1), 8), np.int32),
         pre_items=np.zeros((max(pre_item_cap, 1), 4), np.int32),
         meta=np.zeros(16, np.int32))
     status = load().fqo_pack(

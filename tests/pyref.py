@@ -96,7 +96,10 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
     waves = []
     for w in range(G):
         g0, g1 = w * W // G, (w + 1) * W // G
-        waves.append([*runs[g0], g1 - g0])
+        di, kvh, pg = runs[g0]
+        r = dec[di]
+        waves.append([di, kvh, pg, g1 - g0, r, res["cu_seqlens"][r], computed[r] + 1,
+                      tables[r][pg]])
     # prefill items: tiles sorted by key count descending, stable
     tiles = []
     for r in pre:

@@ -339,8 +339,11 @@ def test_pack_known_answer():
     assert got["meta"][:10].tolist() == [5, 2, 2, 3, 5, 1, 5, 0, 4, 3]
     # W = 8*(2+1) = 24 page runs over 5 waves: shares 4,5,5,5,5
     assert got["dec_seqs"][:2].tolist() == [[0, 0, 18, 0], [2, 4, 1, 16]]
-    assert got["dec_waves"][:5].tolist() == [[0, 0, 0, 4], [0, 2, 0, 5], [0, 4, 1, 5],
-                                             [0, 7, 0, 5], [1, 3, 0, 5]]
+    assert got["dec_waves"][:5, :4].tolist() == [[0, 0, 0, 4], [0, 2, 0, 5], [0, 4, 1, 5],
+                                                 [0, 7, 0, 5], [1, 3, 0, 5]]
+    # {r, row, n_keys, first page id}: page 1 of request 0 is page id 9
+    assert got["dec_waves"][:5, 4:].tolist() == [[0, 0, 18, 5], [0, 0, 18, 5], [0, 0, 18, 9],
+                                                 [0, 0, 18, 5], [2, 4, 1, 11]]
     assert got["pre_items"][:1].tolist() == [[1, 0, 3, 18]]
 
 
@@ -373,7 +376,7 @@ def test_dec_waves_cover_every_run_once():
     got = orc.pack(comp, [1] * 37, synth._assemble("x", comp, [1] * 37, [np.array(t) for t in tabs], 4096, 4096).bt_off,
                    np.concatenate(tabs), **kw)
     seen = []
-    for di, kvh, page, n in got["dec_waves"][: got["meta"][4]]:
+    for di, kvh, page, n, *_ in got["dec_waves"][: got["meta"][4]]:
         while n > 0:
             pages = comp[got["dec_seqs"][di][0]] // 16 + 1
             take = min(n, pages - page)
