@@ -10,34 +10,47 @@
 //  * One 256-thread workgroup per (32 query rows, kv head); wave w owns query head w of
 //    the kv head.  The 4 heads share every K/V tile, staged into LDS once (the
 //    reference runs one block per query head and re-reads K/V 4x, attn_cute.cu:157).
-//    At 212 VGPRs two workgroups share a CU, so one wave's MFMAs overlap another's
-//    softmax on every SIMD.
+//    Two workgroups share a CU, so one wave's MFMAs overlap another's softmax on every
+//    SIMD.
 //  * Transposed FA-2 on v_mfma_f32_32x32x16_bf16:
 //        S^T[32 keys x 32 rows] = K[32 x 128] . Q^T[128 x 32]   (8 MFMAs per 32 keys)
 //        O^T[128 x 32 rows]    += V^T[128 x 16 keys] . P^T      (4 MFMAs per 16 keys)
 //    With rows as accumulator columns every lane owns one query row: the softmax row
 //    max / sum is 16 in-lane values plus one exchange with lane^32, the rescale of O is
-//    a per-lane scalar, and the S^T accumulator registers are already the P^T operand
-//    (the key order inside the contraction is chosen to match, V^T is read to suit).
+//    a per-lane scalar, and the S^T accumulator registers are already the P^T operand.
+//    MFMA row r of S^T holds key perm(r) (bits 2 and 3 of r swapped), so the 8 keys a
+//    lane half contributes to one page's PV step are 8 consecutive tokens: one 16-byte
+//    chunk of the page's V^T row.
 //  * Softmax VALU work per score, not MFMA, is the limit on CDNA (a wave64 VALU op
 //    issues in 4 cycles, exp in more): scores are maxed raw, scaled inside the exp2
 //    FMA, converted with v_cvt_pk_bf16_f32, summed two at a time with v_dot2 against
 //    (1, 1), and O is rescaled lazily (only when the row max grows by more than 2^8).
-//  * K/V tiles are 64 keys = 4 pages = four contiguous 8 KiB runs, double-buffered in
-//    LDS (2 x 32 KiB) with XOR swizzles that make every fragment read bank-conflict
-//    free and every fragment one 16-byte read; the next tile's global loads are in
-//    flight during the current tile's MFMAs.
+//  * Software pipeline over 32-key halves: half t's exp/convert/sum is interleaved with
+//    the S^T MFMAs of half t+1 and the LDS reads of half t's V fragments, then half t's
+//    PV MFMAs issue back to back.
+//  * K/V staging is direct global->LDS (global_load_lds_dwordx4): a ring of four 16 KiB
+//    buffers, one 32-key half (two 8 KiB page runs) each, filled three halves ahead.
+//    Each wave moves one 4 KiB region (K or V^T of one page) per half; every lane picks
+//    the global chunk that lands in its slot of the XOR-swizzled layout, so fragment
+//    reads are conflict-free 16-byte reads and no VGPR carries staged data.  The loads
+//    are issued from inline assembly, so the compiler neither tracks them nor inserts
+//    its own conservative waits: every wait on them is an explicit vmcnt count followed
+//    by a barrier, and the loop issues no other vector-memory loads.
 //  * Work items come from the pack sorted by key count, longest first.
+
 #include "fqa_common.h"
+
+#include <type_traits>
 
 namespace fqa {
 namespace {
 
-constexpr int kQT = 32;        // query rows per workgroup
-constexpr int kKT = 64;        // keys per LDS tile (4 pages)
-constexpr int kPagesPerTile = kKT / kPage;
-constexpr int kRunBytes = kRunElems * 2;                 // 8 KiB
-constexpr int kStageBytes = kPagesPerTile * kRunBytes;   // 32 KiB
+constexpr int kQT = 32;          // query rows per workgroup
+constexpr int kHalfKeys = 32;    // keys per pipeline step (2 pages)
+constexpr int kRunBytes = kRunElems * 2;       // 8 KiB: one (page, kv head) run
+constexpr int kHalfBytes = 2 * kRunBytes;      // 16 KiB LDS buffer
+constexpr int kRing = 4;                       // LDS buffers
+constexpr int kAhead = kRing - 1;              // halves loaded ahead of the current one
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescale = 8.0f;  // lazy-rescale threshold (log2 units)
 
@@ -56,47 +69,95 @@ struct PreArgs {
   float scale_log2;
 };
 
+// One 16-byte-per-lane global->LDS load when `go` != 0: lane i's 16 bytes at base + off
+// land at LDS byte lds + 16 i.  `lds` and `go` are wave-uniform.  M0 carries the LDS
+// address and is restored afterwards (the compiler reserves it); an LDS DMA needs one
+// wait state after an M0 write, hence the s_nop.  The branch lives inside the asm so the
+// caller's basic block is not split and the scheduler can interleave around it.
+__device__ __forceinline__ void dma16_if(uint32_t go, const void* base, uint32_t off, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_cmp_eq_u32 %4, 0\n\t"
+      "s_cbranch_scc1 1f\n\t"
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "s_mov_b32 m0, %0\n"
+      "1:"
+      : "=&s"(saved)
+      : "v"(off), "s"(base), "s"(lds), "s"(go)
+      : "memory", "scc");
+}
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
+  dma16_if(1u, base, off, lds);
+}
+
 // LDS byte offset of K chunk (16 B = 8 dims) `c` of token `t` in page slot `ps`.
 __device__ __forceinline__ int lds_k(int ps, int t, int c) {
   return ps * kRunBytes + t * 256 + ((c ^ t) << 4);
 }
-// LDS byte offset of V^T chunk `h` of dim row `d` in page slot `ps`.  A row's 16 tokens
-// are stored as chunk 0 = tokens {0-3, 8-11}, chunk 1 = tokens {4-7, 12-15}: exactly the
-// 8 keys one lane half contributes to a 16-key PV step.
-// The chunk swizzle h ^ bit2(d) ^ bit3(d) keeps the 16-byte reads of 16 consecutive rows
-// on distinct banks whether the LDS serves 8 lanes from 32 banks or 16 lanes from 64.
+// LDS byte offset of V^T chunk `h` (tokens 8h..8h+7) of dim row `d` in page slot `ps`.
+// The swizzle h ^ bit3(d) keeps the 16-byte reads of 16 consecutive rows on distinct
+// banks.
 __device__ __forceinline__ int lds_v(int ps, int d, int h) {
-  return ps * kRunBytes + kVOff * 2 + d * 32 + ((h ^ ((d >> 2) & 1) ^ ((d >> 3) & 1)) << 4);
+  return ps * kRunBytes + kVOff * 2 + d * 32 + ((h ^ ((d >> 3) & 1)) << 4);
 }
 
 // Keep the first `valid` (0..16) tokens of 8 bf16 tokens t0.. of one V^T row.
-__device__ __forceinline__ uint2 keep_tokens(uint2 v, int t0, int valid) {
-  uint32_t w[2] = {v.x, v.y};
+__device__ __forceinline__ uint4 keep_tokens8(uint4 v, int t0, int valid) {
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < 4; ++i) {
     const int ta = t0 + 2 * i;
     w[i] &= (ta < valid ? 0x0000ffffu : 0u) | (ta + 1 < valid ? 0xffff0000u : 0u);
   }
-  return make_uint2(w[0], w[1]);
+  return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// s_waitcnt with only vmcnt constrained (expcnt and lgkmcnt at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+// Workgroup barrier without the release fence __syncthreads adds (that fence would wait
+// for every outstanding global->LDS load); the memory clobber keeps the compiler from
+// moving LDS accesses across it.  Callers wait for what they need first.
+__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 __global__ void __launch_bounds__(256, 2) prefill_kernel(PreArgs a) {
-  __shared__ __attribute__((aligned(16))) char lds[2 * kStageBytes];
+  __shared__ __attribute__((aligned(1024))) char lds[kRing * kHalfBytes];
+  auto ring = [&](int t) { return lds + (t & (kRing - 1)) * kHalfBytes; };
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
 
   const int item = blockIdx.x >> 3, kvh = blockIdx.x & 7;
-  if (item >= a.meta[FQA_META_PRE_ITEMS]) return;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // the descriptor load does not wait for the count check (slots up to the grid bound
+  // are readable)
+  const int n_items = a.meta[FQA_META_PRE_ITEMS];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int4 it = *reinterpret_cast<const int4*>(a.items + 4 * (long long)item);
-  const int r = it.x, q0 = it.y, q1 = it.z, nkeys = it.w;
+  if (item >= n_items) return;
+  const int r = __builtin_amdgcn_readfirstlane(it.x), q0 = __builtin_amdgcn_readfirstlane(it.y);
+  const int q1 = __builtin_amdgcn_readfirstlane(it.z), nkeys = __builtin_amdgcn_readfirstlane(it.w);
   const int qs = a.cu[r];
   const int32_t* btr = a.bt + (long long)r * a.max_blocks;
-  const int nkb = (nkeys + kKT - 1) / kKT;
+  // The block tables are read-only for the kernel's lifetime: read them through the
+  // constant address space so the loads are scalar.
+  const __attribute__((address_space(4))) int32_t* btr_c =
+      (const __attribute__((address_space(4))) int32_t*)btr;
+  const int n_half = (nkeys + kHalfKeys - 1) / kHalfKeys;
+  const int n_pages = (nkeys + kPage - 1) / kPage;
 
   const int col = lane & 31, hf = lane >> 5;
   const int i_row = q0 + col;  // row within the request
   const bool row_ok = i_row < q1;
-  const int qpos = row_ok ? a.pos[qs + i_row] : -1;
-  const int min_pos = a.pos[qs + q0];  // first row: smallest position of the tile
+  // A request's new rows sit at positions computed .. computed+qlen-1 (the pack writes
+  // positions[] that way, scheduler.h:66-72), and n_keys = computed + q1.
+  const int computed = nkeys - q1;
+  const int qpos = row_ok ? computed + i_row : -1;
+  const int min_pos = computed + q0;  // first row: smallest position of the tile
   const int h = kvh * kG + w;
 
   bf16x8 qf[8];
@@ -118,175 +179,237 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PreArgs a) {
     for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
   float m_run = -1e30f, l_run = 0.f;
 
-  // ---- staging: per tile each thread moves 4 K chunks (16 B) and 2 V^T rows (32 B) ----
-  // K chunk i of thread t: page slot i, token t/16, dims (t%16)*8..; V^T row j: page slot
-  // 2j + t/128, dim t%128.
-  uint4 sk[4];
-  uint4 sv[2][2];
-  // Fast path: every page of the tile is full and in range (all but a workgroup's last
-  // tile, checked on scalar registers): plain loads, no masks.  Otherwise each page is
-  // loaded only if it exists and is in range, and tokens past n_keys are zeroed (their
-  // P is 0, and 0 x garbage must not become NaN in PV).
-  auto stage_load = [&](int kb) {
-    long long pg[kPagesPerTile];
-    bool fast = (kb + 1) * kKT <= nkeys;
+  // ---- staging ----
+  // Wave w moves page slot w/2 of each half: its K region (w even) or its V^T region
+  // (w odd), 4 KiB as four 1 KiB global->LDS loads.  Load q, lane i writes LDS bytes
+  // 16i.. of the region's q-th KiB, which hold
+  //   K:   token 4q + i/16, swizzle slot i%16  -> chunk (i%16) ^ token
+  //   V^T: row 32q + i/2,  swizzle slot i%2   -> chunk (i%2) ^ bit3(row)
+  // Page ids are scalar loads issued one half before their loads (one 64-byte
+  // scalar-cache line holds the ids of 8 halves).  Ids kept in VGPRs instead would be
+  // global loads, and the compiler would then wait for every outstanding global->LDS
+  // load before touching those registers.
+  const int st_ps = w >> 1, st_v = w & 1;
+  uint32_t st_off[4];  // byte offset inside the 8 KiB run of this lane's chunk, per load
 #pragma unroll
-    for (int ps = 0; ps < kPagesPerTile; ++ps) {
-      pg[ps] = fast ? btr[kb * kPagesPerTile + ps] : -1;
-      fast = fast && pg[ps] >= 0 && pg[ps] < a.pool_pages;
+  for (int qd = 0; qd < 4; ++qd) {
+    if (st_v) {
+      const int d = 32 * qd + (lane >> 1);
+      st_off[qd] = kVOff * 2 + d * 32 + (((lane & 1) ^ ((d >> 3) & 1)) << 4);
+    } else {
+      const int t = 4 * qd + (lane >> 4);
+      st_off[qd] = t * 256 + (((lane & 15) ^ t) << 4);
     }
-    if (fast) {
-#pragma unroll
-      for (int ps = 0; ps < kPagesPerTile; ++ps) {
-        const uint16_t* run = a.pool + run_offset(pg[ps], kvh);
-        sk[ps] = *reinterpret_cast<const uint4*>(run + tid * 8);
-      }
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int d = tid & 127;
-        const uint16_t* src = a.pool + run_offset(pg[2 * j + (tid >> 7)], kvh) + kVOff + d * kPage;
-        const uint4 lo = *reinterpret_cast<const uint4*>(src);
-        const uint4 hi = *reinterpret_cast<const uint4*>(src + 8);
-        // chunk 0 = tokens {0-3, 8-11}, chunk 1 = tokens {4-7, 12-15}
-        sv[j][0] = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        sv[j][1] = make_uint4(lo.z, lo.w, hi.z, hi.w);
-      }
-      return;
-    }
-#pragma unroll
-    for (int ps = 0; ps < kPagesPerTile; ++ps) {
-      const int pidx = kb * kPagesPerTile + ps;
-      const int valid = nkeys - pidx * kPage;  // tokens of this page that exist (may be <= 0)
-      const long long page = valid > 0 ? btr[pidx] : -1;
-      const bool ok = page >= 0 && page < a.pool_pages;
-      const uint16_t* run = a.pool + run_offset(ok ? page : 0, kvh);
-      const int tk = tid >> 4;
-      uint4 v = *reinterpret_cast<const uint4*>(run + tid * 8);
-      const bool keep = ok && tk < valid;
-      sk[ps] = keep ? v : make_uint4(0, 0, 0, 0);
-      if ((ps >> 1) * 2 + (tid >> 7) == ps) {  // this thread's V^T row lives in page ps
-        const int j = ps >> 1, d = tid & 127;
-        const uint16_t* vr = run + kVOff + d * kPage;
-        uint4 lo = *reinterpret_cast<const uint4*>(vr);
-        uint4 hi = *reinterpret_cast<const uint4*>(vr + 8);
-        if (!ok) lo = hi = make_uint4(0, 0, 0, 0);
-        if (valid < kPage) {
-          uint2 a0 = keep_tokens(make_uint2(lo.x, lo.y), 0, valid);
-          uint2 a1 = keep_tokens(make_uint2(lo.z, lo.w), 4, valid);
-          uint2 b0 = keep_tokens(make_uint2(hi.x, hi.y), 8, valid);
-          uint2 b1 = keep_tokens(make_uint2(hi.z, hi.w), 12, valid);
-          lo = make_uint4(a0.x, a0.y, a1.x, a1.y);
-          hi = make_uint4(b0.x, b0.y, b1.x, b1.y);
-        }
-        sv[j][0] = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        sv[j][1] = make_uint4(lo.z, lo.w, hi.z, hi.w);
-      }
-    }
+  }
+  // Valid tokens (0..16) of the two page slots of the half in each ring buffer, 5 bits
+  // per (buffer, slot); 0 also marks a page id outside the pool.
+  unsigned long long pvbits = 0;
+  auto pv = [&](int R, int ps) { return (int)((pvbits >> ((R * 2 + ps) * 5)) & 31); };
+
+  struct Ids { int id[2]; };
+  auto load_ids = [&](int hx) {
+    Ids x;
+    x.id[0] = btr_c[2 * hx];
+    x.id[1] = btr_c[min(2 * hx + 1, n_pages - 1)];
+    return x;
   };
-  auto stage_store = [&](int buf) {
-    char* base = lds + buf * kStageBytes;
-    const int tk = tid >> 4, cc = tid & 15;
+  // Where this wave's loads of half `hx` (page ids `ids`) come from and go to; records
+  // the half's valid counts.
+  struct Dma { const uint16_t* run; uint32_t dst; };
+  auto stage_prep = [&](int hx, const Ids& ids) {
+    const int R = hx & (kRing - 1);
+    const int* id2 = ids.id;
+    Dma dm;
 #pragma unroll
-    for (int ps = 0; ps < kPagesPerTile; ++ps)
-      *reinterpret_cast<uint4*>(base + lds_k(ps, tk, cc)) = sk[ps];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int ps = 2 * j + (tid >> 7), d = tid & 127;
-      *reinterpret_cast<uint4*>(base + lds_v(ps, d, 0)) = sv[j][0];
-      *reinterpret_cast<uint4*>(base + lds_v(ps, d, 1)) = sv[j][1];
+    for (int ps = 0; ps < 2; ++ps) {
+      const int pidx = 2 * hx + ps;
+      const long long id = id2[ps];
+      const int valid = min(max(nkeys - pidx * kPage, 0), kPage);
+      const bool ok = valid > 0 && id >= 0 && id < a.pool_pages;
+      const int sh = (R * 2 + ps) * 5;
+      pvbits = (pvbits & ~(31ull << sh)) | ((unsigned long long)(ok ? valid : 0) << sh);
+      // Every wave issues exactly 4 loads per half (a bad page reads page 0, zeroed
+      // later), so the vmcnt counts in half_step hold.
+      if (ps == st_ps) {
+        dm.run = a.pool + run_offset(ok ? id : 0, kvh);
+        dm.dst = lds_base + R * kHalfBytes + st_ps * kRunBytes + st_v * (kVOff * 2);
+      }
     }
+    return dm;
+  };
+  auto stage_issue = [&](int hx, const Ids& ids) {
+    const Dma dm = stage_prep(hx, ids);
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) dma16(dm.run, st_off[qd], dm.dst + qd * 1024);
+  };
+  // Zero what must not count in ring buffer R: V^T tokens past a page's valid count, and
+  // all of K for a page that is missing or outside the pool.  Runs after the barrier
+  // that publishes the buffer's loads; ends with a barrier of its own.
+  auto stage_fix = [&](int hx) {
+    const int R = hx & (kRing - 1);
+    if (pv(R, 0) == kPage && pv(R, 1) == kPage) return;  // uniform
+    char* base = ring(hx);
+    const int ps = tid >> 7, d = tid & 127;
+    const int valid = pv(R, ps);
+    uint4* p0 = reinterpret_cast<uint4*>(base + lds_v(ps, d, 0));
+    uint4* p1 = reinterpret_cast<uint4*>(base + lds_v(ps, d, 1));
+    const uint4 v0 = *p0, v1 = *p1;  // both reads before any write
+    *p0 = keep_tokens8(v0, 0, valid);
+    *p1 = keep_tokens8(v1, 8, valid);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int c = tid * 2 + k, kps = c >> 8;  // 256 K chunks per page
+      if (pv(R, kps) == 0) *reinterpret_cast<uint4*>(base + kps * kRunBytes + (c & 255) * 16) = make_uint4(0, 0, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    barrier();
   };
 
-  stage_load(0);
-  stage_store(0);
-  __syncthreads();
+  // K fragment of S^T MFMA step ks: MFMA row `col` = key perm(col) of the half:
+  // page slot col/16, token bit3(col)*4 | bit2(col)*8 | col%4.
+  const int kf_tok = (col & 3) | (((col >> 2) & 1) << 3) | (((col >> 3) & 1) << 2);
+  auto kfrag = [&](const char* base, int ks) {
+    return *reinterpret_cast<const bf16x8*>(base + lds_k(col >> 4, kf_tok, ks * 2 + hf));
+  };
+  auto s_tile = [&](const char* base) {
+    float16_t s;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfrag(base, ks), qf[ks], s, 0, 0, 0);
+    return s;
+  };
 
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int buf = kb & 1;
-    if (kb + 1 < nkb) stage_load(kb + 1);
-    const char* base = lds + buf * kStageBytes;
-    // Both halves' S^T = K Q^T first, so half 0's softmax (VALU) runs while half 1's
-    // MFMAs execute, and half 1's softmax while half 0's PV MFMAs execute.
-    const bool live1 = kb * kKT + 32 < nkeys;  // second half has keys (wave-uniform)
-    float16_t s2[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      if (j == 1 && !live1) break;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s2[j][i] = 0.f;
-      const int ps = j * 2 + (col >> 4), t = col & 15;
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(base + lds_k(ps, t, ks * 2 + hf));
-        s2[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s2[j], 0, 0, 0);
-      }
+  float16_t s_cur;
+  Ids ids_next;  // page ids of the next half to issue
+  // One pipeline step: half t lives in ring buffer t % kRing.  kNext: a half follows.
+  auto half_step = [&](int t, auto next_tag) {
+    constexpr bool kNext = decltype(next_tag)::value;
+    // B(t): half t+1's loads have landed in every wave, and every wave has finished
+    // reading buffer R3 (half t-1).
+    if (t + 2 < n_half) wait_vm<4>(); else wait_vm<0>();
+    barrier();
+    if (t + kAhead < n_half) {
+      stage_issue(t + kAhead, ids_next);
+      if (t + kAhead + 1 < n_half) ids_next = load_ids(t + kAhead + 1);
     }
+    if (kNext) stage_fix(t + 1);
+
+    // online softmax of half t over this lane's query row: mask (diagonal halves only),
+    // row max, lazy rescale.  Element v of S^T: MFMA row (v/4)*8 + hf*4 + v%4, i.e. key
+    // (v/8)*16 + hf*8 + ((v/4)%2)*4 + v%4 of the half.
+    const int key0 = t * kHalfKeys;
+    float mx = -INFINITY;
+    if (key0 + kHalfKeys - 1 > min_pos) {  // the causal diagonal (or n_keys) crosses these keys
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {  // two 32-key halves of the tile
-      if (j == 1 && !live1) break;
-      const int key0 = kb * kKT + j * 32;
-      float16_t& s = s2[j];
-      // online softmax over this lane's query row
-      float mx = -INFINITY;
-      if (key0 + 31 > min_pos) {  // the causal diagonal crosses these keys
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int key = key0 + (v >> 2) * 8 + hf * 4 + (v & 3);
-          if (key > qpos) s[v] = -INFINITY;
-          mx = fmaxf(mx, s[v]);
-        }
-      } else {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[v]);
+      for (int v = 0; v < 16; ++v) {
+        const int key = key0 + (v >> 3) * 16 + hf * 8 + ((v >> 2) & 1) * 4 + (v & 3);
+        if (key > qpos) s_cur[v] = -INFINITY;
+        mx = fmaxf(mx, s_cur[v]);
       }
-      mx = max_xor32(mx);
-      // Lazy rescale: the reference max only moves when the row max grows by more than
-      // 2^kRescale, so P = exp2(s*scale - m) stays <= 2^kRescale and O, l are rescaled
-      // on few tiles instead of every tile.
-      const float m_new = fmaxf(m_run, mx * a.scale_log2);
-      const bool grow = m_new > m_run + kRescale;
-      if (__builtin_amdgcn_ballot_w64(grow)) {  // wave-uniform: skipped on most tiles
-        const float corr = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-        l_run *= corr;
+    } else {
 #pragma unroll
-        for (int db = 0; db < 4; ++db) o[db] *= corr;
-        m_run = grow ? m_new : m_run;
-      }
-      bf16x8 pt[2];
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s_cur[v]);
+    }
+    mx = max_xor32(mx);
+    // Lazy rescale: the reference max only moves when the row max grows by more than
+    // 2^kRescale, so P = exp2(s*scale - m) stays <= 2^kRescale and O, l are rescaled
+    // on few halves instead of every one.
+    const float m_new = fmaxf(m_run, mx * a.scale_log2);
+    const bool grow = m_new > m_run + kRescale;
+    if (__builtin_amdgcn_ballot_w64(grow)) {  // wave-uniform: skipped on most halves
+      const float corr = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+      l_run *= corr;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o[db] *= corr;
+      m_run = grow ? m_new : m_run;
+    }
+
+    // phase 1: P^T = exp2(S^T*scale - m) as bf16 and l += row sums of the same bf16 P,
+    // interleaved with the S^T MFMAs of half t+1 and the V^T fragment reads of half t
+    const char* base = ring(t);
+    bf16x8 vf[2][4];
+    bf16x8 pt[2];
+    float16_t s_nxt;
+    auto softmax_exp = [&]() {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         // raw v_exp_f32: results below 2^-126 flush to 0, which a softmax weight can be
-        const float p = __builtin_amdgcn_exp2f(fmaf(s[v], a.scale_log2, -m_run));
+        const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[v], a.scale_log2, -m_run));
         pt[v >> 3][v & 7] = (__bf16)p;
       }
-      // l sums the same bf16 P that multiplies V (one v_dot2 per pair instead of one add
-      // per score), so the output weights are normalised exactly
-      {
-        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-        const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+      typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+      const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc)
+      for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const bf16x2_t pr = {pt[kc][2 * e], pt[kc][2 * e + 1]};
-            l_run = __builtin_amdgcn_fdot2_f32_bf16(pr, one, l_run, false);
-          }
-      }
-      // O^T += V^T P^T over the two pages (16 keys each) of this half
-#pragma unroll
-      for (int kc = 0; kc < 2; ++kc) {
-        const int ps = j * 2 + kc;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-          const bf16x8 vf =
-              *reinterpret_cast<const bf16x8*>(base + lds_v(ps, db * 32 + col, hf));
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pt[kc], o[db], 0, 0, 0);
+        for (int e = 0; e < 4; ++e) {
+          const bf16x2_t pr = {pt[kc][2 * e], pt[kc][2 * e + 1]};
+          l_run = __builtin_amdgcn_fdot2_f32_bf16(pr, one, l_run, false);
         }
+    };
+    auto read_v = [&]() {
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+          vf[kc][db] = *reinterpret_cast<const bf16x8*>(base + lds_v(kc, db * 32 + col, hf));
+    };
+    if constexpr (kNext) {
+      // four groups, each: 2 S^T MFMAs of half t+1, 4 exps, 2 V^T fragment reads
+      const char* nb = ring(t + 1);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s_nxt[i] = 0.f;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+#pragma unroll
+        for (int ks = 2 * g; ks < 2 * g + 2; ++ks)
+          s_nxt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfrag(nb, ks), qf[ks], s_nxt, 0, 0, 0);
+#pragma unroll
+        for (int v = 4 * g; v < 4 * g + 4; ++v) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[v], a.scale_log2, -m_run));
+          pt[v >> 3][v & 7] = (__bf16)p;
+        }
+#pragma unroll
+        for (int db = (g & 1) * 2; db < (g & 1) * 2 + 2; ++db)
+          vf[g >> 1][db] = *reinterpret_cast<const bf16x8*>(base + lds_v(g >> 1, db * 32 + col, hf));
       }
+      typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+      const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bf16x2_t pr = {pt[kc][2 * e], pt[kc][2 * e + 1]};
+          l_run = __builtin_amdgcn_fdot2_f32_bf16(pr, one, l_run, false);
+        }
+    } else {
+      read_v();
+      softmax_exp();
     }
-    if (kb + 1 < nkb) stage_store(buf ^ 1);
-    __syncthreads();
-  }
+    // phase 2: O^T += V^T P^T over the two pages (16 keys each) of half t
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[kc][db], pt[kc], o[db], 0, 0, 0);
+    if constexpr (kNext) s_cur = s_nxt;
+  };
+
+  // prologue: halves 0..2 in flight, half 0 published and fixed, S^T of half 0
+  ids_next = load_ids(0);
+  stage_issue(0, ids_next);
+  if (n_half > 1) stage_issue(1, load_ids(1));
+  if (n_half > 2) stage_issue(2, load_ids(2));
+  if (n_half > kAhead) ids_next = load_ids(kAhead);
+  if (n_half > 2) wait_vm<8>(); else if (n_half > 1) wait_vm<4>(); else wait_vm<0>();
+  barrier();
+  stage_fix(0);
+  s_cur = s_tile(ring(0));
+
+  for (int t = 0; t + 1 < n_half; ++t) half_step(t, std::true_type{});
+  half_step(n_half - 1, std::false_type{});
 
   if (!row_ok) return;
   const auto lr = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run),
