@@ -10,8 +10,8 @@
 //  * One 256-thread workgroup per (32 query rows, kv head); wave w owns query head w of
 //    the kv head.  The 4 heads share every K/V tile, staged into LDS once (the
 //    reference runs one block per query head and re-reads K/V 4x, attn_cute.cu:157).
-//    Two workgroups share a CU, so one wave's MFMAs overlap another's softmax on every
-//    SIMD.
+//    Three workgroups share a CU (168 VGPRs, 48 KiB LDS each), so on every SIMD one
+//    wave's MFMAs overlap the others' softmax and waits.
 //  * Transposed FA-2 on v_mfma_f32_32x32x16_bf16:
 //        S^T[32 keys x 32 rows] = K[32 x 128] . Q^T[128 x 32]   (8 MFMAs per 32 keys)
 //        O^T[128 x 32 rows]    += V^T[128 x 16 keys] . P^T      (4 MFMAs per 16 keys)
@@ -28,8 +28,8 @@
 //  * Software pipeline over 32-key halves: half t's exp/convert/sum is interleaved with
 //    the S^T MFMAs of half t+1 and the LDS reads of half t's V fragments, then half t's
 //    PV MFMAs issue back to back.
-//  * K/V staging is direct global->LDS (global_load_lds_dwordx4): a ring of four 16 KiB
-//    buffers, one 32-key half (two 8 KiB page runs) each, filled three halves ahead.
+//  * K/V staging is direct global->LDS (global_load_lds_dwordx4): a ring of three 16 KiB
+//    buffers, one 32-key half (two 8 KiB page runs) each, filled two halves ahead.
 //    Each wave moves one 4 KiB region (K or V^T of one page) per half; every lane picks
 //    the global chunk that lands in its slot of the XOR-swizzled layout, so fragment
 //    reads are conflict-free 16-byte reads and no VGPR carries staged data.  The loads
@@ -49,7 +49,7 @@ constexpr int kQT = 32;          // query rows per workgroup
 constexpr int kHalfKeys = 32;    // keys per pipeline step (2 pages)
 constexpr int kRunBytes = kRunElems * 2;       // 8 KiB: one (page, kv head) run
 constexpr int kHalfBytes = 2 * kRunBytes;      // 16 KiB LDS buffer
-constexpr int kRing = 4;                       // LDS buffers
+constexpr int kRing = 3;                       // LDS buffers
 constexpr int kAhead = kRing - 1;              // halves loaded ahead of the current one
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescale = 8.0f;  // lazy-rescale threshold (log2 units)
@@ -126,9 +126,9 @@ __device__ __forceinline__ void wait_vm() {
 // moving LDS accesses across it.  Callers wait for what they need first.
 __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-__global__ void __launch_bounds__(256, 2) prefill_kernel(PreArgs a) {
+__global__ void __launch_bounds__(256, 3) prefill_kernel(PreArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[kRing * kHalfBytes];
-  auto ring = [&](int t) { return lds + (t & (kRing - 1)) * kHalfBytes; };
+  auto ring = [&](int t) { return lds + (t % kRing) * kHalfBytes; };
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
 
   const int item = blockIdx.x >> 3, kvh = blockIdx.x & 7;
@@ -217,7 +217,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PreArgs a) {
   // the half's valid counts.
   struct Dma { const uint16_t* run; uint32_t dst; };
   auto stage_prep = [&](int hx, const Ids& ids) {
-    const int R = hx & (kRing - 1);
+    const int R = hx % kRing;
     const int* id2 = ids.id;
     Dma dm;
 #pragma unroll
@@ -246,7 +246,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PreArgs a) {
   // all of K for a page that is missing or outside the pool.  Runs after the barrier
   // that publishes the buffer's loads; ends with a barrier of its own.
   auto stage_fix = [&](int hx) {
-    const int R = hx & (kRing - 1);
+    const int R = hx % kRing;
     if (pv(R, 0) == kPage && pv(R, 1) == kPage) return;  // uniform
     char* base = ring(hx);
     const int ps = tid >> 7, d = tid & 127;
@@ -288,7 +288,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PreArgs a) {
     constexpr bool kNext = decltype(next_tag)::value;
     // B(t): half t+1's loads have landed in every wave, and every wave has finished
     // reading buffer R3 (half t-1).
-    if (t + 2 < n_half) wait_vm<4>(); else wait_vm<0>();
+    if (t + kAhead - 1 < n_half) wait_vm<(kAhead - 2) * 4>(); else wait_vm<0>();
     barrier();
     if (t + kAhead < n_half) {
       stage_issue(t + kAhead, ids_next);
@@ -300,17 +300,21 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PreArgs a) {
     // row max, lazy rescale.  Element v of S^T: MFMA row (v/4)*8 + hf*4 + v%4, i.e. key
     // (v/8)*16 + hf*8 + ((v/4)%2)*4 + v%4 of the half.
     const int key0 = t * kHalfKeys;
-    float mx = -INFINITY;
     if (key0 + kHalfKeys - 1 > min_pos) {  // the causal diagonal (or n_keys) crosses these keys
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int key = key0 + (v >> 3) * 16 + hf * 8 + ((v >> 2) & 1) * 4 + (v & 3);
         if (key > qpos) s_cur[v] = -INFINITY;
-        mx = fmaxf(mx, s_cur[v]);
       }
-    } else {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s_cur[v]);
+    }
+    float mx;
+    {  // max3 tree, depth 3
+      const float m0 = fmaxf(fmaxf(s_cur[0], s_cur[1]), s_cur[2]);
+      const float m1 = fmaxf(fmaxf(s_cur[3], s_cur[4]), s_cur[5]);
+      const float m2 = fmaxf(fmaxf(s_cur[6], s_cur[7]), s_cur[8]);
+      const float m3 = fmaxf(fmaxf(s_cur[9], s_cur[10]), s_cur[11]);
+      const float m4 = fmaxf(fmaxf(s_cur[12], s_cur[13]), s_cur[14]);
+      mx = fmaxf(fmaxf(fmaxf(m0, m1), m2), fmaxf(fmaxf(m3, m4), s_cur[15]));
     }
     mx = max_xor32(mx);
     // Lazy rescale: the reference max only moves when the row max grows by more than
@@ -400,10 +404,10 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PreArgs a) {
   // prologue: halves 0..2 in flight, half 0 published and fixed, S^T of half 0
   ids_next = load_ids(0);
   stage_issue(0, ids_next);
-  if (n_half > 1) stage_issue(1, load_ids(1));
-  if (n_half > 2) stage_issue(2, load_ids(2));
+  for (int hx = 1; hx < kAhead; ++hx)
+    if (hx < n_half) stage_issue(hx, load_ids(hx));
   if (n_half > kAhead) ids_next = load_ids(kAhead);
-  if (n_half > 2) wait_vm<8>(); else if (n_half > 1) wait_vm<4>(); else wait_vm<0>();
+  if (n_half >= kAhead) wait_vm<(kAhead - 1) * 4>(); else wait_vm<0>();
   barrier();
   stage_fix(0);
   s_cur = s_tile(ring(0));
