@@ -138,6 +138,7 @@ __global__ void __launch_bounds__(256, 3) prefill_kernel(PreArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int4 it = *reinterpret_cast<const int4*>(a.items + 4 * (long long)item);
+  asm volatile("" ::"s"(it.x), "s"(it.w), "s"(n_items));  // both loads before the check
   if (item >= n_items) return;
   const int r = __builtin_amdgcn_readfirstlane(it.x), q0 = __builtin_amdgcn_readfirstlane(it.y);
   const int q1 = __builtin_amdgcn_readfirstlane(it.z), nkeys = __builtin_amdgcn_readfirstlane(it.w);

@@ -11,12 +11,15 @@
 // norm weights loaded once: lane j holds dims [4j, 4j+4) and [64+4j, 64+4j+4), so both
 // halves of every rotate-half pair sit in one lane and RoPE needs no data exchange; the
 // sum of squares is a 16-lane butterfly.  q is written back in place, k into its page.
-// The row's 8 v heads are split over the W waves and copied into the V^T
-// [dim][16 tokens] rows of the page.  Those are 2-byte writes, so the 16 rows of a page
-// must meet in one L2 before the line goes to HBM: workgroup b runs on XCD b % 8, and
-// rows are dealt to XCDs in contiguous ranges, so a page's rows (except where a range
-// ends) go through the same XCD's L2.  (Dealing rows round-robin spread each page over
-// all 8 L2s and more than doubled the bytes written to HBM.)
+// V goes into the V^T [dim][16 tokens] rows of the page.  When 16 consecutive rows fill
+// one page (every full page of a prefill), the page's first row writes the whole page:
+// per kv head each lane reads one 4-byte word (2 dims) of each of the 16 rows, transposes
+// in registers (v_perm) and stores its two 32-byte V^T rows, so the 4 KiB go out as
+// contiguous 16-byte stores; the other 15 rows skip V.  Rows of a partly filled page
+// (decode rows, the ends of a chunk) write their column with 2-byte stores, split over
+// the W waves; those must meet in one L2 before the line goes to HBM: workgroup b runs
+// on XCD b % 8 and rows are dealt to XCDs in contiguous ranges, so a page's rows (except
+// where a range ends) go through the same XCD's L2.
 // Memory-bound: per row 12 KiB read, 8 KiB (q) + 4 KiB (k, v) written.
 //
 #include "fqa_common.h"
@@ -123,11 +126,49 @@ __global__ void __launch_bounds__(256) qknorm_rope_append_kernel(AppendArgs a) {
     }
   }
 
-  // ---- v heads sw*NKV .. : lane -> (kv head, DPL consecutive dims) --------------------
+  // ---- v ------------------------------------------------------------------------------
+  if (!page_ok) return;
+  // Full page: rows lead..lead+15 hold this page's tokens 0..15 (their slots are
+  // distinct and consecutive, so checking the first and the last suffices), and every
+  // one of them has a table row (positions run consecutively within a request).
+  const int lead = row - tok;
+  bool full = lead >= 0 && lead + kPage <= T;
+  if (full) {
+    const int base_slot = slot - tok;
+    full = a.slots[lead] == base_slot && a.slots[lead + kPage - 1] == base_slot + kPage - 1 &&
+           a.positions[lead] >= 0 && a.positions[lead + kPage - 1] < a.rope_max_pos;
+  }
+  if (full) {
+    if (tok != 0) return;  // the page's first row writes it
+    // kv heads sw*NKV ..: lane -> dims 2*lane, 2*lane+1 of all 16 tokens
+    const uint16_t* vsrc = a.qkv + (long long)row * a.stride + (kHq + kHkv) * kD + 2 * lane;
+#pragma unroll
+    for (int hv = 0; hv < NKV; ++hv) {
+      const int kvh = sw * NKV + hv;
+      if (kvh >= kHkv) break;
+      uint32_t x[kPage];
+#pragma unroll
+      for (int t = 0; t < kPage; ++t)
+        x[t] = *reinterpret_cast<const uint32_t*>(vsrc + (long long)t * a.stride + kvh * kD);
+      uint32_t y0[8], y1[8];  // dim 2*lane / 2*lane+1, tokens 2k, 2k+1
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        y0[k] = __builtin_amdgcn_perm(x[2 * k + 1], x[2 * k], 0x05040100u);
+        y1[k] = __builtin_amdgcn_perm(x[2 * k + 1], x[2 * k], 0x07060302u);
+      }
+      uint4* vt = reinterpret_cast<uint4*>(a.pool + run_offset(page, kvh) + kVOff + 2 * lane * kPage);
+      vt[0] = make_uint4(y0[0], y0[1], y0[2], y0[3]);
+      vt[1] = make_uint4(y0[4], y0[5], y0[6], y0[7]);
+      vt[2] = make_uint4(y1[0], y1[1], y1[2], y1[3]);
+      vt[3] = make_uint4(y1[4], y1[5], y1[6], y1[7]);
+    }
+    return;
+  }
+  // Partly filled page: v heads sw*NKV .. : lane -> (kv head, DPL consecutive dims)
   constexpr int LPK = kWave / NKV;   // lanes per v head
   constexpr int DPL = kD / LPK;      // dims per lane (2, 4 or 16)
   const int kvh = sw * NKV + lane / LPK, d0 = (lane % LPK) * DPL;
-  if (!page_ok || kvh >= kHkv) return;
+  if (kvh >= kHkv) return;
   const uint16_t* vs = src + (kHq + kHkv + kvh) * kD + d0;
   uint32_t wv[DPL / 2];
 #pragma unroll
