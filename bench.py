@@ -46,6 +46,9 @@ def parse():
     ap.add_argument("--dec-min-pages", type=int, default=8)
     ap.add_argument("--pre-tile-q", type=int, default=32, choices=[32])
     ap.add_argument("--layers", type=int, default=None, help="config 5 only (default 36)")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="only copy 1 GiB device to device 3 times (the reference dispatch "
+                         "that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only run the per-kernel graphs (for rocprofv3 passes)")
     return ap.parse_args()
@@ -59,6 +62,16 @@ def main():
                           "per-GPU work (kv-head or sequence sharding needs no exchange); "
                           "run with --gpus 1"}))
         sys.exit(2)
+    if args.copy_calib:
+        import torch
+
+        x = torch.ones(2**28, device="cuda", dtype=torch.float32)
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes": x.numel() * 4, "copies": 3}))
+        return
 
     import torch
 
@@ -197,17 +210,23 @@ def main():
         bt_bytes = int(meta[9]) * 4
         bytes_per = logical + bt_bytes
         achieved = bytes_per / (kern_ms["decode"] * 1e-3) / 1e9
-        roof = {"kernel": "decode (fqa_decode: split-K + combine)", "bound": "hbm",
+        traffic, tsrc = _profile_traffic(args.config,
+                                         ["decode_split_kernel", "decode_combine_kernel"])
+        roof = {"kernel": "fqa_decode (decode_split_kernel + decode_combine_kernel)",
+                "bound": "hbm",
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "traffic_source": tsrc,
                 "bytes_per_launch": bytes_per, "unique_kv_bytes": unique,
                 "launch_us": round(kern_ms["decode"] * 1e3, 2)}
     else:
         flops = synth.prefill_flops(comp_sel, n_sel)
         achieved = flops / (kern_ms["prefill"] * 1e-3) / 1e12
-        roof = {"kernel": "prefill (fqa_prefill)", "bound": "mfma",
+        traffic, tsrc = _profile_traffic(args.config, ["prefill_kernel"])
+        roof = {"kernel": "fqa_prefill (prefill_kernel)", "bound": "mfma",
                 "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": traffic,
+                "traffic_source": tsrc,
                 "flops_per_launch": flops, "launch_us": round(kern_ms["prefill"] * 1e3, 2)}
         if has_decode:
             logical, _ = synth.decode_bytes(_selected(cfg, comp_sel, n_sel))
@@ -244,6 +263,21 @@ def main():
         "wall_s_timed": round(wall, 3),
     }
     print(json.dumps(line))
+
+
+def _profile_traffic(config: int, kernels: list[str]):
+    """HBM bytes per launch of `kernels` (summed) from the committed rocprofv3 summary of
+    this config (profiles/*_config<N>.txt, calibrated FETCH_SIZE + WRITE_SIZE), or None."""
+    prof = Path(__file__).resolve().parent / "profiles"
+    for f in sorted(prof.glob(f"*_config{config}.txt")):
+        got = {}
+        for line in f.read_text().splitlines():
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic_bytes":
+                got[parts[1]] = int(parts[2])
+        if all(k in got for k in kernels):
+            return sum(got[k] for k in kernels), f"profiles/{f.name}"
+    return None, None
 
 
 def _selected(cfg, comp_sel, n_sel):
