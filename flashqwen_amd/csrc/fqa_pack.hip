@@ -286,25 +286,32 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   // Tile t of prefill request r covers rows [t*QT, min((t+1)*QT, n)) and needs
   // c + min((t+1)*QT, n) keys, so per request the number of tiles with more keys than X
   // (and with exactly X) has a closed form; an item's rank is a sum over requests.
-  for (int i = blockIdx.x + tid * gridDim.x; i < npi; i += gsz) {
-    const int r = upper_index(s_preit, R, i);  // the prefill request owning item i
-    const int t = i - s_preit[r];
-    const int n = s_n[r], c = s_comp[r];
-    const int q0 = t * QT, q1 = min(q0 + QT, n);
-    const int X = c + q1;
-    int rank = 0;
-    for (int rr = 0; rr < R; ++rr) {
-      const int nt = s_preit[rr + 1] - s_preit[rr];
-      if (nt == 0) continue;  // decode request or empty prefill
-      const int cc = s_comp[rr], nn = s_n[rr], y = X - cc;
-      const int k = y < 0 ? 0 : y / QT;
-      rank += (cc + nn > X) + max(0, nt - 1 - k);  // tiles with more keys than X
-      // tiles with exactly X keys that come earlier in (request, tile) order
-      const int te = (y > 0 && y % QT == 0 && y / QT - 1 < nt - 1) ? y / QT - 1
-                     : (cc + nn == X ? nt - 1 : -1);
-      if (te >= 0 && (rr < r || (rr == r && te < t))) ++rank;
+  // One wave per item, the lanes splitting the requests; QT is a power of two.
+  {
+    const int lane = tid & (kWave - 1), wv = tid >> 6;
+    const int qsh = QT == 32 ? 5 : (QT == 64 ? 6 : 7);
+    for (int i = blockIdx.x + wv * gridDim.x; i < npi; i += gridDim.x * kPackWaves) {
+      const int r = upper_index(s_preit, R, i);  // the prefill request owning item i
+      const int t = i - s_preit[r];
+      const int n = s_n[r], c = s_comp[r];
+      const int q0 = t * QT, q1 = min(q0 + QT, n);
+      const int X = c + q1;
+      int rank = 0;
+      for (int rr = lane; rr < R; rr += kWave) {
+        const int nt = s_preit[rr + 1] - s_preit[rr];
+        if (nt == 0) continue;  // decode request or empty prefill
+        const int cc = s_comp[rr], nn = s_n[rr], y = X - cc;
+        const int k = y < 0 ? 0 : y >> qsh;
+        rank += (cc + nn > X) + max(0, nt - 1 - k);  // tiles with more keys than X
+        // tiles with exactly X keys that come earlier in (request, tile) order
+        const int te = (y > 0 && (y & (QT - 1)) == 0 && (y >> qsh) - 1 < nt - 1) ? (y >> qsh) - 1
+                       : (cc + nn == X ? nt - 1 : -1);
+        if (te >= 0 && (rr < r || (rr == r && te < t))) ++rank;
+      }
+      rank = __builtin_amdgcn_readlane(wave_incl_scan(rank), kWave - 1);
+      if (lane == 0)
+        *reinterpret_cast<int4*>(a.o.pre_items + 4 * (long long)rank) = make_int4(r, q0, q1, X);
     }
-    *reinterpret_cast<int4*>(a.o.pre_items + 4 * (long long)rank) = make_int4(r, q0, q1, X);
   }
 
   if (blockIdx.x != 0) return;
@@ -323,10 +330,12 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     if (i >= nd) a.o.decode_rids[i] = -1;
     if (i >= np) a.o.prefill_rids[i] = -1;
   }
-  // page-id range check over the concatenated tables: 16-byte loads, 4 in flight per
-  // thread (the scalar head and tail are the at most 3 ids on either side of alignment)
+  // page-id range check over the concatenated tables: 16-byte loads, kPgVec in flight
+  // per thread so most batches take one round trip (the scalar head and tail are the at
+  // most 3 ids on either side of alignment)
   int bad = 0;
   {
+    constexpr int kPgVec = 12;
     const int32_t* pg = a.b.bt_pages + s_btoff[0];
     const int npages = s_btoff[R] - s_btoff[0];
     const int lead = min(npages, (int)(((16 - ((uintptr_t)pg & 15)) & 15) >> 2));
@@ -336,15 +345,16 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     auto badv = [&](int v) { return v < 0 || (long long)v >= np64; };
     for (int e = tid; e < lead; e += kPackThreads) bad |= badv(pg[e]);
     for (int e = lead + 4 * nvec + tid; e < npages; e += kPackThreads) bad |= badv(pg[e]);
-    for (int base = 0; base < nvec; base += 4 * kPackThreads) {
-      int4 v[4];
+    for (int base = 0; base < nvec; base += kPgVec * kPackThreads) {
+      int4 v[kPgVec];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kPgVec; ++u) {
         const int e = base + u * kPackThreads + tid;
         v[u] = e < nvec ? pv[e] : make_int4(0, 0, 0, 0);
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) bad |= (int)badv(v[u].x) | (int)badv(v[u].y) | (int)badv(v[u].z) | (int)badv(v[u].w);
+      for (int u = 0; u < kPgVec; ++u)
+        bad |= (int)badv(v[u].x) | (int)badv(v[u].y) | (int)badv(v[u].z) | (int)badv(v[u].w);
     }
   }
   bad = block_max(bad, sh32);
