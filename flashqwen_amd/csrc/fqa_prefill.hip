@@ -93,10 +93,10 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t l
   dma16_if(1u, base, off, lds);
 }
 
-// LDS byte offset of K chunk (16 B = 8 dims) `c` of token `t` in page slot `ps`.
-__device__ __forceinline__ int lds_k(int ps, int t, int c) {
-  return ps * kRunBytes + t * 256 + ((c ^ t) << 4);
-}
+// K layout in a page slot's LDS run, chunk-major: chunk (16 B = 8 dims) c of token t at
+// byte c*256 + t*16.  The 16 tokens' reads of one chunk are 256 consecutive bytes (no bank
+// conflict), and a lane's 8 K-fragment reads differ only by the constant ks*512.
+__device__ __forceinline__ int lds_k(int ps, int t, int c) { return ps * kRunBytes + c * 256 + t * 16; }
 // LDS byte offset of V^T chunk `h` (tokens 8h..8h+7) of dim row `d` in page slot `ps`.
 // The swizzle h ^ bit3(d) keeps the 16-byte reads of 16 consecutive rows on distinct
 // banks.
@@ -184,7 +184,7 @@ __global__ void __launch_bounds__(256, 3) prefill_kernel(PreArgs a) {
   // Wave w moves page slot w/2 of each half: its K region (w even) or its V^T region
   // (w odd), 4 KiB as four 1 KiB global->LDS loads.  Load q, lane i writes LDS bytes
   // 16i.. of the region's q-th KiB, which hold
-  //   K:   token 4q + i/16, swizzle slot i%16  -> chunk (i%16) ^ token
+  //   K:   chunk 4q + i/16 of token i%16
   //   V^T: row 32q + i/2,  swizzle slot i%2   -> chunk (i%2) ^ bit3(row)
   // Page ids are scalar loads issued one half before their loads (one 64-byte
   // scalar-cache line holds the ids of 8 halves).  Ids kept in VGPRs instead would be
@@ -198,8 +198,8 @@ __global__ void __launch_bounds__(256, 3) prefill_kernel(PreArgs a) {
       const int d = 32 * qd + (lane >> 1);
       st_off[qd] = kVOff * 2 + d * 32 + (((lane & 1) ^ ((d >> 3) & 1)) << 4);
     } else {
-      const int t = 4 * qd + (lane >> 4);
-      st_off[qd] = t * 256 + (((lane & 15) ^ t) << 4);
+      // global [16 tokens][128 dims]: token t's chunk c at t*256 + c*16
+      st_off[qd] = (lane & 15) * 256 + (4 * qd + (lane >> 4)) * 16;
     }
   }
   // Valid tokens (0..16) of the two page slots of the half in each ring buffer, 5 bits
