@@ -69,28 +69,16 @@ struct PreArgs {
   float scale_log2;
 };
 
-// One 16-byte-per-lane global->LDS load when `go` != 0: lane i's 16 bytes at base + off
-// land at LDS byte lds + 16 i.  `lds` and `go` are wave-uniform.  M0 carries the LDS
-// address and is restored afterwards (the compiler reserves it); an LDS DMA needs one
-// wait state after an M0 write, hence the s_nop.  The branch lives inside the asm so the
-// caller's basic block is not split and the scheduler can interleave around it.
-__device__ __forceinline__ void dma16_if(uint32_t go, const void* base, uint32_t off, uint32_t lds) {
-  uint32_t saved;
-  asm volatile(
-      "s_cmp_eq_u32 %4, 0\n\t"
-      "s_cbranch_scc1 1f\n\t"
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %3\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, %2\n\t"
-      "s_mov_b32 m0, %0\n"
-      "1:"
-      : "=&s"(saved)
-      : "v"(off), "s"(base), "s"(lds), "s"(go)
-      : "memory", "scc");
-}
+// One 16-byte-per-lane global->LDS load: lane i's 16 bytes at base + off land at LDS
+// byte lds + 16 i (`base` and `lds` wave-uniform).  The LDS address is an operand bound
+// to M0, so the compiler owns M0; the LDS DMA needs one wait state after an M0 write.
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
-  dma16_if(1u, base, off, lds);
+  asm volatile(
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(off), "s"(base), "{m0}"(lds)
+      : "memory");
 }
 
 // K layout in a page slot's LDS run, chunk-major: chunk (16 B = 8 dims) c of token t at
@@ -207,6 +195,7 @@ __global__ void __launch_bounds__(256, 3) prefill_kernel(PreArgs a) {
   unsigned long long pvbits = 0;
   auto pv = [&](int R, int ps) { return (int)((pvbits >> ((R * 2 + ps) * 5)) & 31); };
 
+  const uint32_t pool_pages32 = (uint32_t)min(a.pool_pages, (int64_t)0x7fffffff);
   struct Ids { int id[2]; };
   auto load_ids = [&](int hx) {
     Ids x;
@@ -224,9 +213,10 @@ __global__ void __launch_bounds__(256, 3) prefill_kernel(PreArgs a) {
 #pragma unroll
     for (int ps = 0; ps < 2; ++ps) {
       const int pidx = 2 * hx + ps;
-      const long long id = id2[ps];
+      const int id = id2[ps];
       const int valid = min(max(nkeys - pidx * kPage, 0), kPage);
-      const bool ok = valid > 0 && id >= 0 && id < a.pool_pages;
+      // one unsigned compare: negative ids wrap above any pool size
+      const bool ok = valid > 0 && (uint32_t)id < pool_pages32;
       const int sh = (R * 2 + ps) * 5;
       pvbits = (pvbits & ~(31ull << sh)) | ((unsigned long long)(ok ? valid : 0) << sh);
       // Every wave issues exactly 4 loads per half (a bad page reads page 0, zeroed
