@@ -118,8 +118,8 @@ def config4(seed: int = 4, decode_sigma: float = 1.0) -> StepConfig:
     """Mixed 8192-token budget step from running state: 2 chunked-prefill continuations
     (3000 cached, 4096 still to go, chunk 2048), 3 fresh prompts of 512/700/900 tokens and
     256 decodes with contexts log-normal (median 1500, sigma `decode_sigma`) clipped to
-    [64, 8192].  The batch (n per request, batch order) is chosen by fqa_schedule; the
-    fields computed/n_new/bt_* hold the oracle's selection for reference."""
+    [64, 8192].  computed/bt_* are the running state; n_new is zero because the batch (n per
+    request, batch order) is chosen on the GPU by fqa_schedule."""
     rng = np.random.default_rng(seed)
     dec_L = np.clip(np.round(rng.lognormal(np.log(1500.0), decode_sigma, size=256)), 64,
                     8192).astype(int)
