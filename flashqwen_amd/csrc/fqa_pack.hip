@@ -23,17 +23,26 @@ namespace {
 constexpr int kPackThreads = 1024;
 constexpr int kPackWaves = kPackThreads / 64;
 
+// Workgroup barrier for LDS exchanges: waits for this wave's LDS (and scalar) accesses
+// only.  __syncthreads would also wait for every outstanding global load; without that,
+// loads issued before a scan stay in flight across it.  No kernel here reads global
+// memory another thread of the same launch wrote.
+__device__ __forceinline__ void lds_sync() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+}
+
 // Exclusive scan of one int per thread over a kPackThreads workgroup (DPP waves + one LDS
 // exchange); the total goes to *total.  `sh` holds >= kPackWaves ints.
 __device__ int block_excl_scan(int v, int* sh, int* total) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
   const int incl = wave_incl_scan(v);
   if (lane == kWave - 1) sh[w] = incl;
-  __syncthreads();
+  lds_sync();
   const int sc = wave_incl_scan(lane < kPackWaves ? sh[lane] : 0);
   *total = __builtin_amdgcn_readlane(sc, kPackWaves - 1);
   const int below = __builtin_amdgcn_readlane(sc, w == 0 ? 0 : w - 1);
-  __syncthreads();
+  lds_sync();
   return (w == 0 ? 0 : below) + incl - v;
 }
 
@@ -42,9 +51,9 @@ __device__ int block_max(int v, int* sh) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
   v = wave_extreme<true>(v, INT_MIN);
   if (lane == 0) sh[w] = v;
-  __syncthreads();
+  lds_sync();
   v = wave_extreme<true>(lane < kPackWaves ? sh[lane] : INT_MIN, INT_MIN);
-  __syncthreads();
+  lds_sync();
   return v;
 }
 
@@ -69,7 +78,7 @@ __device__ Stats block_reduce_stats(Stats v, Stats* sh) {
   r.v[4] = wave_extreme<true>(v.v[4], 1);
   r.v[5] = wave_extreme<true>(v.v[5], 0);
   if (lane == 0) sh[w] = r;
-  __syncthreads();
+  lds_sync();
   const bool have = lane < kPackWaves;
   const Stats o = sh[have ? lane : 0];
   r.v[0] = wave_extreme<false>(have ? o.v[0] : INT_MAX, INT_MAX);
@@ -78,7 +87,7 @@ __device__ Stats block_reduce_stats(Stats v, Stats* sh) {
   r.v[3] = wave_extreme<true>(have ? o.v[3] : 0, 0);
   r.v[4] = wave_extreme<true>(have ? o.v[4] : 1, 1);
   r.v[5] = wave_extreme<true>(have ? o.v[5] : 0, 0);
-  __syncthreads();
+  lds_sync();
   return r;
 }
 
@@ -93,7 +102,7 @@ __device__ Counts block_excl_scan5(const Counts& in, Counts* sh, Counts* total) 
 #pragma unroll
   for (int k = 0; k < 5; ++k) incl.v[k] = wave_incl_scan(in.v[k]);
   if (lane == kWave - 1) sh[w] = incl;
-  __syncthreads();
+  lds_sync();
   const bool have = lane < kPackWaves;
   const Counts o = sh[have ? lane : 0];
   Counts out;
@@ -104,7 +113,7 @@ __device__ Counts block_excl_scan5(const Counts& in, Counts* sh, Counts* total) 
     const int below = __builtin_amdgcn_readlane(sc, w == 0 ? 0 : w - 1);
     out.v[k] = (w == 0 ? 0 : below) + incl.v[k] - in.v[k];
   }
-  __syncthreads();
+  lds_sync();
   return out;
 }
 
@@ -187,6 +196,41 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     return;
   }
   const int T = rows;
+  const int gtid = blockIdx.x * kPackThreads + tid;
+  const int gsz = gridDim.x * kPackThreads;
+
+  // ---- padded block tables: they need only the table offsets, so their loads and
+  // stores go out before the scans (whose barriers leave global accesses in flight) ----
+  {
+    const int total = R * maxb;  // < 2^31: R <= 2048, max_blocks <= 2^19
+    for (int e = gtid; e < total; e += gsz) {
+      const int r = e / maxb, g = e - r * maxb;
+      int nb = s_btoff[r + 1] - s_btoff[r];
+      a.o.block_tables[e] = g < nb ? a.b.bt_pages[s_btoff[r] + g] : -1;
+    }
+  }
+  // ---- workgroup 0: the first chunk of the page-id range check is loaded now and
+  // checked at the end (16-byte loads, kPgVec per thread; the scalar head and tail are
+  // the at most 3 ids on either side of 16-byte alignment) ----------------------------
+  constexpr int kPgVec = 12;
+  const int32_t* pg = a.b.bt_pages + s_btoff[0];
+  const int npages = s_btoff[R] - s_btoff[0];
+  const int pg_lead = min(npages, (int)(((16 - ((uintptr_t)pg & 15)) & 15) >> 2));
+  const int pg_nvec = (npages - pg_lead) >> 2;
+  const int pg_ntail = npages - pg_lead - 4 * pg_nvec;
+  const int4* pgv_src = reinterpret_cast<const int4*>(pg + pg_lead);
+  // Unconditional loads at clamped indices (a load under a lane condition would be
+  // waited for where its value merges with the default); slots past the end are masked
+  // where they are checked.
+  int4 pgv[kPgVec];
+  int pg_head_id = 0, pg_tail_id = 0;
+  if (blockIdx.x == 0 && npages > 0) {
+#pragma unroll
+    for (int u = 0; u < kPgVec; ++u)
+      pgv[u] = pgv_src[max(min(u * kPackThreads + tid, pg_nvec - 1), 0)];
+    pg_head_id = pg[min(tid, npages - 1)];
+    pg_tail_id = pg[max(min(pg_lead + 4 * pg_nvec + tid, npages - 1), 0)];
+  }
 
   // decode plan: W page runs (8 kv heads x pages) cut into G equal shares
   const long long W = 8LL * dpages;
@@ -229,7 +273,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       s_decit[R] = carry.v[3];
       s_preit[R] = carry.v[4];
     }
-    __syncthreads();
+    lds_sync();
   }
   const int nd = s_decidx[R], np = s_preidx[R];
   const int npi = s_preit[R];
@@ -246,37 +290,56 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       s_drid[s_decidx[r]] = r;
     }
   if (tid == 0) s_dstart[nd] = (int)W;
-  __syncthreads();
-  const int gtid = blockIdx.x * kPackThreads + tid;
-  const int gsz = gridDim.x * kPackThreads;
+  lds_sync();
 
-  // ---- rows: positions, request index, slot mapping ------------------------------
-  for (int t = gtid; t < T; t += gsz) {
-    int r = upper_index(s_qstart, R, t);
-    int p = s_comp[r] + (t - s_qstart[r]);
-    int page = a.b.bt_pages[s_btoff[r] + p / kPage];
+  // ---- rows (positions, request index, slot mapping) and decode wave shares (where
+  // share w = [w*W/G, (w+1)*W/G) starts): the page-id loads of both loops' first
+  // iteration are issued before any of their stores ------------------------------------
+  auto row_of = [&](int t, int& r, int& p) {
+    r = upper_index(s_qstart, R, t);
+    p = s_comp[r] + (t - s_qstart[r]);
+  };
+  auto wave_of = [&](int w, int& di, int& kvh, int& page, int& n, int& r) {
+    const long long g0 = (long long)w * W / G, g1 = (long long)(w + 1) * W / G;
+    di = upper_index(s_dstart, nd, (int)g0);
+    const int rem = (int)g0 - s_dstart[di], pg = s_dpages[di];
+    kvh = rem / pg;
+    page = rem % pg;
+    n = (int)(g1 - g0);
+    r = s_drid[di];
+  };
+  auto store_row = [&](int t, int r, int p, int page) {
     a.o.positions[t] = p;
     a.o.row_req[t] = r;
     a.o.slot_mapping[t] = page * kPage + p % kPage;
-  }
-  // ---- padded block tables -------------------------------------------------------
-  {
-    const int total = R * maxb;  // < 2^31: R <= 2048, max_blocks <= 2^19
-    for (int e = gtid; e < total; e += gsz) {
-      const int r = e / maxb, g = e - r * maxb;
-      int nb = s_btoff[r + 1] - s_btoff[r];
-      a.o.block_tables[e] = g < nb ? a.b.bt_pages[s_btoff[r] + g] : -1;
-    }
-  }
-  // ---- decode wave shares: where share w = [w*W/G, (w+1)*W/G) starts ----------------
-  for (int w = gtid; w < G; w += gsz) {
-    const long long g0 = (long long)w * W / G, g1 = (long long)(w + 1) * W / G;
-    const int di = upper_index(s_dstart, nd, (int)g0);
-    const int rem = (int)g0 - s_dstart[di], pg = s_dpages[di];
-    const int kvh = rem / pg, page = rem % pg, r = s_drid[di];
+  };
+  auto store_wave = [&](int w, int di, int kvh, int page, int n, int r, int id) {
     int4* dst = reinterpret_cast<int4*>(a.o.dec_waves + 8 * (long long)w);
-    dst[0] = make_int4(di, kvh, page, (int)(g1 - g0));
-    dst[1] = make_int4(r, s_qstart[r], s_comp[r] + 1, a.b.bt_pages[s_btoff[r] + page]);
+    dst[0] = make_int4(di, kvh, page, n);
+    dst[1] = make_int4(r, s_qstart[r], s_comp[r] + 1, id);
+  };
+  {
+    int r0 = 0, p0 = 0, page0 = 0, di1 = 0, kvh1 = 0, pg1 = 0, n1 = 0, r1 = 0, id1 = 0;
+    if (gtid < T) {
+      row_of(gtid, r0, p0);
+      page0 = a.b.bt_pages[s_btoff[r0] + p0 / kPage];
+    }
+    if (gtid < G) {
+      wave_of(gtid, di1, kvh1, pg1, n1, r1);
+      id1 = a.b.bt_pages[s_btoff[r1] + pg1];
+    }
+    if (gtid < T) store_row(gtid, r0, p0, page0);
+    if (gtid < G) store_wave(gtid, di1, kvh1, pg1, n1, r1, id1);
+  }
+  for (int t = gtid + gsz; t < T; t += gsz) {
+    int r, p;
+    row_of(t, r, p);
+    store_row(t, r, p, a.b.bt_pages[s_btoff[r] + p / kPage]);
+  }
+  for (int w = gtid + gsz; w < G; w += gsz) {
+    int di, kvh, page, n, r;
+    wave_of(w, di, kvh, page, n, r);
+    store_wave(w, di, kvh, page, n, r, a.b.bt_pages[s_btoff[r] + page]);
   }
   for (int r = gtid; r < R; r += gsz)
     if (s_n[r] == 1)
@@ -330,27 +393,26 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     if (i >= nd) a.o.decode_rids[i] = -1;
     if (i >= np) a.o.prefill_rids[i] = -1;
   }
-  // page-id range check over the concatenated tables: 16-byte loads, kPgVec in flight
-  // per thread so most batches take one round trip (the scalar head and tail are the at
-  // most 3 ids on either side of alignment)
+  // page-id range check over the concatenated tables: the first chunk was loaded before
+  // the scans
   int bad = 0;
   {
-    constexpr int kPgVec = 12;
-    const int32_t* pg = a.b.bt_pages + s_btoff[0];
-    const int npages = s_btoff[R] - s_btoff[0];
-    const int lead = min(npages, (int)(((16 - ((uintptr_t)pg & 15)) & 15) >> 2));
-    const int nvec = (npages - lead) >> 2;
-    const int4* pv = reinterpret_cast<const int4*>(pg + lead);
     const long long np64 = a.c.pool_pages;
     auto badv = [&](int v) { return v < 0 || (long long)v >= np64; };
-    for (int e = tid; e < lead; e += kPackThreads) bad |= badv(pg[e]);
-    for (int e = lead + 4 * nvec + tid; e < npages; e += kPackThreads) bad |= badv(pg[e]);
-    for (int base = 0; base < nvec; base += kPgVec * kPackThreads) {
+    if (npages > 0) {
+      bad |= (int)(tid < pg_lead && badv(pg_head_id)) | (int)(tid < pg_ntail && badv(pg_tail_id));
+#pragma unroll
+      for (int u = 0; u < kPgVec; ++u)
+        if (u * kPackThreads + tid < pg_nvec)
+          bad |= (int)badv(pgv[u].x) | (int)badv(pgv[u].y) | (int)badv(pgv[u].z) |
+                 (int)badv(pgv[u].w);
+    }
+    for (int base = kPgVec * kPackThreads; base < pg_nvec; base += kPgVec * kPackThreads) {
       int4 v[kPgVec];
 #pragma unroll
       for (int u = 0; u < kPgVec; ++u) {
         const int e = base + u * kPackThreads + tid;
-        v[u] = e < nvec ? pv[e] : make_int4(0, 0, 0, 0);
+        v[u] = e < pg_nvec ? pgv_src[e] : make_int4(0, 0, 0, 0);
       }
 #pragma unroll
       for (int u = 0; u < kPgVec; ++u)
@@ -390,7 +452,7 @@ schedule_kernel(const int32_t* __restrict__ num_tokens, const int32_t* __restric
   __shared__ int s_wcnt[kSchedThreads / kWave];
   const int tid = threadIdx.x;
   for (int i = tid; i < R; i += kSchedThreads) s_rem[i] = num_tokens[i] - computed[i];
-  __syncthreads();
+  lds_sync();
   // stable sort by remaining ascending: rank = #smaller + #equal-and-earlier
   for (int i = tid; i < R; i += kSchedThreads) {
     int v = s_rem[i], rank = 0;
@@ -400,7 +462,7 @@ schedule_kernel(const int32_t* __restrict__ num_tokens, const int32_t* __restric
     }
     s_order[rank] = i;
   }
-  __syncthreads();
+  lds_sync();
   // n_k = min(B, S_k) - min(B, S_{k-1}), S = inclusive prefix of per-request caps:
   // the greedy loop's budget bookkeeping in closed form.  Only min(B, S) matters, so the
   // prefix is taken with saturating adds at B + 1 (B <= 2^24 keeps every sum in int).
@@ -426,12 +488,12 @@ schedule_kernel(const int32_t* __restrict__ num_tokens, const int32_t* __restric
     x = sat(x, __builtin_amdgcn_update_dpp(0, x, kDppRowBcast15, 0xa, 0xf, false));
     x = sat(x, __builtin_amdgcn_update_dpp(0, x, kDppRowBcast31, 0xc, 0xf, false));
     if (lane == kWave - 1) s_wsum[w] = x;
-    __syncthreads();
+    lds_sync();
     int pre = carry;  // saturating prefix of the earlier waves
     for (int i = 0; i < w; ++i) pre = sat(pre, s_wsum[i]);
     int tot = carry;
     for (int i = 0; i < kSchedThreads / kWave; ++i) tot = sat(tot, s_wsum[i]);
-    __syncthreads();
+    lds_sync();
     // exclusive prefix = the previous lane's saturated inclusive prefix (wave_shr:1)
     const int xe = __builtin_amdgcn_update_dpp(0, x, kDppWaveShr1, 0xf, 0xf, true);
     const int incl = sat(pre, x), excl = sat(pre, xe);
@@ -441,13 +503,13 @@ schedule_kernel(const int32_t* __restrict__ num_tokens, const int32_t* __restric
     // compact the chosen requests in sorted order
     const int c = wave_incl_scan(take);
     if (lane == kWave - 1) s_wcnt[w] = c;
-    __syncthreads();
+    lds_sync();
     int cpre = 0, ctot = 0;
     for (int i = 0; i < kSchedThreads / kWave; ++i) {
       if (i < w) cpre += s_wcnt[i];
       ctot += s_wcnt[i];
     }
-    __syncthreads();
+    lds_sync();
     if (take) {
       const int pos = ccount + cpre + c - 1;
       batch_req[pos] = idx;
@@ -487,7 +549,7 @@ gather_kernel(const int32_t* __restrict__ batch_req, const int32_t* __restrict__
     carry += tot;
   }
   if (tid == 0) s_off[R] = carry;
-  __syncthreads();
+  lds_sync();
   const int gtid = blockIdx.x * kPackThreads + tid, gsz = gridDim.x * kPackThreads;
   if (blockIdx.x == 0)
     for (int i = tid; i <= R; i += kPackThreads) {
