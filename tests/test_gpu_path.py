@@ -81,26 +81,26 @@ def check_pack(step, ref_pk, R, T, kw):
     assert np.array_equal(step.pre_items.cpu().numpy()[:npi], ref_pk["pre_items"][:npi])
 
 
-@pytest.mark.gpu
-@pytest.mark.parametrize("cfgno,tile", [(1, 32), (2, 32), (3, 32)])
-def test_step_parity(gpu, cfgno, tile):
+def _check_step(cfg, sub, kw, seed, label, schedule=False, kernel_only=True):
+    """Run the step on the GPU (cfg: the batch, or for schedule=True the running state it
+    is selected from) and the oracle chain on `sub` (the batch itself); compare the pack
+    bit-exactly, norm/RoPE within 1 ulp, V exactly on sampled rows, and the attention
+    output (end to end, and optionally of the attention kernels alone) within tolerance."""
     from oracle import oracle as orc
 
-    print(f"[test_step_parity] config{cfgno} tile{tile}", flush=True)
-    cfg = synth.CONFIGS[cfgno]()
-    rng = np.random.default_rng(100 + cfgno)
-    T, R = cfg.rows, cfg.n_reqs
-    kw = sc.pack_kwargs(cfg, dec_grid_waves=256 if cfgno == 1 else 2048, dec_min_pages=2,
-                        pre_tile_q=tile)
+    rng = np.random.default_rng(seed)
+    T, R = sub.rows, sub.n_reqs
     qkv_h = synth.rand_bf16(rng, (T, QKV_STRIDE))
     wq, wk = synth.norm_weights()
-    pool = make_pool(cfg.pool_pages, 1000 + cfgno, gpu)
+    pool = make_pool(cfg.pool_pages, 1000 + seed, kw["device"])
     pool_h = _host_u16(pool).reshape(-1).copy()
+    kwp = {k: v for k, v in kw.items() if k != "device"}
 
-    ref = sc.oracle_chain(cfg, qkv_h, pool_h, wq, wk, kw)
-    step, qkv, out = gpu_chain(cfg, qkv_h, pool, wq, wk, gpu, kw)
+    ref = sc.oracle_chain(sub, qkv_h, pool_h, wq, wk, kwp)
+    del pool_h
+    step, qkv, out = gpu_chain(cfg, qkv_h, pool, wq, wk, kw["device"], kwp, schedule=schedule)
 
-    check_pack(step, ref["pack"], R, T, kw)
+    check_pack(step, ref["pack"], R, T, kwp)
 
     # norm + rope: q in place, k/v into the pool (within 1 bf16 ulp; v exact)
     q_got = _host_u16(qkv)
@@ -120,16 +120,59 @@ def test_step_parity(gpu, cfgno, tile):
     # attention end to end
     o_got = _host_u16(out)[:T]
     mx, mean = sc.att_errors(o_got, ref["out"])
-    print(f"config{cfgno}: end-to-end max-abs {mx:.3e} mean-abs {mean:.3e}")
+    print(f"{label}: end-to-end max-abs {mx:.3e} mean-abs {mean:.3e}")
     assert mx <= sc.ATT_MAX_ABS and mean <= sc.ATT_MEAN_ABS
+    if not kernel_only:
+        return
 
     # attention alone: oracle attention on the GPU's post-append qkv and pool
     o_ref = np.zeros((T, N_Q * HEAD_DIM), np.uint16)
     pk = ref["pack"]
-    orc.decode(q_got, pool_got.copy(), cfg.pool_pages, pk["block_tables"], kw["max_blocks"],
+    orc.decode(q_got, pool_got.copy(), sub.pool_pages, pk["block_tables"], kwp["max_blocks"],
                pk["cu_seqlens"], pk["positions"], pk["decode_rids"], int(pk["meta"][1]), o_ref)
-    orc.prefill(q_got, pool_got.copy(), cfg.pool_pages, pk["block_tables"], kw["max_blocks"],
+    orc.prefill(q_got, pool_got.copy(), sub.pool_pages, pk["block_tables"], kwp["max_blocks"],
                 pk["cu_seqlens"], pk["positions"], pk["prefill_rids"], int(pk["meta"][2]), o_ref)
     mx, mean = sc.att_errors(o_got, o_ref)
-    print(f"config{cfgno}: kernel-only max-abs {mx:.3e} mean-abs {mean:.3e}")
+    print(f"{label}: kernel-only max-abs {mx:.3e} mean-abs {mean:.3e}")
     assert mx <= sc.ATT_MAX_ABS and mean <= sc.ATT_MEAN_ABS
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cfgno,tile", [(1, 32), (2, 32), (3, 32)])
+def test_step_parity(gpu, cfgno, tile):
+    print(f"[test_step_parity] config{cfgno} tile{tile}", flush=True)
+    cfg = synth.CONFIGS[cfgno]()
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=256 if cfgno == 1 else 2048, dec_min_pages=2,
+                        pre_tile_q=tile)
+    _check_step(cfg, cfg, dict(kw, device=gpu), 100 + cfgno, f"config{cfgno}")
+
+
+@pytest.mark.gpu
+def test_step_parity_scheduled(gpu):
+    """Config 4: the GPU selects the batch from running state (fqa_schedule +
+    fqa_gather_batch), packs and runs it: 2 chunked prefills on cached prefixes, 3 fresh
+    prompts and 256 decodes in one step.  The oracle selects, packs and runs the same."""
+    from oracle import oracle as orc
+
+    print("[test_step_parity_scheduled] config4", flush=True)
+    cfg = synth.config4()
+    sel_req, sel_n = orc.schedule(cfg.num_tokens, cfg.computed, cfg.token_budget,
+                                  cfg.prefill_chunk)
+    tabs = cfg.tables()
+    sub = synth._assemble("config4-selected", cfg.computed[sel_req], sel_n,
+                          [tabs[i] for i in sel_req], cfg.pool_pages, cfg.max_ctx)
+    kw = sc.pack_kwargs(sub, dec_grid_waves=2048, dec_min_pages=8)
+    _check_step(cfg, sub, dict(kw, device=gpu), 104, "config4", schedule=True,
+                kernel_only=False)
+
+
+@pytest.mark.gpu
+def test_decode_long_and_shared_prefix(gpu):
+    """Config 5's decode batch on one layer: 32 sequences of 32768 tokens, each stream cut
+    across several decode wavefronts (the combine merges more partials than one batch of
+    loads holds), and 96 sequences sharing 4 prefixes of 128 pages through their block
+    tables.  Pool sized to the pages the batch uses (70000 pages, 4.6 GB)."""
+    print("[test_decode_long_and_shared_prefix] config5, 1 layer", flush=True)
+    cfg = synth.config5(layers=1, pool_pages=70000)
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=2048, dec_min_pages=8)
+    _check_step(cfg, cfg, dict(kw, device=gpu), 105, "config5", kernel_only=False)
