@@ -125,13 +125,25 @@ __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* bt
                                              int pb, int pe, int L, const bf16x8 (&qf)[4],
                                              int lane, DecState& st, int first_page) {
   const int g = lane >> 4;
+  // Page ids through the constant address space: scalar loads (lgkmcnt), so waiting for an
+  // id does not also wait for the page loads issued before it.
+  const __attribute__((address_space(4))) int32_t* btc =
+      (const __attribute__((address_space(4))) int32_t*)btr;
+  // one unsigned 32-bit scalar compare (negative ids wrap above any pool size); a 64-bit
+  // compare runs on the VALU and needs a temporary register pair, which the allocator
+  // may take from a page buffer still in flight (a full vmcnt drain)
+  const uint32_t pool32 = (uint32_t)min(a.pool_pages, (long long)0x7fffffff);
   auto load = [&](PageFrag& f, bool& ok, int p) {
-    const long long page = (p == pb && first_page >= 0) ? first_page : btr[p];
-    ok = page >= 0 && page < a.pool_pages;
+    const int page = (p == pb && first_page >= 0) ? first_page : btc[p];
+    ok = (uint32_t)page < pool32;
     load_page(f, a.pool + run_offset(ok ? page : 0, kvh), lane);
   };
   // Four page buffers in registers: page p is processed while p+1..p+3 are in flight.
-  // The buffers rotate through a 4-way unrolled loop so every index is static.
+  // The buffers rotate through a 4-way unrolled loop so every index is static.  (The
+  // refills are conditional, so the compiler drains the loads at each one and about one
+  // page per wave is in flight in practice; unconditional refills that keep three in
+  // flight were measured 2% slower on config 5 and equal on config 2: with 8 waves per
+  // CU the DRAM queues are already full.)
   PageFrag f0, f1, f2, f3;
   bool k0 = false, k1 = false, k2 = false, k3 = false;
   load(f0, k0, pb);
@@ -157,16 +169,23 @@ __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* bt
 // whole.  Whole streams are written as bf16 output; a cut stream leaves its partial in
 // slot 2w (the share's first stream) or 2w+1 (its last).
 __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel(DecArgs a) {
-  const int w = blockIdx.x * kDecWavesPerBlock + (threadIdx.x >> 6);
+  // Everything a wave's loop indexes with is wave-uniform; readfirstlane says so, so that
+  // block-table reads become scalar loads (see stream_pages).
+  const int w = blockIdx.x * kDecWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (w >= a.meta[FQA_META_DEC_WAVES]) return;
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
-  const int4 desc = *reinterpret_cast<const int4*>(a.waves + 8 * (long long)w);
-  int4 sq = reinterpret_cast<const int4*>(a.waves + 8 * (long long)w)[1];  // {r, row, L, page id}
+  auto uni4 = [](int4 v) {
+    return make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+                     __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
+  };
+  const int4 desc = uni4(*reinterpret_cast<const int4*>(a.waves + 8 * (long long)w));
+  // {r, row, L, page id}
+  int4 sq = uni4(reinterpret_cast<const int4*>(a.waves + 8 * (long long)w)[1]);
   int di = desc.x, kvh = desc.y, page = desc.z, left = desc.w;
   for (int seg = 0; left > 0; ++seg) {
     if (seg > 0) {
-      sq = *reinterpret_cast<const int4*>(a.seqs + 4 * (long long)di);
+      sq = uni4(*reinterpret_cast<const int4*>(a.seqs + 4 * (long long)di));
       sq.w = -1;  // first page id of a later stream: read from the block table
     }
     const int r = sq.x, row = sq.y, L = sq.z;
