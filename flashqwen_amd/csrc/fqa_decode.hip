@@ -144,6 +144,10 @@ __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* bt
   // page per wave is in flight in practice; unconditional refills that keep three in
   // flight were measured 2% slower on config 5 and equal on config 2: with 8 waves per
   // CU the DRAM queues are already full.)
+  // A page outside the pool (the pack flags the batch) reads as zeros: its keys score 0
+  // and add nothing to the numerator.  The online softmax merge is order-free, so such
+  // keys are only counted here and merged into `st` once, after the loop.
+  int n_zero = 0;
   PageFrag f0, f1, f2, f3;
   bool k0 = false, k1 = false, k2 = false, k3 = false;
   load(f0, k0, pb);
@@ -152,15 +156,29 @@ __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* bt
   for (int p = pb; p < pe; p += 4) {
     if (p + 3 < pe) load(f3, k3, p + 3);
     if (k0) process_page(f0, qf, p, L, g, a.scale_log2, st);
+    else n_zero += min(kPage, L - (p) * kPage);
     if (p + 1 >= pe) break;
     if (p + 4 < pe) load(f0, k0, p + 4);
     if (k1) process_page(f1, qf, p + 1, L, g, a.scale_log2, st);
+    else n_zero += min(kPage, L - (p + 1) * kPage);
     if (p + 2 >= pe) break;
     if (p + 5 < pe) load(f1, k1, p + 5);
     if (k2) process_page(f2, qf, p + 2, L, g, a.scale_log2, st);
+    else n_zero += min(kPage, L - (p + 2) * kPage);
     if (p + 3 >= pe) break;
     if (p + 6 < pe) load(f2, k2, p + 6);
     if (k3) process_page(f3, qf, p + 3, L, g, a.scale_log2, st);
+    else n_zero += min(kPage, L - (p + 3) * kPage);
+  }
+  if (n_zero > 0) {  // n_zero keys with score 0 and value 0 (uniform, rare)
+    const float m_new = fmaxf(st.m, 0.f);
+    const float corr = __builtin_amdgcn_exp2f(st.m - m_new);
+    // st.l holds this lane's share of the row sum (summed over the 4 lanes of a column
+    // at the end): lane group g = 0 takes the zero keys
+    st.l = st.l * corr + ((lane >> 4) == 0 ? (float)n_zero * __builtin_amdgcn_exp2f(-m_new) : 0.f);
+    st.m = m_new;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) st.acc[b] *= corr;
   }
 }
 

@@ -322,15 +322,20 @@ void fqo_qknorm_rope_append(int n_q, int n_kv, int D, int stride, float eps, uin
   }
 }
 
-/* Gather keys [0, nkeys) of one request's kv head into float rows K[n][D], V[n][D];
- * rows whose page id is out of range are flagged so they are skipped. */
+/* Gather keys [0, nkeys) of one request's kv head into float rows K[n][D], V[n][D].
+ * A page id outside the pool (a batch the pack flags with status 4; the reference reads
+ * out of bounds there) reads as zeros: its keys score 0 and add nothing to the output
+ * numerator.  This is the path's convention for such pages, kept by both GPU kernels. */
 static void gather_kv(int n_kv, int D, const uint16_t* pool, int64_t pool_pages,
                       const int32_t* bt_row, int nkeys, int kvh, float* K, float* V,
                       unsigned char* ok) {
   for (int kp = 0; kp < nkeys; ++kp) {
     int64_t page = bt_row[kp / PAGE];
-    ok[kp] = page >= 0 && page < pool_pages;
-    if (!ok[kp]) continue;
+    ok[kp] = 1;
+    if (page < 0 || page >= pool_pages) {
+      for (int d = 0; d < D; ++d) K[(int64_t)kp * D + d] = V[(int64_t)kp * D + d] = 0.f;
+      continue;
+    }
     int tok = kp % PAGE;
     const uint16_t* kb = pool + fqo_pool_offset(n_kv, D, page, kvh, 0, tok, 0);
     const uint16_t* vb = pool + fqo_pool_offset(n_kv, D, page, kvh, 1, 0, 0);

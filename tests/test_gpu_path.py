@@ -176,3 +176,26 @@ def test_decode_long_and_shared_prefix(gpu):
     cfg = synth.config5(layers=1, pool_pages=70000)
     kw = sc.pack_kwargs(cfg, dec_grid_waves=2048, dec_min_pages=8)
     _check_step(cfg, cfg, dict(kw, device=gpu), 105, "config5", kernel_only=False)
+
+
+@pytest.mark.gpu
+def test_pages_outside_pool_read_as_zeros(gpu):
+    """Block-table entries outside the pool (one past the end, one negative) in two decode
+    sequences and in a prefill's cached prefix: the pack flags the batch (status 4), and
+    both attention kernels read those pages as zeros (keys score 0, add nothing to the
+    numerator), as the oracle does; the rows' own pages are valid, so the append is
+    unaffected."""
+    print("[test_pages_outside_pool_read_as_zeros] config1 + 70-row prefill on a 40-token prefix",
+          flush=True)
+    base = synth.config1()
+    rng = np.random.default_rng(31)
+    used = set(base.bt_pages.tolist())
+    free = np.array([p for p in rng.permutation(base.pool_pages) if p not in used][:7], np.int32)
+    tabs = [t.copy() for t in base.tables()] + [free]
+    tabs[3][5] = base.pool_pages + 7   # decode, 512 keys: page 5 of 32
+    tabs[1][2] = -3                     # decode, 100 keys: page 2 of 7
+    tabs[4][1] = base.pool_pages        # prefill: page 1 of the 40-token cached prefix
+    cfg = synth._assemble("bad-pages", list(base.computed) + [40], list(base.n_new) + [70],
+                          tabs, base.pool_pages, base.max_ctx)
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=64, dec_min_pages=2)
+    _check_step(cfg, cfg, dict(kw, device=gpu), 131, "bad-pages")
