@@ -21,18 +21,22 @@
 //    MFMA row r of S^T holds key perm(r) (bits 2 and 3 of r swapped), so the 8 keys a
 //    lane half contributes to one page's PV step are 8 consecutive tokens: one 16-byte
 //    chunk of the page's V^T row.
-//  * Softmax VALU work per score, not MFMA, is the limit on CDNA (a wave64 VALU op
-//    issues in 4 cycles, exp in more): scores are maxed raw, scaled inside the exp2
-//    FMA, converted with v_cvt_pk_bf16_f32, summed two at a time with v_dot2 against
-//    (1, 1), and O is rescaled lazily (only when the row max grows by more than 2^8).
+//  * Per score the softmax costs about as much VALU issue as the MFMAs take (a wave64
+//    VALU op issues in ~4.5 cycles, exp in ~8-11), so it is kept minimal and hidden
+//    behind MFMAs: scores are maxed raw, scaled inside the exp2 FMA, converted with
+//    v_cvt_pk_bf16_f32, summed two at a time with v_dot2 against (1, 1), and O is
+//    rescaled lazily (only when the row max grows by more than 2^8).  Measured, the
+//    per-half staging (the 4 global->LDS instructions per wave, ~10% of the kernel) and
+//    the softmax (~9%) are the largest costs after the MFMAs themselves.
 //  * Software pipeline over 32-key halves: half t's exp/convert/sum is interleaved with
 //    the S^T MFMAs of half t+1 and the LDS reads of half t's V fragments, then half t's
 //    PV MFMAs issue back to back.
 //  * K/V staging is direct global->LDS (global_load_lds_dwordx4): a ring of three 16 KiB
 //    buffers, one 32-key half (two 8 KiB page runs) each, filled two halves ahead.
 //    Each wave moves one 4 KiB region (K or V^T of one page) per half; every lane picks
-//    the global chunk that lands in its slot of the XOR-swizzled layout, so fragment
-//    reads are conflict-free 16-byte reads and no VGPR carries staged data.  The loads
+//    the global chunk that lands in its slot of the LDS layout (K chunk-major, V^T
+//    XOR-swizzled), so fragment reads are conflict-free 16-byte reads and no VGPR
+//    carries staged data.  The loads
 //    are issued from inline assembly, so the compiler neither tracks them nor inserts
 //    its own conservative waits: every wait on them is an explicit vmcnt count followed
 //    by a barrier, and the loop issues no other vector-memory loads.
