@@ -64,5 +64,14 @@ def build_cpp_driver() -> Path:
     return exe
 
 
+def build_sched_driver() -> Path:
+    """tests/cpp/sched_cpp: a host program driving include/fqa_sched.hpp (no HIP)."""
+    root = PKG.parent
+    src = root / "tests" / "cpp" / "sched_cpp.cpp"
+    exe = src.with_suffix("")
+    _run(["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", "-o", str(exe), str(src)])
+    return exe
+
+
 if __name__ == "__main__":
     build(verbose=True)
