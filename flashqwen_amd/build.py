@@ -64,6 +64,16 @@ def build_cpp_driver() -> Path:
     return exe
 
 
+def build_serve_driver() -> Path:
+    """tests/cpp/serve_cpp: host scheduler + C++ step mirror serving loop on the GPU."""
+    root = PKG.parent
+    src = root / "tests" / "cpp" / "serve_cpp.cpp"
+    exe = src.with_suffix("")
+    _run([HIPCC, "-O2", "-std=c++17", "-o", str(exe), str(src), f"-L{PKG}", "-lfqa",
+          "-Wl,-rpath,$ORIGIN/../../flashqwen_amd"])
+    return exe
+
+
 def build_sched_driver() -> Path:
     """tests/cpp/sched_cpp: a host program driving include/fqa_sched.hpp (no HIP)."""
     root = PKG.parent
