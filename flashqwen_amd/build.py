@@ -74,6 +74,16 @@ def build_serve_driver() -> Path:
     return exe
 
 
+def build_graph_driver() -> Path:
+    """tests/cpp/graph_cpp: eager vs captured-graph steps through include/fqa_step.hpp."""
+    root = PKG.parent
+    src = root / "tests" / "cpp" / "graph_cpp.cpp"
+    exe = src.with_suffix("")
+    _run([HIPCC, "-O2", "-std=c++17", "-o", str(exe), str(src), f"-L{PKG}", "-lfqa",
+          "-Wl,-rpath,$ORIGIN/../../flashqwen_amd"])
+    return exe
+
+
 def build_sched_driver() -> Path:
     """tests/cpp/sched_cpp: a host program driving include/fqa_sched.hpp (no HIP)."""
     root = PKG.parent

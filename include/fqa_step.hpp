@@ -7,6 +7,7 @@
 //   LaunchHeadNormRope(...) + KvStore::StoreKV(...)          kernels.cuh:28-31, kv_store.h:29-31
 //   LaunchAttnDecodeCute(...)                                attn_cute.h:14-20
 //   LaunchAttnPrefillCute(...)                               attn_cute.h:7-12
+//   GraphCache (decode-step capture)                         model_runtime.h:160-201
 //
 // Differences a caller sees: PrepareInputs takes the batch as plain host vectors (the
 // reference's ForwardInput rows are derived on the device from computed/n per request),
@@ -95,6 +96,7 @@ class StepContext {
     dwaves_ = DeviceBuffer<int32_t>((size_t)dec_cap_ * 8);
     items_ = DeviceBuffer<int32_t>((size_t)pre_cap_ * 4);
     meta_ = DeviceBuffer<int32_t>(FQA_META_LEN);
+    nreq_ = DeviceBuffer<int32_t>(1);
     ws_ = DeviceBuffer<unsigned char>((size_t)fqa_decode_workspace_bytes(&dims_, dec_cap_));
     std::vector<float> c((size_t)max_ctx * 64), s((size_t)max_ctx * 64);
     Check(fqa_rope_tables(max_ctx, 128, 1.0e6f, c.data(), s.data()), "fqa_rope_tables");
@@ -107,6 +109,16 @@ class StepContext {
 
   // StepContext::PrepareInputs: upload the per-request batch and pack it on the GPU.
   void PrepareInputs(const BatchInput& in, hipStream_t stream) {
+    UploadBatch(in, stream);
+    fqa_batch b{computed_.D(), n_new_.D(), bt_off_.D(), bt_pages_.D(), nullptr, n_reqs_};
+    fqa_pack_out o = PackOut();
+    Check(fqa_pack(&b, &cfg_, &o, stream), "fqa_pack");
+  }
+
+  // The host half of PrepareInputs: copy the batch (and its request count) to the device.
+  // With Pack / RunLayerBounded, the device half can be captured once (StepGraph) and
+  // replayed for every batch.
+  void UploadBatch(const BatchInput& in, hipStream_t stream) {
     const int R = (int)in.computed.size();
     if (R > slots_) throw std::runtime_error("batch larger than slots");
     h_off_.assign(R + 1, 0);
@@ -124,13 +136,34 @@ class StepContext {
     }
     bt_off_.Upload(h_off_.data(), R + 1, stream);
     if (!h_pages_.empty()) bt_pages_.Upload(h_pages_.data(), h_pages_.size(), stream);
-    fqa_batch b{computed_.D(), n_new_.D(), bt_off_.D(), bt_pages_.D(), nullptr, R};
-    fqa_pack_out o{cu_.D(), qlen_.D(), pos_.D(), req_.D(), slot_.D(), bt_.D(), drids_.D(),
-                   prids_.D(), dseqs_.D(), dwaves_.D(), items_.D(), meta_.D()};
-    Check(fqa_pack(&b, &cfg_, &o, stream), "fqa_pack");
+    h_nreq_ = R;
+    nreq_.Upload(&h_nreq_, 1, stream);
     n_reqs_ = R;
     has_decode_ = has_prefill_ = false;
     for (int r = 0; r < R; ++r) (in.n_new[r] == 1 ? has_decode_ : has_prefill_) = true;
+  }
+
+  // The device half: fqa_pack over the uploaded batch with the request count read on the
+  // device and grids sized from the context's bounds (slots, max_rows).
+  void Pack(hipStream_t stream) const {
+    fqa_batch b{computed_.D(), n_new_.D(), bt_off_.D(), bt_pages_.D(), nreq_.D(), slots_};
+    fqa_pack_out o = PackOut();
+    Check(fqa_pack(&b, &cfg_, &o, stream), "fqa_pack");
+  }
+  // RunLayer for any batch within the bounds: rows and requests bounded by max_rows and
+  // slots, both attention kernels launched (each does nothing without its kind of rows).
+  void RunLayerBounded(uint16_t* qkv, const float* q_norm, const float* k_norm,
+                       uint16_t* pool_layer, uint16_t* out, hipStream_t stream) const {
+    Check(fqa_qknorm_rope_append(&dims_, qkv, q_norm, k_norm, cos_.D(), sin_.D(), max_ctx_,
+                                 pos_.D(), slot_.D(), meta_.D(), max_rows_, pool_layer,
+                                 pool_pages_, 0, stream),
+          "fqa_qknorm_rope_append");
+    Check(fqa_decode(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_, dwaves_.D(),
+                     dseqs_.D(), meta_.D(), dec_cap_, slots_, ws_.D(), out, stream),
+          "fqa_decode");
+    Check(fqa_prefill(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_, cu_.D(),
+                      pos_.D(), items_.D(), meta_.D(), 32, pre_cap_, out, stream),
+          "fqa_prefill");
   }
 
   // LaunchHeadNormRope + KvStore::StoreKV for one layer (fused).
@@ -169,6 +202,11 @@ class StepContext {
   int Rows() const { return rows_; }
 
  private:
+  fqa_pack_out PackOut() const {
+    return fqa_pack_out{cu_.D(), qlen_.D(), pos_.D(), req_.D(), slot_.D(), bt_.D(),
+                        drids_.D(), prids_.D(), dseqs_.D(), dwaves_.D(), items_.D(), meta_.D()};
+  }
+
   int max_rows_, slots_, max_ctx_, max_blocks_ = 0;
   int64_t pool_pages_;
   int dec_cap_ = 0, pre_cap_ = 0, n_reqs_ = 0, rows_ = 0;
@@ -176,11 +214,57 @@ class StepContext {
   fqa_dims dims_{};
   fqa_pack_cfg cfg_{};
   std::vector<int32_t> h_off_, h_pages_;
+  int32_t h_nreq_ = 0;  // host copy the request-count upload reads (kept until the copy ran)
   DeviceBuffer<int32_t> computed_, n_new_, bt_off_, bt_pages_;
   DeviceBuffer<int32_t> cu_, qlen_, pos_, req_, slot_, bt_, drids_, prids_, dseqs_, dwaves_, items_,
-      meta_;
+      meta_, nreq_;
   DeviceBuffer<unsigned char> ws_;
   DeviceBuffer<float> cos_, sin_;
+};
+
+// Buffers of one layer's attention block.
+struct LayerBuffers {
+  uint16_t* qkv;
+  const float* q_norm;
+  const float* k_norm;
+  uint16_t* pool;
+  uint16_t* out;
+};
+
+// One step captured as a HIP graph (the reference's GraphCache, model_runtime.h:160-201):
+// the pack and every layer's attention block.  Counts are read on the device from `meta`,
+// so where the reference keeps one graph per (rows, decodes) shape, one graph here serves
+// every batch within the context's bounds: per step, UploadBatch outside the graph, then
+// Launch.  The captured launches allocate nothing and record no memset.
+class StepGraph {
+ public:
+  StepGraph(const StepContext& ctx, const std::vector<LayerBuffers>& layers,
+            hipStream_t stream) {
+    HipCheck(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "begin capture");
+    try {
+      ctx.Pack(stream);
+      for (const LayerBuffers& l : layers)
+        ctx.RunLayerBounded(l.qkv, l.q_norm, l.k_norm, l.pool, l.out, stream);
+    } catch (...) {
+      hipGraph_t g = nullptr;
+      (void)hipStreamEndCapture(stream, &g);
+      if (g) (void)hipGraphDestroy(g);
+      throw;
+    }
+    HipCheck(hipStreamEndCapture(stream, &graph_), "end capture");
+    HipCheck(hipGraphInstantiate(&exec_, graph_, nullptr, nullptr, 0), "instantiate");
+  }
+  StepGraph(const StepGraph&) = delete;
+  StepGraph& operator=(const StepGraph&) = delete;
+  ~StepGraph() {
+    if (exec_) (void)hipGraphExecDestroy(exec_);
+    if (graph_) (void)hipGraphDestroy(graph_);
+  }
+  void Launch(hipStream_t stream) const { HipCheck(hipGraphLaunch(exec_, stream), "launch"); }
+
+ private:
+  hipGraph_t graph_ = nullptr;
+  hipGraphExec_t exec_ = nullptr;
 };
 
 }  // namespace fqa
