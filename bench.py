@@ -51,6 +51,9 @@ def parse():
                          "that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only run the per-kernel graphs (for rocprofv3 passes)")
+    ap.add_argument("--sampler", action="store_true",
+                    help="only measure fqa_sample (256 rows x 151936 logits: greedy, "
+                         "temperature, temperature + top-p 0.9)")
     return ap.parse_args()
 
 
@@ -71,6 +74,10 @@ def main():
             y.copy_(x)
         torch.cuda.synchronize()
         print(json.dumps({"copy_calib_bytes": x.numel() * 4, "copies": 3}))
+        return
+
+    if args.sampler:
+        bench_sampler(args)
         return
 
     import torch
@@ -270,6 +277,46 @@ def main():
         "wall_s_timed": round(wall, 3),
     }
     print(json.dumps(line))
+
+
+def bench_sampler(args):
+    """fqa_sample on 256 rows of 151936 fp32 logits (one sampling row per request of a
+    256-sequence decode step): greedy, temperature 1, temperature 1 + top-p 0.9.  The
+    roofline is HBM: one read of the logits (B*N*4 bytes) per launch; the kernel reads a
+    sampled row up to 6 times (the later passes mostly from L2 / MALL)."""
+    import torch
+
+    from flashqwen_amd.sample import sample
+
+    B, N = 256, 151936
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    logits = torch.randn(B, N, device="cuda", generator=g) * 3
+    u = torch.rand(B, device="cuda", generator=g)
+    out = torch.empty(B, dtype=torch.int32, device="cuda")
+    res = {}
+    for name, it, tp in (("greedy", 0.0, 1.0), ("temperature", 1.0, 1.0),
+                         ("top_p_0.9", 1.0, 0.9)):
+        itv = torch.full((B,), it, device="cuda")
+        tpv = torch.full((B,), tp, device="cuda")
+        for _ in range(5):
+            sample(logits, itv, tpv, u, out)
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for _ in range(20):
+                sample(logits, itv, tpv, u, out)
+        gr.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / 200
+        res[name] = {"us": round(us, 2), "rows_per_s": round(B / (us * 1e-6), 1),
+                     "logit_GBps": round(B * N * 4 / (us * 1e-6) / 1e9, 1)}
+    print(json.dumps({"sampler": res, "rows": B, "vocab": N, "peak_GBps": HBM_PEAK_GBS}))
 
 
 def _profile_traffic(config: int, kernels: list[str]):

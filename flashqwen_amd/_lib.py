@@ -106,6 +106,7 @@ SIGNATURES = {
         C.c_int,
         [C.POINTER(FqaDims), P, P, I64, P, I32, P, P, P, P, I32, I32, P, P],
     ),
+    "fqa_sample": (C.c_int, [P, I32, I32, I64, P, P, P, P, P]),
     "fqa_version": (C.c_char_p, []),
 }
 

@@ -1,0 +1,349 @@
+// fqa_sample.hip — token sampling over fp32 logits (gfx950).
+//
+// Replaces ArgmaxKernel + SampleKernel + LaunchSampleBatch (engine/src/kernels.cu:184-327):
+// per row, greedy argmax when inv_temp <= 0, else temperature + top-p nucleus sampling
+// with the caller's uniform draw u: weights w = exp((l - max) * inv_temp), the kept set
+// is the fewest largest weights whose mass reaches top_p * sum(w), and the token is the
+// first index at which the running kept mass reaches u * (kept mass).
+//
+// MI355X design: one 1024-thread workgroup per row.  Wave w owns a contiguous segment of
+// the row and its lanes read consecutive elements (coalesced 256-byte wave loads), so
+// index order is (segment, step, lane) and the inverse-CDF pick keeps vocabulary order.
+// The reference finds the top-p threshold by 32 bisection passes over the row, each
+// recomputing every weight; here it is a 3-level radix select on the weights' float bits
+// (bits 30..20, 19..9, 8..0; positive floats order like their bit patterns), with mass
+// histograms in LDS (ds_add_f32): the exact smallest kept weight after 3 passes.  A
+// sampled row is read 6 times (max, sum + level 1, level 2, level 3, kept mass, pick),
+// against 35 in the reference; the later passes mostly hit the L2 and the MALL.
+
+#include "fqa_common.h"
+
+namespace fqa {
+namespace {
+
+constexpr int kSThreads = 1024;
+constexpr int kSWaves = kSThreads / kWave;
+constexpr int kBins = 2048;  // histogram bins per radix level (levels use 11, 11, 9 bits)
+
+struct SampArgs {
+  const float* logits;
+  int vocab;
+  long long stride;
+  const float* inv_temp;
+  const float* top_p;
+  const float* u;
+  int* out;
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+// Inclusive prefix sum over the wave's lanes.
+__device__ __forceinline__ float wave_scan(float v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const float x = __shfl_up(v, o, kWave);
+    if (lane >= o) v += x;
+  }
+  return v;
+}
+
+// Sum / max over the workgroup; every thread gets the result.  `sh` holds kSWaves floats.
+__device__ float block_sum(float v, float* sh) {
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();  // sh is free again
+  if (lane == 0) sh[w] = v;
+  __syncthreads();
+  float r = lane < kSWaves ? sh[lane] : 0.f;
+  return __shfl(wave_sum(r), 0, kWave);
+}
+__device__ float block_max(float v, float* sh) {
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
+  v = wave_max(v);
+  __syncthreads();
+  if (lane == 0) sh[w] = v;
+  __syncthreads();
+  float r = lane < kSWaves ? sh[lane] : -INFINITY;
+  return __shfl(wave_max(r), 0, kWave);
+}
+
+// Descending scan of a mass histogram: the bin at which the mass of bins above it plus
+// `above` first reaches `need` (need <= above + the histogram's total).  Returns the bin
+// and, in *above_out, the mass above it.  Every thread takes 2 bins, highest first.
+__device__ int find_crossing(const float* hist, int nbins, float above, float need,
+                             float* sh, int* sres, float* sres_f, float* above_out) {
+  const int t = threadIdx.x;
+  const int b0 = nbins - 1 - 2 * t, b1 = b0 - 1;
+  const float m0 = b0 >= 0 ? hist[b0] : 0.f, m1 = b1 >= 0 ? hist[b1] : 0.f;
+  const float local = m0 + m1;
+  // exclusive block scan of `local` in thread order (= descending bins)
+  const int lane = t & (kWave - 1), w = t >> 6;
+  const float incl = wave_scan(local);
+  __syncthreads();
+  if (lane == kWave - 1) sh[w] = incl;
+  if (t == 0) {
+    *sres = 0;  // lowest bin unless a crossing is found
+    *sres_f = above;
+  }
+  __syncthreads();
+  float before = above;
+  for (int i = 0; i < w; ++i) before += sh[i];
+  before += incl - local;
+  if (before < need && before + local >= need) {
+    if (b0 >= 0 && before + m0 >= need) {
+      *sres = b0;
+      *sres_f = before;
+    } else {
+      *sres = b1;
+      *sres_f = before + m0;
+    }
+  }
+  __syncthreads();
+  *above_out = *sres_f;
+  return *sres;
+}
+
+// Wave w of the row covers [seg0, seg1), a whole number of 256-element steps except at
+// the row's end; in a step lane l holds elements s0 + 4l .. s0 + 4l + 3, so vocabulary
+// order is (wave, step, lane, element).  With kVec4 (16-byte aligned rows) a lane loads its
+// 4 logits as one float4: a wave load moves 1 KiB.
+template <bool kVec4>
+__device__ __forceinline__ void load4(const float* lg, int i, int end, float (&x)[4]) {
+  if (kVec4 && i + 3 < end) {
+    const float4 v = *reinterpret_cast<const float4*>(lg + i);
+    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = i + e < end ? lg[i + e] : -INFINITY;
+  }
+}
+
+template <bool kVec4>
+__global__ void __launch_bounds__(kSThreads) sample_kernel(SampArgs a) {
+  __shared__ float hist[kBins];
+  __shared__ float sh[kSWaves];
+  __shared__ float sh2[kSWaves];
+  __shared__ int sres;
+  __shared__ float sres_f;
+  __shared__ int s_pick;
+
+  const int row = blockIdx.x;
+  const int N = a.vocab;
+  const float* lg = a.logits + (long long)row * a.stride;
+  const int t = threadIdx.x, lane = t & (kWave - 1), w = t >> 6;
+  constexpr int kStep = 4 * kWave;
+  const int seg = ((N + kSWaves * kStep - 1) / (kSWaves * kStep)) * kStep;
+  const int seg0 = min(w * seg, N), seg1 = min(seg0 + seg, N);
+  const float it = a.inv_temp[row];
+  // calls f(index, logit) for this lane's elements, in vocabulary order per lane
+  auto for_each = [&](auto&& f) {
+    for (int s0 = seg0; s0 < seg1; s0 += kStep) {
+      const int i = s0 + 4 * lane;
+      float x[4];
+      load4<kVec4>(lg, i, seg1, x);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (i + e < seg1) f(i + e, x[e]);
+    }
+  };
+
+  if (it <= 0.f) {  // greedy: largest logit, smallest index among equals
+    float best = -INFINITY;
+    int bi = N;
+    for_each([&](int i, float v) {
+      if (v > best) {  // strictly greater: the first index in this lane's order
+        best = v;
+        bi = i;
+      }
+    });
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(best, o, kWave);
+      const int oi = __shfl_xor(bi, o, kWave);
+      if (ov > best || (ov == best && oi < bi)) {
+        best = ov;
+        bi = oi;
+      }
+    }
+    __shared__ int wbi[kSWaves];
+    if (lane == 0) {
+      sh[w] = best;
+      wbi[w] = bi;
+    }
+    __syncthreads();
+    if (t == 0) {
+      float b = sh[0];
+      int i0 = wbi[0];
+      for (int k = 1; k < kSWaves; ++k)
+        if (sh[k] > b || (sh[k] == b && wbi[k] < i0)) {
+          b = sh[k];
+          i0 = wbi[k];
+        }
+      a.out[row] = i0 < N ? i0 : 0;  // all -inf/NaN: token 0
+    }
+    return;
+  }
+
+  // pass 1: row max and total weight together (online: the running sum is rescaled when
+  // the running max grows), merged across lanes and waves the same way
+  float lm = -INFINITY, ls = 0.f;
+  for_each([&](int, float v) {
+    if (v == -INFINITY) return;  // a masked token weighs 0 (and -inf - -inf is NaN)
+    if (v > lm) {
+      ls = ls * __expf((lm - v) * it) + 1.f;
+      lm = v;
+    } else {
+      ls += __expf((v - lm) * it);
+    }
+  });
+  auto merge = [&](float& m0, float& s0v, float m1, float s1) {
+    const float mn = fmaxf(m0, m1);
+    if (mn == -INFINITY) return;
+    s0v = (m0 == -INFINITY ? 0.f : s0v * __expf((m0 - mn) * it)) +
+          (m1 == -INFINITY ? 0.f : s1 * __expf((m1 - mn) * it));
+    m0 = mn;
+  };
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) merge(lm, ls, __shfl_xor(lm, o, kWave), __shfl_xor(ls, o, kWave));
+  if (lane == 0) {
+    sh[w] = lm;
+    sh2[w] = ls;
+  }
+  __syncthreads();
+  float m = sh[0], Z = sh2[0];
+  for (int k = 1; k < kSWaves; ++k) merge(m, Z, sh[k], sh2[k]);
+  auto weight = [&](float v) { return __expf((v - m) * it); };
+
+  uint32_t thr = 0;  // kept: weights whose bits are >= thr (all, without top-p)
+  const float tp = a.top_p[row];
+  if (tp < 1.f) {
+    // pass 2: level-1 histogram (weight bits 30..20).  Weights below
+    // x_min = (1 - top_p) * Z / (2N) are left out: all of them together weigh less than
+    // (1 - top_p) * Z / 2, so the top-p boundary lies above them.
+    const float need = fmaxf(tp * Z, 1e-37f);  // top_p = 0 still keeps the largest weight
+    const float x_min = 0.5f * (1.f - tp) * Z / (float)N;
+    for (int b = t; b < kBins; b += kSThreads) hist[b] = 0.f;
+    __syncthreads();
+    for_each([&](int, float v) {
+      const float wv = weight(v);
+      if (wv >= x_min) atomicAdd(&hist[(__float_as_uint(wv) >> 20) & 2047], wv);
+    });
+    __syncthreads();
+    float above;
+    const int b1 = find_crossing(hist, kBins, 0.f, need, sh, &sres, &sres_f, &above);
+    // pass 3: level 2, bits 19..9 of the weights in bin b1
+    for (int b = t; b < kBins; b += kSThreads) hist[b] = 0.f;
+    __syncthreads();
+    for_each([&](int, float v) {
+      const uint32_t bits = __float_as_uint(weight(v));
+      if ((int)((bits >> 20) & 2047) == b1) atomicAdd(&hist[(bits >> 9) & 2047], __uint_as_float(bits));
+    });
+    __syncthreads();
+    const int b2 = find_crossing(hist, kBins, above, need, sh, &sres, &sres_f, &above);
+    // pass 4: level 3, bits 8..0 of the weights in (b1, b2)
+    const uint32_t hi = ((uint32_t)b1 << 11) | (uint32_t)b2;
+    for (int b = t; b < kBins; b += kSThreads) hist[b] = 0.f;
+    __syncthreads();
+    for_each([&](int, float v) {
+      const uint32_t bits = __float_as_uint(weight(v));
+      if ((bits >> 9) == hi) atomicAdd(&hist[bits & 511], __uint_as_float(bits));
+    });
+    __syncthreads();
+    const int b3 = find_crossing(hist, 512, above, need, sh, &sres, &sres_f, &above);
+    thr = (hi << 9) | (uint32_t)b3;
+  }
+
+  // last pass: kept mass per wave segment, prefix over the waves; the wave whose segment
+  // holds the draw, [before, before + km), walks it again step by step to the first kept
+  // token whose running mass reaches the draw
+  auto kept = [&](float v) {
+    const float wv = weight(v);
+    return __float_as_uint(wv) >= thr ? wv : 0.f;
+  };
+  float km = 0.f;
+  for_each([&](int, float v) { km += kept(v); });
+  km = wave_sum(km);
+  __syncthreads();
+  if (lane == 0) sh[w] = km;
+  if (t == 0) s_pick = N - 1;  // a draw past the summed mass (rounding): the last token
+  __syncthreads();
+  float total = 0.f, before = 0.f;
+  for (int k = 0; k < kSWaves; ++k) {
+    if (k < w) before += sh[k];
+    total += sh[k];
+  }
+  const float target = a.u[row] * total;
+  if (before <= target && target < before + km) {
+    float acc = before;
+    for (int s0 = seg0; s0 < seg1; s0 += kStep) {
+      const int i = s0 + 4 * lane;
+      float x[4], kw[4];
+      load4<kVec4>(lg, i, seg1, x);
+      float lsum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kw[e] = i + e < seg1 ? kept(x[e]) : 0.f;
+        lsum += kw[e];
+      }
+      const float incl = wave_scan(lsum);
+      const float step = __shfl(incl, kWave - 1, kWave);
+      if (acc + step >= target) {
+        // the first lane whose running mass reaches the target, then its first element
+        const unsigned long long hit = __ballot(lsum > 0.f && acc + incl >= target);
+        if (hit) {
+          const int l = (int)__builtin_ctzll(hit);
+          if (lane == l) {
+            float run = acc + incl - lsum;
+            int pick = -1;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              run += kw[e];
+              if (pick < 0 && kw[e] > 0.f && run >= target) pick = i + e;
+            }
+            // (the lane's sum reached the target but its own running sum fell short by
+            // rounding: its last kept element)
+            if (pick < 0)
+              for (int e = 0; e < 4; ++e)
+                if (kw[e] > 0.f) pick = i + e;
+            s_pick = pick;
+          }
+          break;
+        }
+      }
+      acc += step;
+    }
+  }
+  __syncthreads();
+  if (t == 0) a.out[row] = s_pick;
+}
+
+}  // namespace
+}  // namespace fqa
+
+using namespace fqa;
+
+extern "C" int fqa_sample(const float* logits, int32_t n_rows, int32_t vocab,
+                          int64_t row_stride, const float* inv_temp, const float* top_p,
+                          const float* u, int32_t* out, void* stream) {
+  if (n_rows < 0 || vocab < 1 || vocab > (1 << 24) || row_stride < vocab) return FQA_EINVAL;
+  if (n_rows == 0) return FQA_OK;
+  if (!logits || !inv_temp || !top_p || !u || !out) return FQA_EINVAL;
+  SampArgs a{logits, vocab, row_stride, inv_temp, top_p, u, out};
+  const bool vec4 = ((uintptr_t)logits & 15) == 0 && (row_stride & 3) == 0;
+  if (vec4)
+    hipLaunchKernelGGL(sample_kernel<true>, dim3((unsigned)n_rows), dim3(kSThreads), 0,
+                       (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(sample_kernel<false>, dim3((unsigned)n_rows), dim3(kSThreads), 0,
+                       (hipStream_t)stream, a);
+  return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
+}

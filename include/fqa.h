@@ -13,6 +13,7 @@
  *   fqa_decode              <- LaunchAttnDecodeCute (split + combine)         (attn_cute.cu:165-261)
  *   fqa_prefill             <- LaunchAttnPrefillCute                          (attn_cute.cu:30-163)
  *   fqa_pool_bytes          <- KvStore pool sizing                            (kv_store.cu:10-46)
+ *   fqa_sample              <- LaunchSampleBatch (greedy / temperature + top-p) (kernels.cu:184-327)
  *
  * Conventions (all entry points):
  *   - Plain device pointers and sizes; every launch goes on the caller's hipStream_t
@@ -234,6 +235,25 @@ int fqa_prefill(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
                 const int32_t* cu_seqlens, const int32_t* positions,
                 const int32_t* pre_items, const int32_t* meta, int32_t pre_tile_q,
                 int32_t pre_item_cap, uint16_t* out, void* stream);
+
+/* Token sampling over fp32 logits, one row per sampling request (LaunchSampleBatch,
+ * kernels.cu:184-327; SampleParams, sampler.h): row b of `logits` (row stride
+ * `row_stride` floats, `vocab` entries) yields out[b]:
+ *   inv_temp[b] <= 0: greedy, the index of the largest logit (the smallest such index
+ *     when several are equal; the reference's tie order follows its thread layout);
+ *   inv_temp[b] > 0: weights w_i = exp((l_i - max) * inv_temp[b]); with top_p[b] < 1 only
+ *     the largest weights are kept, the fewest whose mass reaches top_p[b] * sum(w) (all
+ *     weights equal to the smallest kept one included); the token is the first index i
+ *     (in vocabulary order) at which the running sum of kept weights reaches
+ *     u[b] * (kept mass), u[b] in [0, 1) the caller's uniform draw; a token of zero
+ *     weight is never picked (the reference can pick one for u = 0 exactly), and a
+ *     draw past the summed mass picks the last token, as in the reference.
+ * One 1024-thread workgroup per row.  Weights are summed in fp32 (as the reference does),
+ * so a draw that lands within the rounding of a cumulative-mass boundary can pick either
+ * neighbour.  vocab in [1, 2^24], n_rows >= 0. */
+int fqa_sample(const float* logits, int32_t n_rows, int32_t vocab, int64_t row_stride,
+               const float* inv_temp, const float* top_p, const float* u, int32_t* out,
+               void* stream);
 
 /* Library version string. */
 const char* fqa_version(void);

@@ -447,3 +447,71 @@ void fqo_prefill(int n_q, int n_kv, int D, int stride, float scale, const uint16
     free(ok);
   }
 }
+
+/* ArgmaxKernel + SampleKernel (kernels.cu:184-327) restated in fp64 for one row each:
+ * inv_temp <= 0: index of the largest logit (smallest index among equals);
+ * else w_i = exp((l_i - max) * inv_temp); with top_p < 1 the kept set is the fewest
+ * largest weights whose mass reaches top_p * sum(w) (weights equal to the smallest kept
+ * one included; the reference's 32-step bisection converges to this set); the token is
+ * the first index, in vocabulary order, whose running kept mass reaches u * (kept mass),
+ * skipping zero weights; the last token when the draw lies past the summed mass.
+ * kept_thr[b] / kept_mass[b] (optional) receive the smallest kept weight and the kept
+ * mass, so tests can judge a pick that fp32 rounding moved across a boundary. */
+static int cmp_desc(const void* a, const void* b) {
+  double x = *(const double*)a, y = *(const double*)b;
+  return x < y ? 1 : (x > y ? -1 : 0);
+}
+void fqo_sample(const float* logits, int n_rows, int vocab, int64_t stride,
+                const float* inv_temp, const float* top_p, const float* u, int32_t* out,
+                double* kept_thr, double* kept_mass) {
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int b = 0; b < n_rows; ++b) {
+    const float* lg = logits + (int64_t)b * stride;
+    if (inv_temp[b] <= 0.f) {
+      int bi = 0;
+      for (int i = 1; i < vocab; ++i)
+        if (lg[i] > lg[bi]) bi = i;
+      out[b] = bi;
+      if (kept_thr) kept_thr[b] = 0.0;
+      if (kept_mass) kept_mass[b] = 0.0;
+      continue;
+    }
+    double m = -INFINITY;
+    for (int i = 0; i < vocab; ++i) if (lg[i] > m) m = lg[i];
+    double* w = (double*)malloc(sizeof(double) * (size_t)vocab);
+    double z = 0.0;
+    for (int i = 0; i < vocab; ++i) {
+      w[i] = exp(((double)lg[i] - m) * (double)inv_temp[b]);
+      z += w[i];
+    }
+    double thr = 0.0;
+    if (top_p[b] < 1.f) {
+      double* s = (double*)malloc(sizeof(double) * (size_t)vocab);
+      memcpy(s, w, sizeof(double) * (size_t)vocab);
+      qsort(s, (size_t)vocab, sizeof(double), cmp_desc);
+      const double need = (double)top_p[b] * z;
+      double acc = 0.0;
+      thr = s[0];  /* top_p = 0 keeps the largest weight */
+      for (int k = 0; k < vocab; ++k) {
+        acc += s[k];
+        thr = s[k];
+        if (acc >= need) break;
+      }
+      free(s);
+    }
+    double mass = 0.0;
+    for (int i = 0; i < vocab; ++i) if (w[i] >= thr) mass += w[i];
+    const double target = (double)u[b] * mass;
+    int pick = vocab - 1;
+    double acc = 0.0;
+    for (int i = 0; i < vocab; ++i) {
+      if (w[i] < thr || w[i] <= 0.0) continue;
+      acc += w[i];
+      if (acc >= target) { pick = i; break; }
+    }
+    out[b] = pick;
+    if (kept_thr) kept_thr[b] = thr;
+    if (kept_mass) kept_mass[b] = mass;
+    free(w);
+  }
+}

@@ -58,6 +58,11 @@ int64_t fqo_pool_offset(int n_kv, int head_dim, int64_t page, int kvh, int plane
 
 int fqo_num_threads(void);
 
+/* LaunchSampleBatch (kernels.cu:184-327) in fp64; kept_thr / kept_mass may be NULL. */
+void fqo_sample(const float* logits, int n_rows, int vocab, int64_t stride,
+                const float* inv_temp, const float* top_p, const float* u, int32_t* out,
+                double* kept_thr, double* kept_mass);
+
 #ifdef __cplusplus
 }
 #endif

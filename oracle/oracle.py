@@ -125,3 +125,20 @@ def prefill(qkv, pool, pool_pages, block_tables, max_blocks, cu_seqlens, positio
 
 def pool_offset(page, kvh, plane, tok, d, n_kv=8, head_dim=128) -> int:
     return int(load().fqo_pool_offset(n_kv, head_dim, page, kvh, plane, tok, d))
+
+
+def sample(logits, inv_temp, top_p, u):
+    """LaunchSampleBatch restated in fp64 (oracle/fqa_oracle.c, fqo_sample): returns the
+    picked token per row, the smallest kept weight and the kept mass (both fp64)."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    B, N = logits.shape
+    f32 = lambda x: np.ascontiguousarray(x, np.float32)  # noqa: E731
+    it, tp, uu = f32(inv_temp), f32(top_p), f32(u)
+    out = np.zeros(max(B, 1), np.int32)
+    thr = np.zeros(max(B, 1), np.float64)
+    mass = np.zeros(max(B, 1), np.float64)
+    lib = load()
+    lib.fqo_sample.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int64, C.c_void_p, C.c_void_p,
+                               C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+    lib.fqo_sample(_p(logits), B, N, N, _p(it), _p(tp), _p(uu), _p(out), _p(thr), _p(mass))
+    return out[:B].copy(), thr[:B].copy(), mass[:B].copy()

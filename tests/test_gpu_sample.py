@@ -1,0 +1,94 @@
+"""fqa_sample on the GPU (LaunchSampleBatch, kernels.cu:184-327) against the fp64 oracle
+(oracle/fqa_oracle.c, fqo_sample), through the C ABI.  Greedy rows: bit-exact.  Sampled
+rows: the kernel sums fp32 weights (as the reference does), so its pick is checked for
+what fp32 rounding cannot change: the token is kept (weight >= the oracle's smallest kept
+weight, within 1e-5 relative), and its cumulative-mass interval in vocabulary order,
+computed in fp64, contains the draw u * (kept mass) within 1e-4 of the kept mass; and
+nearly every pick must equal the oracle's exactly."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+VOCAB = 151936  # Qwen3 vocabulary
+
+
+def _run(lg, it, tp, u):
+    import torch
+
+    from flashqwen_amd.sample import sample
+
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()  # noqa: E731
+    out = sample(t(lg), t(it), t(tp), t(u))
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def _check_sampled(lg, it, tp, u, got):
+    from oracle import oracle as orc
+
+    ref, thr, mass = orc.sample(lg, it, tp, u)
+    exact = 0
+    for b in range(lg.shape[0]):
+        w = np.exp((lg[b].astype(np.float64) - lg[b].max()) * it[b])
+        kept = np.where((w >= thr[b] * (1 - 1e-5)) & (w > 0), w, 0.0)
+        g = int(got[b])
+        assert 0 <= g < lg.shape[1]
+        assert kept[g] > 0, (b, g, w[g], thr[b])
+        cum = np.cumsum(kept)
+        target, tol = u[b] * mass[b], 1e-4 * mass[b]
+        lo = cum[g - 1] if g > 0 else 0.0
+        assert lo - tol <= target <= cum[g] + tol, (b, g, int(ref[b]), lo, cum[g], target)
+        exact += g == ref[b]
+    return exact
+
+
+@pytest.mark.gpu
+def test_greedy_rows_bit_exact(gpu):
+    from oracle import oracle as orc
+
+    print("[test_greedy_rows_bit_exact] 64 rows x 151936", flush=True)
+    rng = np.random.default_rng(11)
+    B = 64
+    lg = (rng.standard_normal((B, VOCAB)) * 4).astype(np.float32)
+    lg[3, [5, 90000]] = 50.0          # a tie: the smaller index wins
+    lg[7, :] = -np.inf                # all -inf: token 0
+    it = np.zeros(B, np.float32)
+    got = _run(lg, it, np.ones(B, np.float32), rng.random(B).astype(np.float32))
+    ref = orc.sample(lg, it, np.ones(B, np.float32), np.zeros(B, np.float32))[0]
+    assert np.array_equal(got, ref)
+    assert got[3] == 5 and got[7] == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("vocab", [VOCAB, 1001, 64, 1])
+def test_sampled_rows(gpu, vocab):
+    print(f"[test_sampled_rows] vocab {vocab}", flush=True)
+    rng = np.random.default_rng(12 + vocab)
+    B = 96
+    scale = rng.choice([0.5, 2.0, 6.0], size=B)
+    lg = (rng.standard_normal((B, vocab)) * scale[:, None]).astype(np.float32)
+    it = rng.choice([0.5, 1.0, 1.7], size=B).astype(np.float32)
+    tp = rng.choice([1.0, 0.95, 0.8, 0.5, 0.1, 0.0], size=B).astype(np.float32)
+    u = rng.random(B).astype(np.float32)
+    u[:4] = [0.0, 0.5, 0.999999, 0.25]
+    got = _run(lg, it, tp, u)
+    exact = _check_sampled(lg, it, tp, u, got)
+    print(f"vocab {vocab}: {exact}/{B} picks equal the fp64 oracle's")
+    assert exact >= B - 3
+
+
+@pytest.mark.gpu
+def test_sampled_closed_forms(gpu):
+    """Uniform logits, top_p = 1: token ceil(u*N) - 1 (up to one token of fp32 rounding);
+    top_p = 0 keeps only the largest weight: the argmax."""
+    rng = np.random.default_rng(13)
+    B = 32
+    u = rng.random(B).astype(np.float32)
+    lg = np.full((B, VOCAB), 1.25, np.float32)
+    got = _run(lg, np.ones(B, np.float32), np.ones(B, np.float32), u)
+    want = np.ceil(u.astype(np.float64) * VOCAB).astype(np.int64) - 1
+    assert np.all(np.abs(got - want) <= 1), (got, want)
+    lg = rng.standard_normal((B, VOCAB)).astype(np.float32)
+    got = _run(lg, np.full(B, 0.8, np.float32), np.zeros(B, np.float32), u)
+    assert np.array_equal(got, lg.argmax(axis=1))

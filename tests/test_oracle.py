@@ -413,3 +413,71 @@ def test_schedule_config4_known_batch():
     assert list(nn[:256]) == [1] * 256  # decodes first
     assert sorted(nn[256:259].tolist()) == [512, 700, 900]
     assert nn[259:].tolist() == [2048, 2048] and list(rem[259:]) == [4096, 4096]
+
+
+# ---- sampling (fqo_sample, kernels.cu:184-327) ------------------------------------------
+
+def _sample_numpy(lg, it, tp, u):
+    """Independent formulation: numpy sort + cumsum + searchsorted, fp64."""
+    if it <= 0:
+        return int(np.argmax(lg))
+    w = np.exp((lg.astype(np.float64) - lg.max()) * it)
+    thr = 0.0
+    if tp < 1:
+        s = np.sort(w)[::-1]
+        k = int(np.searchsorted(np.cumsum(s), tp * w.sum()))  # first k with cum >= need
+        thr = s[min(k, len(s) - 1)]
+    kept = np.where((w >= thr) & (w > 0), w, 0.0)
+    cum = np.cumsum(kept)
+    i = int(np.searchsorted(cum, u * cum[-1]))  # first i with cum >= target
+    while i < len(kept) and kept[i] == 0.0:
+        i += 1
+    return min(i, len(lg) - 1)
+
+
+def test_sample_known_answer():
+    """logits 0..7, temperature 1: w = e^(l-7), sum 1.5814; u = 0.5 -> target 0.7907, the
+    first seven weights sum to 0.5814, so token 7; u = 0 -> token 0; top_p = 0.5 keeps only
+    token 7 (its weight 1 >= 0.79); greedy -> 7."""
+    from oracle import oracle as orc
+
+    lg = np.arange(8, dtype=np.float32)[None, :]
+    assert orc.sample(lg, [1.0], [1.0], [0.5])[0][0] == 7
+    assert orc.sample(lg, [1.0], [1.0], [0.0])[0][0] == 0
+    assert orc.sample(lg, [1.0], [1.0], [0.30])[0][0] == 6   # 0.474 in (0.2141, 0.5814]
+    pick, thr, mass = orc.sample(lg, [1.0], [0.5], [0.2])
+    assert pick[0] == 7 and thr[0] == 1.0 and mass[0] == 1.0
+    assert orc.sample(lg, [0.0], [1.0], [0.5])[0][0] == 7
+
+
+def test_sample_closed_forms():
+    from oracle import oracle as orc
+
+    rng = np.random.default_rng(3)
+    N = 1000
+    # uniform logits, top_p = 1: the pick is ceil(u*N) - 1
+    for u in (0.0005, 0.1234, 0.5, 0.99951):
+        lg = np.full((1, N), 2.5, np.float32)
+        assert orc.sample(lg, [0.7], [1.0], [u])[0][0] == int(np.ceil(u * N)) - 1
+    # top_p -> 0 keeps only the largest weight: the argmax, whatever u
+    lg = rng.standard_normal((4, N)).astype(np.float32)
+    for b in range(4):
+        assert orc.sample(lg[b:b + 1], [1.3], [1e-6], [rng.random()])[0][0] == int(np.argmax(lg[b]))
+    # greedy: the first index of the maximum
+    lg = rng.standard_normal((1, N)).astype(np.float32)
+    lg[0, [17, 400]] = 9.0
+    assert orc.sample(lg, [0.0], [1.0], [0.3])[0][0] == 17
+
+
+def test_sample_against_numpy():
+    from oracle import oracle as orc
+
+    rng = np.random.default_rng(4)
+    for trial in range(60):
+        N = int(rng.integers(2, 300))
+        lg = (rng.standard_normal((1, N)) * rng.choice([0.5, 3.0])).astype(np.float32)
+        it = float(rng.choice([0.0, 0.5, 1.0, 2.0]))
+        tp = float(rng.choice([1.0, 0.95, 0.6, 0.1]))
+        u = float(rng.random())
+        got = orc.sample(lg, [it], [tp], [u])[0][0]
+        assert got == _sample_numpy(lg[0], it, tp, u), (trial, N, it, tp, u)
