@@ -12,9 +12,11 @@
 // The reference finds the top-p threshold by 32 bisection passes over the row, each
 // recomputing every weight; here it is a 3-level radix select on the weights' float bits
 // (bits 30..20, 19..9, 8..0; positive floats order like their bit patterns), with mass
-// histograms in LDS (ds_add_f32): the exact smallest kept weight after 3 passes.  A
-// sampled row is read 6 times (max, sum + level 1, level 2, level 3, kept mass, pick),
-// against 35 in the reference; the later passes mostly hit the L2 and the MALL.
+// histograms in LDS (ds_add_f32): the exact smallest kept weight after 3 passes.  The
+// level-3 histograms are kept per wave, so the same pass also gives each wave's kept
+// mass.  A top-p row is read 4 times in full (max + sum, level 1, level 2, level 3 + kept
+// mass), a temperature-only row once (its kept mass per wave is the rescaled pass-1 sum),
+// against 35 in the reference; the pick then reads 1/16 of one wave's segment twice.
 
 #include "fqa_common.h"
 
@@ -223,6 +225,9 @@ __global__ void __launch_bounds__(kSThreads) sample_kernel(SampArgs a) {
   for (int k = 1; k < kSWaves; ++k) merge(m, Z, sh[k], sh2[k]);
   auto weight = [&](float v) { return __expf((v - m) * it); };
 
+  // skm[w]: the kept mass of wave w's segment
+  __shared__ float skm[kSWaves];
+  __shared__ float hist3[kSWaves][512];
   uint32_t thr = 0;  // kept: weights whose bits are >= thr (all, without top-p)
   const float tp = a.top_p[row];
   if (tp < 1.f) {
@@ -249,78 +254,141 @@ __global__ void __launch_bounds__(kSThreads) sample_kernel(SampArgs a) {
     });
     __syncthreads();
     const int b2 = find_crossing(hist, kBins, above, need, sh, &sres, &sres_f, &above);
-    // pass 4: level 3, bits 8..0 of the weights in (b1, b2)
+    // pass 4: level 3 (bits 8..0 of the weights in (b1, b2)) as one histogram per wave,
+    // and per wave the mass of the weights above (b1, b2), which are all kept: the
+    // kept mass per wave then follows from the histograms without another pass
     const uint32_t hi = ((uint32_t)b1 << 11) | (uint32_t)b2;
-    for (int b = t; b < kBins; b += kSThreads) hist[b] = 0.f;
+    float* h3 = &hist3[0][0];
+    for (int b = t; b < kSWaves * 512; b += kSThreads) h3[b] = 0.f;
     __syncthreads();
+    float km_hi = 0.f;
     for_each([&](int, float v) {
-      const uint32_t bits = __float_as_uint(weight(v));
-      if ((bits >> 9) == hi) atomicAdd(&hist[bits & 511], __uint_as_float(bits));
+      const float wv = weight(v);
+      const uint32_t bits = __float_as_uint(wv);
+      if ((bits >> 9) > hi) km_hi += wv;
+      else if ((bits >> 9) == hi) atomicAdd(&hist3[w][bits & 511], wv);
     });
+    __syncthreads();
+    if (t < 512) {
+      float s = 0.f;
+      for (int k = 0; k < kSWaves; ++k) s += hist3[k][t];
+      hist[t] = s;
+    }
     __syncthreads();
     const int b3 = find_crossing(hist, 512, above, need, sh, &sres, &sres_f, &above);
     thr = (hi << 9) | (uint32_t)b3;
+    float km = km_hi;
+    for (int b = b3 + lane; b < 512; b += kWave) km += hist3[w][b];
+    km = wave_sum(km);
+    if (lane == 0) skm[w] = km;
+  } else {
+    // every weight is kept: wave w's mass is its pass-1 sum rescaled to the row max
+    if (t < kSWaves) skm[t] = sh[t] == -INFINITY ? 0.f : sh2[t] * __expf((sh[t] - m) * it);
   }
+  __syncthreads();
 
-  // last pass: kept mass per wave segment, prefix over the waves; the wave whose segment
-  // holds the draw, [before, before + km), walks it again step by step to the first kept
-  // token whose running mass reaches the draw
+  // the pick: the wave whose kept mass [before, before + km) holds the draw u * total;
+  // its segment is split into kSWaves sub-segments whose kept masses all waves sum at
+  // once, and the wave owning the sub-segment that holds the draw walks it step by step
+  // to the first kept token whose running mass reaches the draw
   auto kept = [&](float v) {
     const float wv = weight(v);
     return __float_as_uint(wv) >= thr ? wv : 0.f;
   };
-  float km = 0.f;
-  for_each([&](int, float v) { km += kept(v); });
-  km = wave_sum(km);
-  __syncthreads();
-  if (lane == 0) sh[w] = km;
-  if (t == 0) s_pick = N - 1;  // a draw past the summed mass (rounding): the last token
-  __syncthreads();
-  float total = 0.f, before = 0.f;
-  for (int k = 0; k < kSWaves; ++k) {
-    if (k < w) before += sh[k];
-    total += sh[k];
-  }
+  float total = 0.f;
+  for (int k = 0; k < kSWaves; ++k) total += skm[k];
   const float target = a.u[row] * total;
-  if (before <= target && target < before + km) {
-    float acc = before;
-    for (int s0 = seg0; s0 < seg1; s0 += kStep) {
+  int ws = -1;
+  float before = 0.f;
+  {
+    float acc = 0.f;
+    for (int k = 0; k < kSWaves; ++k) {
+      if (ws < 0 && acc <= target && target < acc + skm[k]) {
+        ws = k;
+        before = acc;
+      }
+      acc += skm[k];
+    }
+  }
+  if (ws < 0) {  // a draw past the summed mass (rounding): the last token
+    if (t == 0) a.out[row] = N - 1;
+    return;
+  }
+  const int S0 = min(ws * seg, N), S1 = min(S0 + seg, N);
+  const int sub = ((S1 - S0 + kSWaves * kStep - 1) / (kSWaves * kStep)) * kStep;
+  const int u0 = min(S0 + w * sub, S1), u1 = min(u0 + sub, S1);
+  float m2 = 0.f;
+  for (int s0 = u0; s0 < u1; s0 += kStep) {
+    const int i = s0 + 4 * lane;
+    float x[4];
+    load4<kVec4>(lg, i, u1, x);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (i + e < u1) m2 += kept(x[e]);
+  }
+  m2 = wave_sum(m2);
+  if (lane == 0) sh2[w] = m2;
+  if (t == 0) s_pick = N - 1;
+  __syncthreads();
+  // the walker: the last sub-segment with kept mass that starts at or below the draw
+  // (the first one with kept mass if rounding puts the draw below them all)
+  int wk = -1, first = -1;
+  float b2v = before, wb = before;
+  for (int k = 0; k < kSWaves; ++k) {
+    if (sh2[k] > 0.f) {
+      if (first < 0) first = k;
+      if (b2v <= target) {
+        wk = k;
+        wb = b2v;
+      }
+    }
+    b2v += sh2[k];
+  }
+  if (wk < 0) {
+    wk = first;
+    wb = before;
+  }
+  if (w == wk) {
+    float acc = wb;
+    int last = -1;  // the last kept token walked so far
+    for (int s0 = u0; s0 < u1; s0 += kStep) {
       const int i = s0 + 4 * lane;
       float x[4], kw[4];
-      load4<kVec4>(lg, i, seg1, x);
+      load4<kVec4>(lg, i, u1, x);
       float lsum = 0.f;
+      int llast = -1;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        kw[e] = i + e < seg1 ? kept(x[e]) : 0.f;
+        kw[e] = i + e < u1 ? kept(x[e]) : 0.f;
         lsum += kw[e];
+        if (kw[e] > 0.f) llast = i + e;
       }
       const float incl = wave_scan(lsum);
       const float step = __shfl(incl, kWave - 1, kWave);
-      if (acc + step >= target) {
-        // the first lane whose running mass reaches the target, then its first element
-        const unsigned long long hit = __ballot(lsum > 0.f && acc + incl >= target);
-        if (hit) {
-          const int l = (int)__builtin_ctzll(hit);
-          if (lane == l) {
-            float run = acc + incl - lsum;
-            int pick = -1;
+      // the first lane whose running mass reaches the draw, then its first such element
+      const unsigned long long hit = __ballot(lsum > 0.f && acc + incl >= target);
+      if (hit) {
+        const int l = (int)__builtin_ctzll(hit);
+        if (lane == l) {
+          float run = acc + incl - lsum;
+          // the first element whose running sum reaches the draw; if rounding leaves the
+          // lane's own running sum short, its last kept element
+          int pick = -1;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              run += kw[e];
-              if (pick < 0 && kw[e] > 0.f && run >= target) pick = i + e;
-            }
-            // (the lane's sum reached the target but its own running sum fell short by
-            // rounding: its last kept element)
-            if (pick < 0)
-              for (int e = 0; e < 4; ++e)
-                if (kw[e] > 0.f) pick = i + e;
-            s_pick = pick;
+          for (int e = 0; e < 4; ++e) {
+            run += kw[e];
+            if (pick < 0 && kw[e] > 0.f && run >= target) pick = i + e;
           }
-          break;
+          s_pick = pick >= 0 ? pick : llast;
         }
+        last = -2;
+        break;
       }
+      const unsigned long long has = __ballot(llast >= 0);
+      if (has) last = __shfl(llast, 63 - __builtin_clzll(has), kWave);
       acc += step;
     }
+    if (last >= 0 && lane == 0) s_pick = last;  // the draw lies past this sub-segment's sum
   }
   __syncthreads();
   if (t == 0) a.out[row] = s_pick;
