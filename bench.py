@@ -283,7 +283,7 @@ def bench_sampler(args):
     """fqa_sample on 256 rows of 151936 fp32 logits (one sampling row per request of a
     256-sequence decode step): greedy, temperature 1, temperature 1 + top-p 0.9.  The
     roofline is HBM: one read of the logits (B*N*4 bytes) per launch; the kernel reads a
-    sampled row up to 6 times (the later passes mostly from L2 / MALL)."""
+    row once for greedy and temperature-only sampling, 4 times with top-p."""
     import torch
 
     from flashqwen_amd.sample import sample

@@ -72,6 +72,10 @@ def test_sampled_rows(gpu, vocab):
     tp = rng.choice([1.0, 0.95, 0.8, 0.5, 0.1, 0.0], size=B).astype(np.float32)
     u = rng.random(B).astype(np.float32)
     u[:4] = [0.0, 0.5, 0.999999, 0.25]
+    if vocab >= 64:  # masked tokens (-inf logits) weigh 0 and are never picked
+        mask = rng.random((12, vocab)) < 0.3
+        mask[:, 0] = False
+        lg[4:16][mask] = -np.inf
     got = _run(lg, it, tp, u)
     exact = _check_sampled(lg, it, tp, u, got)
     print(f"vocab {vocab}: {exact}/{B} picks equal the fp64 oracle's")
