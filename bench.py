@@ -54,6 +54,11 @@ def parse():
     ap.add_argument("--sampler", action="store_true",
                     help="only measure fqa_sample (256 rows x 151936 logits: greedy, "
                          "temperature, temperature + top-p 0.9)")
+    ap.add_argument("--gemm", action="store_true",
+                    help="only measure fqa_gemm on the Qwen3-8B projections (decode and "
+                         "prefill row counts) beside torch.matmul (hipBLASLt)")
+    ap.add_argument("--gemm-rows", type=str, default="128,256,1024,8192",
+                    help="row counts for --gemm")
     return ap.parse_args()
 
 
@@ -78,6 +83,9 @@ def main():
 
     if args.sampler:
         bench_sampler(args)
+        return
+    if args.gemm:
+        bench_gemm(args)
         return
 
     import torch
@@ -317,6 +325,67 @@ def bench_sampler(args):
         res[name] = {"us": round(us, 2), "rows_per_s": round(B / (us * 1e-6), 1),
                      "logit_GBps": round(B * N * 4 / (us * 1e-6) / 1e9, 1)}
     print(json.dumps({"sampler": res, "rows": B, "vocab": N, "peak_GBps": HBM_PEAK_GBS}))
+
+
+GEMM_SHAPES = {"qkv": (6144, 4096), "o_proj": (4096, 4096), "gate_up": (24576, 4096),
+               "down": (4096, 12288), "lm_head": (151936, 4096)}
+
+
+def bench_gemm(args):
+    """fqa_gemm on the Qwen3-8B projections (N, K) at several row counts M, beside
+    torch.matmul (hipBLASLt) on the same tensors.  Algorithmic work: 2MNK FLOP; bytes
+    (M K + N K + M N) * 2 (fp32 logits for lm_head).  lm_head only at M <= 256 (sampling
+    rows).  Each timing replays a graph of 20 calls 10 times."""
+    import torch
+
+    from flashqwen_amd.gemm import gemm
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for _ in range(20):
+                fn()
+        gr.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / 200
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3)
+    rows = [int(v) for v in args.gemm_rows.split(",")]
+    out = {}
+    for name, (N, K) in GEMM_SHAPES.items():
+        w = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        f32 = name == "lm_head"
+        for M in rows:
+            if f32 and M > 256:
+                continue
+            x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+            y = torch.empty(M, N, device="cuda", dtype=torch.float32 if f32 else torch.bfloat16)
+            us = timed(lambda: gemm(x, w, out=y, out_f32=f32))
+            if f32:
+                # hipBLASLt has no bf16 x bf16 -> fp32 path in torch.matmul: bf16 + cast
+                ut = timed(lambda: torch.matmul(x, w.t()).float())
+            else:
+                yt = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+                ut = timed(lambda: torch.matmul(x, w.t(), out=yt))
+            fl = 2.0 * M * N * K
+            by = (M * K + N * K) * 2 + M * N * (4 if f32 else 2)
+            out[f"{name}_M{M}"] = {
+                "us": round(us, 2), "TFLOPs": round(fl / us / 1e6, 1),
+                "GBps": round(by / us / 1e3, 1), "torch_us": round(ut, 2),
+                "speedup": round(ut / us, 2)}
+            print(name, M, out[f"{name}_M{M}"], flush=True)
+            del x, y
+        del w
+    print(json.dumps({"gemm": out, "peak_TFLOPs": 2516.6, "peak_GBps": HBM_PEAK_GBS}))
 
 
 def _profile_traffic(config: int, kernels: list[str]):

@@ -1,0 +1,363 @@
+// fqa_gemm.hip — the layer projections y = x · W^T on bf16 MFMA (gfx950).
+//
+// Replaces LaunchGemm (engine/src/kernels.cu:9-16: cublasGemmEx, bf16 in, fp32 compute,
+// bf16 or fp32 out), which the step calls for QKV, o_proj, gate-up, down and lm_head
+// (engine/src/model_runtime.cu:261, 280, 285, 288, 322).  x is [M, K] and W is [N, K],
+// both K-contiguous (the reference's weight layout), y is [M, N].
+//
+// MI355X design:
+//  * One 256-thread workgroup (4 waves) per output tile of 256, 128, 64 or 32 rows by 128
+//    columns (the smallest that covers M; 256 above 128 rows).  A wave owns a block of
+//    32 x 32 v_mfma_f32_32x32x16_bf16 tiles (4 x 2 of them in the 256 x 128 tile: 128
+//    fp32 accumulators per lane, 6 KiB of fragment reads per 8 MFMAs).
+//  * K advances 64 at a time.  Both operand tiles of a k step move global -> LDS by DMA
+//    (global_load_lds_dwordx4, 1 KiB per wave instruction) into a ring of 3 to 8 steps
+//    (as deep as 160 KiB of LDS allows), all but one in flight ahead of the MFMAs: the
+//    small-M tiles are streams of W, and the deeper ring keeps ~64-100 KiB of W in flight
+//    per CU, what HBM latency needs at a CU's share of 8 TB/s.  A DMA lane's 16 bytes land
+//    at LDS byte 16 * lane, so the bank swizzle is applied on the read side of the DMA:
+//    LDS chunk c of row r holds global chunk c ^ (r & 7), and the ds_read_b128 fragment
+//    reads of 8 consecutive rows hit 8 distinct 16-byte bank groups.
+//  * Shapes with few tiles (decode steps) split K over `splits` workgroups per tile so
+//    that one round of workgroups fills the 256 CUs; each writes fp32 partials and a
+//    second kernel sums them into y.
+//  * Workgroups are dealt to the 8 XCDs round robin; tile_of() renumbers them so that the
+//    workgroups on one XCD walk 8 m tiles per n tile and share W and x tiles in its L2.
+
+#include "fqa_common.h"
+
+namespace fqa {
+namespace {
+
+constexpr int kGK = 64;  // K granularity of the shapes accepted (k steps are 32 or 64)
+
+// Tile shapes.  kWM x kWN waves; a wave owns kTM x kTN blocks of 32 x 32 outputs; K
+// advances kBK (32 or 64) per step, through a ring of kRing steps in LDS (kRing - 1 in
+// flight ahead of the MFMAs).  An LDS row of a step holds kBK bf16 (kPitch bytes) in
+// 16-byte chunks, chunk c of row r at c ^ swz(r): (r >> 1) & 7 for 8 chunks, (r >> 2) & 3
+// for 4.  A ds_read_b128 is served 16 lanes at a time from the 64 banks (256 bytes); the
+// 16 lanes of a fragment read take one chunk of 16 consecutive rows, and with this swizzle
+// those land on 16 distinct 16-byte bank groups.
+template <int kWM_, int kWN_, int kTM_, int kTN_, int kRing_, int kBK_ = 64>
+struct Tile {
+  static constexpr int kWM = kWM_, kWN = kWN_, kTM = kTM_, kTN = kTN_, kRing = kRing_;
+  static constexpr int kBK = kBK_, kPitch = kBK * 2, kChunks = kBK / 8, kKK = kBK / 16;
+  static constexpr int kRowsPerDma = 1024 / kPitch;
+  static constexpr int kBM = kWM * kTM * 32, kBN = kWN * kTN * 32;
+  static constexpr int kABytes = kBM * kPitch, kBBytes = kBN * kPitch;
+  static constexpr int kStage = kABytes + kBBytes;
+  static constexpr int kWaves = kWM * kWN, kThreads = 64 * kWaves;
+  // DMA instructions per wave per step
+  static constexpr int kDmaA = kBM / kRowsPerDma / kWaves, kDmaB = kBN / kRowsPerDma / kWaves;
+  static_assert(kBK == 32 || kBK == 64, "k step");
+  static_assert(kWaves == 4 || kWaves == 8, "4 or 8 waves");
+  static_assert(kDmaA * kRowsPerDma * kWaves == kBM && kDmaB * kRowsPerDma * kWaves == kBN,
+                "DMA split");
+  static_assert(kRing * kStage <= 160 * 1024, "LDS");
+  static_assert((kRing - 1) * (kDmaA + kDmaB) < 64, "vmcnt");
+  __device__ static int swz(int r) { return kChunks == 8 ? ((r >> 1) & 7) : ((r >> 2) & 3); }
+};
+using TileL = Tile<2, 4, 4, 2, 4, 32>;  // 256 x 256 on 8 waves: prefill-sized M
+using TileL8 = Tile<4, 2, 2, 2, 3>;     // 256 x 128 on 8 waves: 129..1024 rows
+using TileM = Tile<2, 2, 2, 2, 5>;      // 128 x 128
+using TileS = Tile<1, 4, 2, 1, 6>;      // 64 x 128
+using TileT = Tile<1, 4, 1, 1, 8>;      // 32 x 128: a few decode rows
+
+struct GemmArgs {
+  const uint16_t* x;
+  const uint16_t* w;
+  void* y;
+  float* part;  // [splits][M][N] fp32 when splits > 1
+  long long ldx, ldw, ldy;
+  int M, N, K;
+  int splits;
+  int m_tiles, n_tiles;
+};
+
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile(
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(off), "s"(base), "{m0}"(lds)
+      : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+// Wait until at most n * kPer of this wave's loads are outstanding, n in [0, kMax].
+template <int kPer, int kMax>
+__device__ __forceinline__ void wait_steps(int n) {
+  if constexpr (kMax <= 0) {
+    wait_vm<0>();
+  } else {
+    if (n >= kMax)
+      wait_vm<kMax * kPer>();
+    else
+      wait_steps<kPer, kMax - 1>(n);
+  }
+}
+__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// Workgroup -> (m tile, n tile, split).  Workgroups are dealt to the 8 XCDs round robin,
+// so the linear id is first turned into an index that runs contiguously within an XCD;
+// that index walks the tiles in groups of 8 m tiles per n tile (consecutive workgroups on
+// an XCD share a W tile, and 4 consecutive n tiles share the group's x tiles in L2).
+__device__ __forceinline__ void tile_of(const GemmArgs& a, int& tm, int& tn, int& sp) {
+  const int G = a.m_tiles * a.n_tiles * a.splits;
+  const int L = blockIdx.x;
+  int t = L;
+  if ((G & 7) == 0) t = (L & 7) * (G >> 3) + (L >> 3);
+  const int per = a.m_tiles * a.n_tiles;
+  sp = t / per;
+  t -= sp * per;
+  constexpr int kGroup = 8;
+  const int span = kGroup * a.n_tiles;
+  const int g = t / span, m0 = g * kGroup;
+  const int gs = min(a.m_tiles - m0, kGroup);
+  const int r = t - g * span;
+  tm = m0 + r % gs;
+  tn = r / gs;
+}
+
+template <class T, bool kF32Out, bool kPartial>
+__global__ void __launch_bounds__(T::kThreads, 1) gemm_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(1024))) char lds[T::kRing * T::kStage];
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w % T::kWM, wn = w / T::kWM;
+  int tm, tn, sp;
+  tile_of(a, tm, tn, sp);
+  const int row0 = tm * T::kBM, col0 = tn * T::kBN;
+  // split sp takes k steps sp, sp + splits, sp + 2 splits, ...: the splits of a tile run
+  // side by side and read adjacent pieces of the same W rows
+  const int nst = a.K / T::kBK;
+  const int n_my = (nst - sp + a.splits - 1) / a.splits;
+  const int kstride = a.splits * T::kBK;
+  const uint16_t* xk = a.x + (long long)sp * T::kBK;
+  const uint16_t* wk = a.w + (long long)sp * T::kBK;
+
+  // DMA sources: wave w's instruction i covers rows kRowsPerDma (w kDmaA + i) + lane /
+  // kChunks of the x tile (likewise of the W tile); lane fills LDS chunk lane % kChunks
+  // of its row, so it reads global chunk (lane % kChunks) ^ swz(row)
+  const int drow = lane / T::kChunks, dlc = lane % T::kChunks;
+  uint32_t off_a[T::kDmaA], off_b[T::kDmaB];
+#pragma unroll
+  for (int i = 0; i < T::kDmaA; ++i) {
+    const int tr = T::kRowsPerDma * (w * T::kDmaA + i) + drow;  // row within the tile
+    const int r = min(row0 + tr, a.M - 1);
+    off_a[i] = (uint32_t)((long long)r * a.ldx * 2) + (dlc ^ T::swz(tr)) * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < T::kDmaB; ++i) {
+    const int tr = T::kRowsPerDma * (w * T::kDmaB + i) + drow;
+    off_b[i] = (uint32_t)((long long)(col0 + tr) * a.ldw * 2) + (dlc ^ T::swz(tr)) * 16;
+  }
+  auto issue = [&](int j) {  // this workgroup's j-th k step
+    const uint32_t dst = lds_base + (j % T::kRing) * T::kStage;
+    const uint16_t* xa = xk + (long long)j * kstride;
+    const uint16_t* wb = wk + (long long)j * kstride;
+#pragma unroll
+    for (int i = 0; i < T::kDmaA; ++i) dma16(xa, off_a[i], dst + (w * T::kDmaA + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < T::kDmaB; ++i)
+      dma16(wb, off_b[i], dst + T::kABytes + (w * T::kDmaB + i) * 1024);
+  };
+
+  // fragment reads: lane reads row (lane & 31) of a 32-row block, k chunk 2 kk + lane/32,
+  // stored at chunk (2 kk + lane/32) ^ swz(lane & 31)
+  const int a_off = (wm * T::kTM * 32 + (lane & 31)) * T::kPitch;
+  const int b_off = T::kABytes + (wn * T::kTN * 32 + (lane & 31)) * T::kPitch;
+  int phk[T::kKK];
+#pragma unroll
+  for (int kk = 0; kk < T::kKK; ++kk) phk[kk] = ((2 * kk + (lane >> 5)) ^ T::swz(lane & 31)) * 16;
+
+  float16_t acc[T::kTM][T::kTN];
+#pragma unroll
+  for (int rb = 0; rb < T::kTM; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < T::kTN; ++cb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[rb][cb][i] = 0.f;
+
+  // Pipeline: every ring slot holds a step in flight.  The one barrier per step sits
+  // before the step's last MFMAs: by then every wave has read all of the step's
+  // fragments, so its slot is refilled (step s + kRing) and the next step's first
+  // fragments are read while those MFMAs run.
+  bf16x8 af[2][T::kTM], bfg[2][T::kTN];
+  auto read_frags = [&](int buf, int s, int kk) {
+    const char* sb = lds + (s % T::kRing) * T::kStage;
+#pragma unroll
+    for (int rb = 0; rb < T::kTM; ++rb)
+      af[buf][rb] = *reinterpret_cast<const bf16x8*>(sb + a_off + rb * 32 * T::kPitch + phk[kk]);
+#pragma unroll
+    for (int cb = 0; cb < T::kTN; ++cb)
+      bfg[buf][cb] = *reinterpret_cast<const bf16x8*>(sb + b_off + cb * 32 * T::kPitch + phk[kk]);
+  };
+  constexpr int kPer = T::kDmaA + T::kDmaB;
+#pragma unroll
+  for (int j = 0; j < T::kRing; ++j)
+    if (j < n_my) issue(j);
+  wait_steps<kPer, T::kRing - 1>(min(T::kRing - 1, n_my - 1));
+  barrier();  // step 0 landed for every wave
+  read_frags(0, 0, 0);
+  for (int s = 0; s < n_my; ++s) {
+#pragma unroll
+    for (int kk = 0; kk < T::kKK; ++kk) {
+      if (kk + 1 < T::kKK) {
+        read_frags((kk + 1) & 1, s, kk + 1);
+      } else if (s + 1 < n_my) {
+        // step s + 1 landed (steps up to s + kRing - 1 may still be in flight)
+        wait_steps<kPer, T::kRing - 2>(min(T::kRing - 2, n_my - 2 - s));
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of step s done
+        barrier();
+        if (s + T::kRing < n_my) issue(s + T::kRing);
+        read_frags(0, s + 1, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep those reads ahead of this sub-step's MFMAs
+#pragma unroll
+      for (int rb = 0; rb < T::kTM; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < T::kTN; ++cb)
+          acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk & 1][rb], bfg[kk & 1][cb],
+                                                                acc[rb][cb], 0, 0, 0);
+    }
+  }
+
+  // accumulator (rb, cb) register r of lane: row 32 rb + 8 (r / 4) + 4 (lane / 32) + r % 4,
+  // column 32 cb + lane % 32 of the wave's block
+#pragma unroll
+  for (int rb = 0; rb < T::kTM; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < T::kTN; ++cb) {
+      const int n = col0 + (wn * T::kTN + cb) * 32 + (lane & 31);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = row0 + (wm * T::kTM + rb) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m >= a.M) continue;
+        const float v = acc[rb][cb][r];
+        if (kPartial)
+          a.part[((long long)sp * a.M + m) * a.N + n] = v;
+        else if (kF32Out)
+          static_cast<float*>(a.y)[m * a.ldy + n] = v;
+        else
+          static_cast<uint16_t*>(a.y)[m * a.ldy + n] = f32_to_bf16_bits(v);
+      }
+    }
+}
+
+// y = sum over the splits of the fp32 partials, 4 columns per thread.
+template <bool kF32Out>
+__global__ void __launch_bounds__(256) gemm_reduce_kernel(GemmArgs a) {
+  const long long q = (long long)blockIdx.x * 256 + threadIdx.x;  // float4 index
+  const int n4 = a.N / 4;
+  if (q >= (long long)a.M * n4) return;
+  const int m = (int)(q / n4), n = (int)(q % n4) * 4;
+  const long long plane = (long long)a.M * a.N;
+  float4 s = *reinterpret_cast<const float4*>(a.part + (long long)m * a.N + n);
+  for (int k = 1; k < a.splits; ++k) {
+    const float4 v = *reinterpret_cast<const float4*>(a.part + k * plane + (long long)m * a.N + n);
+    s.x += v.x;
+    s.y += v.y;
+    s.z += v.z;
+    s.w += v.w;
+  }
+  if (kF32Out) {
+    *reinterpret_cast<float4*>(static_cast<float*>(a.y) + m * a.ldy + n) = s;
+  } else {
+    const uint2 p = make_uint2(pack_bf16x2(s.x, s.y), pack_bf16x2(s.z, s.w));
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.y) + m * a.ldy + n) = p;
+  }
+}
+
+// The launch plan of one call: the tile with the fewest rows that covers M (tile 1, 2, 3
+// = 128, 64, 32 rows), 256 rows above 128 (tile 0); 128 columns.  When the tiles alone
+// leave CUs idle, K is split so that tiles x splits fill the 256 CUs once (the kernels
+// run one workgroup per CU).
+struct GemmPlan {
+  int tile, bm, bn, splits, m_tiles, n_tiles;
+};
+GemmPlan gemm_plan(int M, int N, int K) {
+  GemmPlan p;
+  p.tile = M > 1024 && N % 256 == 0 ? 0 : M > 128 ? 4 : M > 64 ? 1 : M > 32 ? 2 : 3;
+  p.bm = p.tile == 0 || p.tile == 4 ? 256 : p.tile == 1 ? 128 : p.tile == 2 ? 64 : 32;
+  p.bn = p.tile == 0 ? 256 : 128;
+  p.m_tiles = (M + p.bm - 1) / p.bm;
+  p.n_tiles = N / p.bn;
+  const int tiles = p.m_tiles * p.n_tiles;
+  const int nst = K / kGK;
+  int s = tiles >= 160 ? 1 : 256 / tiles;
+  if (s > 16) s = 16;
+  if (s > nst) s = nst;
+  p.splits = s < 1 ? 1 : s;
+  return p;
+}
+
+bool gemm_shape_ok(int M, int N, int K) {
+  return M >= 0 && N > 0 && K > 0 && N % 128 == 0 && K % kGK == 0;
+}
+
+template <class T>
+void launch_gemm(const GemmArgs& a, bool f32, hipStream_t st) {
+  const dim3 grid((unsigned)(a.m_tiles * a.n_tiles * a.splits));
+  const dim3 block(T::kThreads);
+  if (a.splits > 1)
+    hipLaunchKernelGGL((gemm_kernel<T, false, true>), grid, block, 0, st, a);
+  else if (f32)
+    hipLaunchKernelGGL((gemm_kernel<T, true, false>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((gemm_kernel<T, false, false>), grid, block, 0, st, a);
+}
+}  // namespace
+}  // namespace fqa
+
+using namespace fqa;
+
+extern "C" int64_t fqa_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K) {
+  if (!gemm_shape_ok(M, N, K) || M == 0) return 0;
+  const GemmPlan p = gemm_plan(M, N, K);
+  return p.splits > 1 ? (int64_t)p.splits * M * N * 4 : 0;
+}
+
+extern "C" int fqa_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y,
+                        int64_t ldy, int32_t M, int32_t N, int32_t K, int32_t y_f32,
+                        void* workspace, int64_t workspace_bytes, void* stream) {
+  if (M < 0 || N <= 0 || K <= 0) return FQA_EINVAL;
+  if (!gemm_shape_ok(M, N, K)) return FQA_EUNSUPPORTED;
+  if (M == 0) return FQA_OK;
+  if (!x || !w || !y) return FQA_EINVAL;
+  if (ldx < K || ldw < K || ldy < N || ldx % 8 || ldw % 8 || ldy % 4) return FQA_EINVAL;
+  if (((uintptr_t)x & 15) || ((uintptr_t)w & 15) || ((uintptr_t)y & 15)) return FQA_EINVAL;
+  // DMA lane offsets are 32-bit: every row start of x and W must lie within 4 GiB
+  if ((int64_t)(M - 1) * ldx * 2 >= (int64_t)1 << 32 || (int64_t)(N - 1) * ldw * 2 >= (int64_t)1 << 32)
+    return FQA_EUNSUPPORTED;
+  const GemmPlan p = gemm_plan(M, N, K);
+  if ((int64_t)p.m_tiles * p.n_tiles * p.splits > 0x7fffffff) return FQA_EINVAL;
+  GemmArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), y, nullptr,
+             ldx, ldw, ldy, M, N, K, p.splits, p.m_tiles, p.n_tiles};
+  if (p.splits > 1) {
+    if (!workspace || workspace_bytes < (int64_t)p.splits * M * N * 4 || ((uintptr_t)workspace & 15))
+      return FQA_EINVAL;
+    a.part = static_cast<float*>(workspace);
+  }
+  hipStream_t st = (hipStream_t)stream;
+  switch (p.tile) {
+    case 0: launch_gemm<TileL>(a, y_f32 != 0, st); break;
+    case 4: launch_gemm<TileL8>(a, y_f32 != 0, st); break;
+    case 1: launch_gemm<TileM>(a, y_f32 != 0, st); break;
+    case 2: launch_gemm<TileS>(a, y_f32 != 0, st); break;
+    default: launch_gemm<TileT>(a, y_f32 != 0, st); break;
+  }
+  if (p.splits > 1) {
+    const long long n4 = (long long)M * (N / 4);
+    const unsigned blocks = (unsigned)((n4 + 255) / 256);
+    if (y_f32)
+      hipLaunchKernelGGL((gemm_reduce_kernel<true>), dim3(blocks), dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((gemm_reduce_kernel<false>), dim3(blocks), dim3(256), 0, st, a);
+  }
+  return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
+}

@@ -14,6 +14,7 @@
  *   fqa_prefill             <- LaunchAttnPrefillCute                          (attn_cute.cu:30-163)
  *   fqa_pool_bytes          <- KvStore pool sizing                            (kv_store.cu:10-46)
  *   fqa_sample              <- LaunchSampleBatch (greedy / temperature + top-p) (kernels.cu:184-327)
+ *   fqa_gemm                <- LaunchGemm (QKV, o_proj, gate-up, down, lm_head) (kernels.cu:9-16)
  *
  * Conventions (all entry points):
  *   - Plain device pointers and sizes; every launch goes on the caller's hipStream_t
@@ -254,6 +255,21 @@ int fqa_prefill(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
 int fqa_sample(const float* logits, int32_t n_rows, int32_t vocab, int64_t row_stride,
                const float* inv_temp, const float* top_p, const float* u, int32_t* out,
                void* stream);
+
+/* The layer projections y = x . W^T (LaunchGemm, kernels.cu:9-16, called at
+ * model_runtime.cu:261, 280, 285, 288, 322): x [M, K] bf16 (row stride ldx), W [N, K] bf16
+ * (row stride ldw; the reference's weight layout), y [M, N] (row stride ldy) in bf16
+ * (y_f32 = 0, rounded to nearest even) or fp32 (y_f32 = 1, as for the reference's
+ * lm_head); fp32 accumulation.  Requires N % 128 == 0 and K % 64 == 0 (FQA_EUNSUPPORTED
+ * otherwise: every Qwen3-8B projection qualifies), ldx and ldw multiples of 8 and ldy of 4
+ * elements, x, W and y 16-byte aligned, and every row start of x and W within 4 GiB of
+ * its base.  Shapes with few 256 x 128 output tiles split K over several workgroups and
+ * need `workspace` (16-byte aligned) of fqa_gemm_workspace_bytes(M, N, K) bytes (0: none;
+ * its contents need no initialisation).  M = 0 is a no-op. */
+int64_t fqa_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K);
+int fqa_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
+             int32_t M, int32_t N, int32_t K, int32_t y_f32, void* workspace,
+             int64_t workspace_bytes, void* stream);
 
 /* Library version string. */
 const char* fqa_version(void);

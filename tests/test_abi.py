@@ -109,3 +109,20 @@ def test_zero_work_is_ok(name):
     else:
         pytest.skip("launches a kernel even for empty input (covered on the GPU)")
     assert rc == _lib.FQA_OK
+
+
+def test_gemm_rejections_without_gpu():
+    """fqa_gemm rejects unsupported shapes and bad arguments before any launch, and sizes
+    its split-K workspace."""
+    from flashqwen_amd import _lib
+
+    lib = _lib.load()
+    assert lib.fqa_gemm(None, 64, None, 64, None, 128, 4, 100, 64, 0, None, 0, None) == _lib.FQA_EUNSUPPORTED
+    assert lib.fqa_gemm(None, 64, None, 64, None, 128, 4, 128, 60, 0, None, 0, None) == _lib.FQA_EUNSUPPORTED
+    assert lib.fqa_gemm(None, 64, None, 64, None, 128, -1, 128, 64, 0, None, 0, None) == _lib.FQA_EINVAL
+    assert lib.fqa_gemm(None, 64, None, 64, None, 128, 0, 128, 64, 0, None, 0, None) == _lib.FQA_OK
+    assert lib.fqa_gemm(None, 64, None, 64, None, 128, 4, 128, 64, 0, None, 0, None) == _lib.FQA_EINVAL
+    # 48 tiles of QKV at M=256: K split 5 ways (240 workgroups), fp32 partials
+    assert lib.fqa_gemm_workspace_bytes(256, 6144, 4096) == 5 * 256 * 6144 * 4
+    assert lib.fqa_gemm_workspace_bytes(8192, 6144, 4096) == 0
+    assert lib.fqa_gemm_workspace_bytes(1, 128, 64) == 0  # one k step cannot be split

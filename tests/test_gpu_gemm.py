@@ -1,0 +1,115 @@
+"""fqa_gemm (LaunchGemm, kernels.cu:9-16: y = x . W^T, bf16 in, fp32 accumulate) on the
+GPU through the C ABI against a float64 reference of the same bf16 inputs.  bf16 outputs
+must be the float64 result rounded once (within one bf16 rounding, 2^-8 relative, plus an
+fp32-accumulation allowance); fp32 outputs within 1e-5 relative.  Shapes cover a single
+tile, ragged M, the split-K path (few tiles) and its reduction, the unsplit path, strided
+rows and every Qwen3-8B projection at decode batch sizes."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+
+def _bf16(rng, shape, scale=1.0):
+    import torch
+
+    return (torch.from_numpy(rng.standard_normal(shape).astype(np.float32)) * scale).to(
+        torch.bfloat16)
+
+
+def _ref(x, w):
+    return x.double().numpy() @ w.double().numpy().T
+
+
+def _run_case(gpu, M, N, K, out_f32=False, ldx_pad=0, ldy_pad=0, seed=0):
+    import torch
+
+    from flashqwen_amd.gemm import gemm, workspace_bytes
+
+    print(f"[gemm] M={M} N={N} K={K} f32={out_f32} ws={workspace_bytes(M, N, K)}", flush=True)
+    rng = np.random.default_rng(seed)
+    x = _bf16(rng, (M, K + ldx_pad))
+    w = _bf16(rng, (N, K), 0.05)
+    xd = x.to(gpu)[:, :K]
+    dt = torch.float32 if out_f32 else torch.bfloat16
+    yfull = torch.full((M, N + ldy_pad), 7.0, dtype=dt, device=gpu)
+    y = yfull[:, :N]
+    gemm(xd, w.to(gpu), out=y, out_f32=out_f32)
+    torch.cuda.synchronize()
+    got = y.float().cpu().numpy().astype(np.float64)
+    ref = _ref(x[:, :K], w)
+    err = np.abs(got - ref)
+    if out_f32:
+        tol = 1e-5 * np.abs(ref) + 1e-6 * np.sqrt(K)
+    else:
+        tol = 2.0 ** -8 * np.abs(ref) + 1e-6 * np.sqrt(K)
+    bad = err > tol
+    assert not bad.any(), (M, N, K, int(bad.sum()), float(err.max()))
+    if ldy_pad:  # padding columns untouched
+        assert torch.all(yfull[:, N:] == 7.0)
+    return float(err.max())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", [
+    (1, 128, 64),       # one tile, one k step
+    (20, 512, 1024),    # 32-row tiles, split K
+    (40, 384, 640),     # 64-row tiles
+    (100, 768, 832),    # 128-row tiles
+    (300, 256, 128),    # ragged M over 2 row tiles, split K
+    (520, 384, 192),    # 256 x 128 tiles (N not a multiple of 256)
+    (256, 6144, 512),   # QKV width, split K
+    (1024, 5120, 256),  # 160 tiles: no split
+    (2048, 4096, 1024),  # 256 tiles
+])
+def test_gemm_shapes(gpu, M, N, K):
+    _run_case(gpu, M, N, K)
+
+
+@pytest.mark.gpu
+def test_gemm_fp32_out_and_strides(gpu):
+    _run_case(gpu, 1024, 5120, 256, out_f32=True, seed=1)      # unsplit, fp32
+    _run_case(gpu, 100, 1280, 448, out_f32=True, seed=2)       # split, fp32
+    _run_case(gpu, 77, 384, 192, ldx_pad=24, ldy_pad=12, seed=3)  # row strides
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,N,K", [
+    ("qkv", 6144, 4096), ("o_proj", 4096, 4096), ("gate_up", 24576, 4096),
+    ("down", 4096, 12288)])
+def test_gemm_qwen3_projections_decode(gpu, name, N, K):
+    """The step's projections at a 128-row decode batch (checked on 256 sampled columns)."""
+    import torch
+
+    from flashqwen_amd.gemm import gemm
+
+    print(f"[gemm] {name}", flush=True)
+    rng = np.random.default_rng(7)
+    M = 128
+    x = _bf16(rng, (M, K))
+    w = _bf16(rng, (N, K), 0.02)
+    y = gemm(x.to(gpu), w.to(gpu))
+    torch.cuda.synchronize()
+    cols = np.sort(rng.choice(N, 256, replace=False))
+    ref = _ref(x, w[cols])
+    got = y.float().cpu().numpy()[:, cols]
+    assert np.all(np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-6 * np.sqrt(K))
+
+
+@pytest.mark.gpu
+def test_gemm_lm_head_fp32(gpu):
+    """lm_head: 4096 -> 151936 fp32 logits for 64 sampling rows (checked on 512 columns)."""
+    import torch
+
+    from flashqwen_amd.gemm import gemm
+
+    rng = np.random.default_rng(8)
+    M, N, K = 64, 151936, 4096
+    x = _bf16(rng, (M, K))
+    w = _bf16(rng, (N, K), 0.02)
+    y = gemm(x.to(gpu), w.to(gpu), out_f32=True)
+    torch.cuda.synchronize()
+    cols = np.sort(rng.choice(N, 512, replace=False))
+    ref = _ref(x, w[cols])
+    got = y.cpu().numpy()[:, cols].astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 1e-5 * np.abs(ref) + 1e-4)
