@@ -385,6 +385,49 @@ def bench_gemm(args):
             print(name, M, out[f"{name}_M{M}"], flush=True)
             del x, y
         del w
+    # the QKV projection with the norm/RoPE/append fused (fqa_qkv_proj_append) against
+    # fqa_gemm + fqa_qknorm_rope_append, one decode row per sequence on its own page
+    import ctypes as C
+
+    from flashqwen_amd import _lib
+    from flashqwen_amd.gemm import workspace_bytes
+    from flashqwen_amd.step import alloc_pool, make_dims, rope_tables
+
+    lib = _lib.load()
+    dims = make_dims()
+    N, K = GEMM_SHAPES["qkv"]
+    w = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    qn = torch.ones(128, device="cuda")
+    cos, sin = (torch.from_numpy(t).cuda() for t in rope_tables(4096))
+    for M in [r for r in rows if r <= 1024]:
+        x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+        qkv = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+        pool = alloc_pool(M + 16)[0]
+        pos = torch.arange(M, dtype=torch.int32, device="cuda") + 1000
+        slots = torch.arange(M, dtype=torch.int32, device="cuda") * 16 + 7
+        meta = torch.zeros(16, dtype=torch.int32, device="cuda")
+        meta[_lib.META_ROWS] = M
+        nb = workspace_bytes(M, N, K)
+        ws = torch.empty(max(nb, 16), dtype=torch.uint8, device="cuda")
+
+        def unfused():
+            gemm(x, w, out=qkv, workspace=ws)
+            lib.fqa_qknorm_rope_append(C.byref(dims), qkv.data_ptr(), qn.data_ptr(), qn.data_ptr(),
+                                       cos.data_ptr(), sin.data_ptr(), 4096, pos.data_ptr(),
+                                       slots.data_ptr(), meta.data_ptr(), M, pool.data_ptr(),
+                                       M + 16, 0, torch.cuda.current_stream().cuda_stream)
+
+        def fused():
+            lib.fqa_qkv_proj_append(C.byref(dims), x.data_ptr(), K, w.data_ptr(), K, M, K,
+                                    qkv.data_ptr(), qn.data_ptr(), qn.data_ptr(), cos.data_ptr(),
+                                    sin.data_ptr(), 4096, pos.data_ptr(), slots.data_ptr(),
+                                    meta.data_ptr(), pool.data_ptr(), M + 16, 0,
+                                    ws.data_ptr() if nb else None, nb,
+                                    torch.cuda.current_stream().cuda_stream)
+
+        uf, fu = timed(unfused), timed(fused)
+        out[f"qkv_append_M{M}"] = {"fused_us": round(fu, 2), "unfused_us": round(uf, 2)}
+        print("qkv+append", M, out[f"qkv_append_M{M}"], flush=True)
     print(json.dumps({"gemm": out, "peak_TFLOPs": 2516.6, "peak_GBps": HBM_PEAK_GBS}))
 
 

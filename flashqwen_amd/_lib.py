@@ -109,6 +109,11 @@ SIGNATURES = {
     "fqa_sample": (C.c_int, [P, I32, I32, I64, P, P, P, P, P]),
     "fqa_gemm_workspace_bytes": (I64, [I32, I32, I32]),
     "fqa_gemm": (C.c_int, [P, I64, P, I64, P, I64, I32, I32, I32, I32, P, I64, P]),
+    "fqa_qkv_proj_append": (
+        C.c_int,
+        [C.POINTER(FqaDims), P, I64, P, I64, I32, I32, P, P, P, P, P, I32, P, P, P, P, I64, I32,
+         P, I64, P],
+    ),
     "fqa_version": (C.c_char_p, []),
 }
 

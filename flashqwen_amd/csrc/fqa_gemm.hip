@@ -25,6 +25,7 @@
 //    workgroups on one XCD walk 8 m tiles per n tile and share W and x tiles in its L2.
 
 #include "fqa_common.h"
+#include "fqa_gemm_internal.h"
 
 namespace fqa {
 namespace {
@@ -322,9 +323,12 @@ extern "C" int64_t fqa_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K) {
   return p.splits > 1 ? (int64_t)p.splits * M * N * 4 : 0;
 }
 
-extern "C" int fqa_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y,
-                        int64_t ldy, int32_t M, int32_t N, int32_t K, int32_t y_f32,
-                        void* workspace, int64_t workspace_bytes, void* stream) {
+namespace fqa {
+
+// Validates a call and fills the kernel arguments and plan; FQA_OK or an FQA_E code.
+static int gemm_prepare(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y,
+                        int64_t ldy, int32_t M, int32_t N, int32_t K, void* workspace,
+                        int64_t workspace_bytes, GemmArgs& a, GemmPlan& p) {
   if (M < 0 || N <= 0 || K <= 0) return FQA_EINVAL;
   if (!gemm_shape_ok(M, N, K)) return FQA_EUNSUPPORTED;
   if (M == 0) return FQA_OK;
@@ -334,23 +338,50 @@ extern "C" int fqa_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, 
   // DMA lane offsets are 32-bit: every row start of x and W must lie within 4 GiB
   if ((int64_t)(M - 1) * ldx * 2 >= (int64_t)1 << 32 || (int64_t)(N - 1) * ldw * 2 >= (int64_t)1 << 32)
     return FQA_EUNSUPPORTED;
-  const GemmPlan p = gemm_plan(M, N, K);
+  p = gemm_plan(M, N, K);
   if ((int64_t)p.m_tiles * p.n_tiles * p.splits > 0x7fffffff) return FQA_EINVAL;
-  GemmArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), y, nullptr,
-             ldx, ldw, ldy, M, N, K, p.splits, p.m_tiles, p.n_tiles};
+  a = GemmArgs{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), y, nullptr,
+               ldx, ldw, ldy, M, N, K, p.splits, p.m_tiles, p.n_tiles};
   if (p.splits > 1) {
     if (!workspace || workspace_bytes < (int64_t)p.splits * M * N * 4 || ((uintptr_t)workspace & 15))
       return FQA_EINVAL;
     a.part = static_cast<float*>(workspace);
   }
-  hipStream_t st = (hipStream_t)stream;
+  return FQA_OK;
+}
+
+static void gemm_launch_main(const GemmArgs& a, const GemmPlan& p, bool f32, hipStream_t st) {
   switch (p.tile) {
-    case 0: launch_gemm<TileL>(a, y_f32 != 0, st); break;
-    case 4: launch_gemm<TileL8>(a, y_f32 != 0, st); break;
-    case 1: launch_gemm<TileM>(a, y_f32 != 0, st); break;
-    case 2: launch_gemm<TileS>(a, y_f32 != 0, st); break;
-    default: launch_gemm<TileT>(a, y_f32 != 0, st); break;
+    case 0: launch_gemm<TileL>(a, f32, st); break;
+    case 4: launch_gemm<TileL8>(a, f32, st); break;
+    case 1: launch_gemm<TileM>(a, f32, st); break;
+    case 2: launch_gemm<TileS>(a, f32, st); break;
+    default: launch_gemm<TileT>(a, f32, st); break;
   }
+}
+
+int gemm_launch_partials(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y,
+                         int64_t ldy, int32_t M, int32_t N, int32_t K, void* workspace,
+                         int64_t workspace_bytes, hipStream_t st) {
+  GemmArgs a;
+  GemmPlan p;
+  const int rc = gemm_prepare(x, ldx, w, ldw, y, ldy, M, N, K, workspace, workspace_bytes, a, p);
+  if (rc != FQA_OK || M == 0) return rc;
+  gemm_launch_main(a, p, false, st);
+  return p.splits;
+}
+
+}  // namespace fqa
+
+extern "C" int fqa_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y,
+                        int64_t ldy, int32_t M, int32_t N, int32_t K, int32_t y_f32,
+                        void* workspace, int64_t workspace_bytes, void* stream) {
+  GemmArgs a;
+  GemmPlan p;
+  const int rc = gemm_prepare(x, ldx, w, ldw, y, ldy, M, N, K, workspace, workspace_bytes, a, p);
+  if (rc != FQA_OK || M == 0) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  gemm_launch_main(a, p, y_f32 != 0, st);
   if (p.splits > 1) {
     const long long n4 = (long long)M * (N / 4);
     const unsigned blocks = (unsigned)((n4 + 255) / 256);

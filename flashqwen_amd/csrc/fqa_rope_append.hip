@@ -23,6 +23,7 @@
 // Memory-bound: per row 12 KiB read, 8 KiB (q) + 4 KiB (k, v) written.
 //
 #include "fqa_common.h"
+#include "fqa_gemm_internal.h"
 
 namespace fqa {
 namespace {
@@ -45,7 +46,50 @@ struct AppendArgs {
   float eps;
   int write_k;
   int blocks_per_xcd;
+  // fused with the QKV projection: the row's qkv values are the sum of `splits` fp32
+  // partials part[s][row][col] (row stride pstride, plane stride plane), rounded to bf16
+  const float* part;
+  int splits;
+  int pstride;
+  long long plane;
+  int part_rows;
 };
+
+// The row's 4 (load4) or 2 (load2) qkv values from column col on, as packed bf16: from the
+// qkv buffer, or (kPart) summed over the split partials in split order and rounded, the
+// values the projection's own reduction writes.
+template <bool kPart>
+__device__ __forceinline__ uint2 load4(const AppendArgs& a, long long row, int col) {
+  if constexpr (kPart) {
+    const float* p = a.part + row * a.pstride + col;
+    float4 s = *reinterpret_cast<const float4*>(p);
+    for (int k = 1; k < a.splits; ++k) {
+      const float4 v = *reinterpret_cast<const float4*>(p + k * a.plane);
+      s.x += v.x;
+      s.y += v.y;
+      s.z += v.z;
+      s.w += v.w;
+    }
+    return make_uint2(pack_bf16x2(s.x, s.y), pack_bf16x2(s.z, s.w));
+  } else {
+    return *reinterpret_cast<const uint2*>(a.qkv + row * a.stride + col);
+  }
+}
+template <bool kPart>
+__device__ __forceinline__ uint32_t load2(const AppendArgs& a, long long row, int col) {
+  if constexpr (kPart) {
+    const float* p = a.part + row * a.pstride + col;
+    float2 s = *reinterpret_cast<const float2*>(p);
+    for (int k = 1; k < a.splits; ++k) {
+      const float2 v = *reinterpret_cast<const float2*>(p + k * a.plane);
+      s.x += v.x;
+      s.y += v.y;
+    }
+    return pack_bf16x2(s.x, s.y);
+  } else {
+    return *reinterpret_cast<const uint32_t*>(a.qkv + row * a.stride + col);
+  }
+}
 
 __device__ __forceinline__ void unpack4(uint2 v, float* f) {
   f[0] = __uint_as_float(v.x << 16);
@@ -54,17 +98,19 @@ __device__ __forceinline__ void unpack4(uint2 v, float* f) {
   f[3] = __uint_as_float(v.y & 0xffff0000u);
 }
 
-template <int HPG>
+template <int HPG, bool kPart>
 __global__ void __launch_bounds__(256) qknorm_rope_append_kernel(AppendArgs a) {
   constexpr int W = 10 / HPG;                  // waves per row
   constexpr int NKV = (kHkv + W - 1) / W;      // v heads per wave
-  const int T = a.meta[FQA_META_ROWS];
+  // rows past the projection's M have no partials
+  const int T = kPart ? min(a.meta[FQA_META_ROWS], a.part_rows) : a.meta[FQA_META_ROWS];
   const int b = blockIdx.x;
   const int wid = ((b & 7) * a.blocks_per_xcd + (b >> 3)) * kWavesPerBlock + (threadIdx.x >> 6);
   const int row = wid / W, sw = wid % W;
   if (row >= T) return;
   const int pos = a.positions[row];
-  if (pos < 0 || pos >= a.rope_max_pos) return;  // no table row: leave the row untouched
+  const bool pos_ok = pos >= 0 && pos < a.rope_max_pos;
+  if (!kPart && !pos_ok) return;  // no table row: leave the row untouched
   const int slot = a.slots[row];
   const long long page = slot / kPage;
   const bool page_ok = slot >= 0 && page < a.pool_pages;
@@ -76,9 +122,19 @@ __global__ void __launch_bounds__(256) qknorm_rope_append_kernel(AppendArgs a) {
   uint2 lo[HPG], hi[HPG];
 #pragma unroll
   for (int i = 0; i < HPG; ++i) {
-    const uint16_t* hs = src + (g + 4 * (sw * HPG + i)) * kD;
-    lo[i] = *reinterpret_cast<const uint2*>(hs + 4 * j);
-    hi[i] = *reinterpret_cast<const uint2*>(hs + 64 + 4 * j);
+    const int col = (g + 4 * (sw * HPG + i)) * kD;
+    lo[i] = load4<kPart>(a, row, col + 4 * j);
+    hi[i] = load4<kPart>(a, row, col + 64 + 4 * j);
+  }
+  if (kPart && !pos_ok) {  // no table row: the projection's values, as unfused
+#pragma unroll
+    for (int i = 0; i < HPG; ++i) {
+      const int head = g + 4 * (sw * HPG + i);
+      if (head >= kHq && !a.write_k) continue;
+      *reinterpret_cast<uint2*>(src + head * kD + 4 * j) = lo[i];
+      *reinterpret_cast<uint2*>(src + head * kD + 64 + 4 * j) = hi[i];
+    }
+    return;
   }
   const float4 c4 = *reinterpret_cast<const float4*>(a.cos_tab + (long long)pos * 64 + 4 * j);
   const float4 s4 = *reinterpret_cast<const float4*>(a.sin_tab + (long long)pos * 64 + 4 * j);
@@ -141,7 +197,6 @@ __global__ void __launch_bounds__(256) qknorm_rope_append_kernel(AppendArgs a) {
   if (full) {
     if (tok != 0) return;  // the page's first row writes it
     // kv heads sw*NKV ..: lane -> dims 2*lane, 2*lane+1 of all 16 tokens
-    const uint16_t* vsrc = a.qkv + (long long)row * a.stride + (kHq + kHkv) * kD + 2 * lane;
 #pragma unroll
     for (int hv = 0; hv < NKV; ++hv) {
       const int kvh = sw * NKV + hv;
@@ -149,7 +204,7 @@ __global__ void __launch_bounds__(256) qknorm_rope_append_kernel(AppendArgs a) {
       uint32_t x[kPage];
 #pragma unroll
       for (int t = 0; t < kPage; ++t)
-        x[t] = *reinterpret_cast<const uint32_t*>(vsrc + (long long)t * a.stride + kvh * kD);
+        x[t] = load2<kPart>(a, (long long)row + t, (kHq + kHkv + kvh) * kD + 2 * lane);
       uint32_t y0[8], y1[8];  // dim 2*lane / 2*lane+1, tokens 2k, 2k+1
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
@@ -169,10 +224,9 @@ __global__ void __launch_bounds__(256) qknorm_rope_append_kernel(AppendArgs a) {
   constexpr int DPL = kD / LPK;      // dims per lane (2, 4 or 16)
   const int kvh = sw * NKV + lane / LPK, d0 = (lane % LPK) * DPL;
   if (kvh >= kHkv) return;
-  const uint16_t* vs = src + (kHq + kHkv + kvh) * kD + d0;
   uint32_t wv[DPL / 2];
 #pragma unroll
-  for (int e = 0; e < DPL / 2; ++e) wv[e] = reinterpret_cast<const uint32_t*>(vs)[e];
+  for (int e = 0; e < DPL / 2; ++e) wv[e] = load2<kPart>(a, row, (kHq + kHkv + kvh) * kD + d0 + 2 * e);
   uint16_t* vt = a.pool + run_offset(page, kvh) + kVOff + d0 * kPage + tok;
 #pragma unroll
   for (int e = 0; e < DPL / 2; ++e) {
@@ -186,18 +240,25 @@ bool dims_ok(const fqa_dims* d) {
          d->page_size == kPage && d->qkv_stride >= kQkvStride && d->qkv_stride % 4 == 0;
 }
 
-}  // namespace
-}  // namespace fqa
+template <bool kPart>
+void launch_append(const AppendArgs& a, int hpg, dim3 grid, hipStream_t st) {
+  const dim3 block(256);
+  if (hpg == 1)
+    hipLaunchKernelGGL((qknorm_rope_append_kernel<1, kPart>), grid, block, 0, st, a);
+  else if (hpg == 2)
+    hipLaunchKernelGGL((qknorm_rope_append_kernel<2, kPart>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((qknorm_rope_append_kernel<10, kPart>), grid, block, 0, st, a);
+}
 
-using namespace fqa;
-
-extern "C" int fqa_qknorm_rope_append(const fqa_dims* dims, uint16_t* qkv, const float* q_norm_w,
-                                      const float* k_norm_w, const float* cos_tab,
-                                      const float* sin_tab, int32_t rope_max_pos,
-                                      const int32_t* positions,
-                                      const int32_t* slot_mapping, const int32_t* meta,
-                                      int32_t rows_bound, uint16_t* pool, int64_t pool_pages,
-                                      int32_t write_k_inplace, void* stream) {
+// Validates the append arguments and launches the append kernel (kPart: reading the
+// projection's split partials `part`, splits > 1).
+int append_launch(const fqa_dims* dims, uint16_t* qkv, const float* q_norm_w,
+                  const float* k_norm_w, const float* cos_tab, const float* sin_tab,
+                  int32_t rope_max_pos, const int32_t* positions, const int32_t* slot_mapping,
+                  const int32_t* meta, int32_t rows_bound, uint16_t* pool, int64_t pool_pages,
+                  int32_t write_k_inplace, const float* part, int splits, int part_rows,
+                  hipStream_t st) {
   if (!dims) return FQA_EINVAL;
   if (!dims_ok(dims)) return FQA_EUNSUPPORTED;
   if (rows_bound < 0 || pool_pages < 1 || rope_max_pos < 1 || !meta) return FQA_EINVAL;
@@ -213,13 +274,55 @@ extern "C" int fqa_qknorm_rope_append(const fqa_dims* dims, uint16_t* qkv, const
   const int blocks_per_xcd = (blocks + 7) / 8;
   AppendArgs a{qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, rope_max_pos, positions, slot_mapping,
                meta, pool, pool_pages, dims->qkv_stride, dims->eps, write_k_inplace,
-               blocks_per_xcd};
-  const dim3 grid(8 * blocks_per_xcd), block(256);
-  if (hpg == 1)
-    hipLaunchKernelGGL(qknorm_rope_append_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
-  else if (hpg == 2)
-    hipLaunchKernelGGL(qknorm_rope_append_kernel<2>, grid, block, 0, (hipStream_t)stream, a);
+               blocks_per_xcd, part, splits, kQkvStride, (long long)part_rows * kQkvStride,
+               part_rows};
+  const dim3 grid(8 * blocks_per_xcd);
+  if (part)
+    launch_append<true>(a, hpg, grid, st);
   else
-    hipLaunchKernelGGL(qknorm_rope_append_kernel<10>, grid, block, 0, (hipStream_t)stream, a);
+    launch_append<false>(a, hpg, grid, st);
   return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
+}
+
+}  // namespace
+}  // namespace fqa
+
+using namespace fqa;
+
+extern "C" int fqa_qknorm_rope_append(const fqa_dims* dims, uint16_t* qkv, const float* q_norm_w,
+                                      const float* k_norm_w, const float* cos_tab,
+                                      const float* sin_tab, int32_t rope_max_pos,
+                                      const int32_t* positions,
+                                      const int32_t* slot_mapping, const int32_t* meta,
+                                      int32_t rows_bound, uint16_t* pool, int64_t pool_pages,
+                                      int32_t write_k_inplace, void* stream) {
+  return append_launch(dims, qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, rope_max_pos, positions,
+                       slot_mapping, meta, rows_bound, pool, pool_pages, write_k_inplace, nullptr,
+                       1, 0, (hipStream_t)stream);
+}
+
+extern "C" int fqa_qkv_proj_append(const fqa_dims* dims, const uint16_t* x, int64_t ldx,
+                                   const uint16_t* w_qkv, int64_t ldw, int32_t rows,
+                                   int32_t hidden, uint16_t* qkv, const float* q_norm_w,
+                                   const float* k_norm_w, const float* cos_tab,
+                                   const float* sin_tab, int32_t rope_max_pos,
+                                   const int32_t* positions, const int32_t* slot_mapping,
+                                   const int32_t* meta, uint16_t* pool, int64_t pool_pages,
+                                   int32_t write_k_inplace, void* workspace,
+                                   int64_t workspace_bytes, void* stream) {
+  if (!dims) return FQA_EINVAL;
+  if (!dims_ok(dims)) return FQA_EUNSUPPORTED;
+  if (rows < 0 || hidden <= 0 || pool_pages < 1 || rope_max_pos < 1 || !meta) return FQA_EINVAL;
+  if (rows == 0) return FQA_OK;
+  if (!qkv || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !positions || !slot_mapping ||
+      !pool)
+    return FQA_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  const int splits = gemm_launch_partials(x, ldx, w_qkv, ldw, qkv, dims->qkv_stride, rows,
+                                          kQkvStride, hidden, workspace, workspace_bytes, st);
+  if (splits < 0) return splits;
+  return append_launch(dims, qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, rope_max_pos, positions,
+                       slot_mapping, meta, rows, pool, pool_pages, write_k_inplace,
+                       splits > 1 ? static_cast<const float*>(workspace) : nullptr, splits, rows,
+                       st);
 }

@@ -42,11 +42,6 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
   return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
-}
 // Inclusive prefix sum over the wave's lanes.
 __device__ __forceinline__ float wave_scan(float v) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -56,26 +51,6 @@ __device__ __forceinline__ float wave_scan(float v) {
     if (lane >= o) v += x;
   }
   return v;
-}
-
-// Sum / max over the workgroup; every thread gets the result.  `sh` holds kSWaves floats.
-__device__ float block_sum(float v, float* sh) {
-  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
-  v = wave_sum(v);
-  __syncthreads();  // sh is free again
-  if (lane == 0) sh[w] = v;
-  __syncthreads();
-  float r = lane < kSWaves ? sh[lane] : 0.f;
-  return __shfl(wave_sum(r), 0, kWave);
-}
-__device__ float block_max(float v, float* sh) {
-  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
-  v = wave_max(v);
-  __syncthreads();
-  if (lane == 0) sh[w] = v;
-  __syncthreads();
-  float r = lane < kSWaves ? sh[lane] : -INFINITY;
-  return __shfl(wave_max(r), 0, kWave);
 }
 
 // Descending scan of a mass histogram: the bin at which the mass of bins above it plus

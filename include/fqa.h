@@ -15,6 +15,7 @@
  *   fqa_pool_bytes          <- KvStore pool sizing                            (kv_store.cu:10-46)
  *   fqa_sample              <- LaunchSampleBatch (greedy / temperature + top-p) (kernels.cu:184-327)
  *   fqa_gemm                <- LaunchGemm (QKV, o_proj, gate-up, down, lm_head) (kernels.cu:9-16)
+ *   fqa_qkv_proj_append     <- LaunchGemm(QKV) + LaunchHeadNormRope + StoreKV (model_runtime.cu:261-268)
  *
  * Conventions (all entry points):
  *   - Plain device pointers and sizes; every launch goes on the caller's hipStream_t
@@ -270,6 +271,26 @@ int64_t fqa_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K);
 int fqa_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
              int32_t M, int32_t N, int32_t K, int32_t y_f32, void* workspace,
              int64_t workspace_bytes, void* stream);
+
+/* The QKV projection fused with fqa_qknorm_rope_append (model_runtime.cu:261-268:
+ * LaunchGemm into buf_.qkv, LaunchHeadNormRope, StoreKV): qkv = x . w_qkv^T for `rows`
+ * rows (x [rows, hidden] bf16, row stride ldx; w_qkv [6144, hidden], row stride ldw), then
+ * per row the norm + RoPE + append of fqa_qknorm_rope_append with the same arguments and
+ * results (rows_bound = rows; meta[FQA_META_ROWS] must not exceed rows).  When the
+ * projection splits K (decode-sized row counts), the append kernel reads the fp32 split
+ * partials directly, summed in the order fqa_gemm's reduction uses, so the bf16 qkv of the
+ * unfused path is never written and read back; the results are bit-identical to fqa_gemm
+ * followed by fqa_qknorm_rope_append.  In that case only q (and k with write_k_inplace) of
+ * qkv is written; v goes to the pool only.  workspace: fqa_gemm_workspace_bytes(rows, 6144,
+ * hidden) bytes. */
+int fqa_qkv_proj_append(const fqa_dims* dims, const uint16_t* x, int64_t ldx,
+                        const uint16_t* w_qkv, int64_t ldw, int32_t rows, int32_t hidden,
+                        uint16_t* qkv, const float* q_norm_w, const float* k_norm_w,
+                        const float* cos_tab, const float* sin_tab, int32_t rope_max_pos,
+                        const int32_t* positions, const int32_t* slot_mapping,
+                        const int32_t* meta, uint16_t* pool, int64_t pool_pages,
+                        int32_t write_k_inplace, void* workspace, int64_t workspace_bytes,
+                        void* stream);
 
 /* Library version string. */
 const char* fqa_version(void);
