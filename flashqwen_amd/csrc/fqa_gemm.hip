@@ -58,7 +58,7 @@ struct Tile {
   static_assert((kRing - 1) * (kDmaA + kDmaB) < 64, "vmcnt");
   __device__ static int swz(int r) { return kChunks == 8 ? ((r >> 1) & 7) : ((r >> 2) & 3); }
 };
-using TileL = Tile<2, 4, 4, 2, 4, 32>;  // 256 x 256 on 8 waves: prefill-sized M
+using TileL = Tile<2, 4, 4, 2, 2, 64>;  // 256 x 256 on 8 waves: prefill-sized M
 using TileL8 = Tile<4, 2, 2, 2, 3>;     // 256 x 128 on 8 waves: 129..1024 rows
 using TileM = Tile<2, 2, 2, 2, 5>;      // 128 x 128
 using TileS = Tile<1, 4, 2, 1, 6>;      // 64 x 128
