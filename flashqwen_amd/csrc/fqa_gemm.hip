@@ -274,16 +274,21 @@ __global__ void __launch_bounds__(256) gemm_reduce_kernel(GemmArgs a) {
   }
 }
 
-// The launch plan of one call: the tile with the fewest rows that covers M (tile 1, 2, 3
-// = 128, 64, 32 rows), 256 rows above 128 (tile 0); 128 columns.  When the tiles alone
-// leave CUs idle, K is split so that tiles x splits fill the 256 CUs once (the kernels
-// run one workgroup per CU).
+// The launch plan of one call: up to 128 rows the tile with the fewest rows that covers
+// M (tile 1, 2, 3 = 128, 64, 32 rows by 128 columns); up to 1024 rows 256 x 128 (tile 4);
+// above, 256 x 256 (tile 0) when N allows.  When the tiles alone leave CUs idle, K is
+// split so that tiles x splits fill the 256 CUs once (the kernels run one workgroup per
+// CU).
 struct GemmPlan {
   int tile, bm, bn, splits, m_tiles, n_tiles;
 };
 GemmPlan gemm_plan(int M, int N, int K) {
   GemmPlan p;
   p.tile = M > 1024 && N % 256 == 0 ? 0 : M > 128 ? 4 : M > 64 ? 1 : M > 32 ? 2 : 3;
+  // 129..256 rows over few columns (o_proj, down: 32 tiles of 256 x 128, split 8 ways):
+  // two 128-row tiles halve the split count and the partial traffic (measured 23.0 ->
+  // 21.2 us on o_proj at 256 rows; with 48 or more tiles the 256-row tile wins)
+  if (M > 128 && M <= 256 && N / 128 < 40) p.tile = 1;
   p.bm = p.tile == 0 || p.tile == 4 ? 256 : p.tile == 1 ? 128 : p.tile == 2 ? 64 : 32;
   p.bn = p.tile == 0 ? 256 : 128;
   p.m_tiles = (M + p.bm - 1) / p.bm;
