@@ -223,31 +223,36 @@ __global__ void __launch_bounds__(T::kThreads, 1) gemm_kernel(GemmArgs a) {
       for (int rb = 0; rb < T::kTM; ++rb)
 #pragma unroll
         for (int cb = 0; cb < T::kTN; ++cb)
-          acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk & 1][rb], bfg[kk & 1][cb],
+          acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfg[kk & 1][cb], af[kk & 1][rb],
                                                                 acc[rb][cb], 0, 0, 0);
     }
   }
 
-  // accumulator (rb, cb) register r of lane: row 32 rb + 8 (r / 4) + 4 (lane / 32) + r % 4,
-  // column 32 cb + lane % 32 of the wave's block
+  // The MFMAs compute the transposed block (W fragments as the 32-row operand), so
+  // accumulator (rb, cb) registers 4q..4q+3 of lane hold row 32 rb + lane % 32 and the 4
+  // consecutive columns 32 cb + 8 q + 4 (lane / 32) + 0..3 of the wave's block: one
+  // 16-byte (fp32) or 8-byte (bf16) store each, a quarter of the store instructions of
+  // a row-per-register layout
 #pragma unroll
-  for (int rb = 0; rb < T::kTM; ++rb)
+  for (int rb = 0; rb < T::kTM; ++rb) {
+    const int m = row0 + (wm * T::kTM + rb) * 32 + (lane & 31);
+    if (m >= a.M) continue;
 #pragma unroll
-    for (int cb = 0; cb < T::kTN; ++cb) {
-      const int n = col0 + (wn * T::kTN + cb) * 32 + (lane & 31);
+    for (int cb = 0; cb < T::kTN; ++cb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = row0 + (wm * T::kTM + rb) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m >= a.M) continue;
-        const float v = acc[rb][cb][r];
+      for (int q = 0; q < 4; ++q) {
+        const int n = col0 + (wn * T::kTN + cb) * 32 + 8 * q + 4 * (lane >> 5);
+        const float4 v = make_float4(acc[rb][cb][4 * q], acc[rb][cb][4 * q + 1],
+                                     acc[rb][cb][4 * q + 2], acc[rb][cb][4 * q + 3]);
         if (kPartial)
-          a.part[((long long)sp * a.M + m) * a.N + n] = v;
+          *reinterpret_cast<float4*>(a.part + ((long long)sp * a.M + m) * a.N + n) = v;
         else if (kF32Out)
-          static_cast<float*>(a.y)[m * a.ldy + n] = v;
+          *reinterpret_cast<float4*>(static_cast<float*>(a.y) + m * a.ldy + n) = v;
         else
-          static_cast<uint16_t*>(a.y)[m * a.ldy + n] = f32_to_bf16_bits(v);
+          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.y) + m * a.ldy + n) =
+              make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
       }
-    }
+  }
 }
 
 // y = sum over the splits of the fp32 partials, 4 columns per thread.
