@@ -126,3 +126,30 @@ def test_gemm_rejections_without_gpu():
     assert lib.fqa_gemm_workspace_bytes(256, 6144, 4096) == 5 * 256 * 6144 * 4
     assert lib.fqa_gemm_workspace_bytes(8192, 6144, 4096) == 0
     assert lib.fqa_gemm_workspace_bytes(1, 128, 64) == 0  # one k step cannot be split
+
+
+def test_sample_and_fused_qkv_rejections_without_gpu():
+    """fqa_sample and fqa_qkv_proj_append refuse bad arguments before any launch; empty
+    calls succeed."""
+    lib = _lib.load()
+    null = None
+    # sample: vocab out of range, stride below vocab, null pointers with rows; 0 rows ok
+    assert lib.fqa_sample(null, 4, 0, 8, null, null, null, null, null) == _lib.FQA_EINVAL
+    assert lib.fqa_sample(null, 4, (1 << 24) + 1, 1 << 25, null, null, null, null,
+                          null) == _lib.FQA_EINVAL
+    assert lib.fqa_sample(null, 4, 16, 8, null, null, null, null, null) == _lib.FQA_EINVAL
+    assert lib.fqa_sample(null, 4, 16, 16, null, null, null, null, null) == _lib.FQA_EINVAL
+    assert lib.fqa_sample(null, 0, 16, 16, null, null, null, null, null) == _lib.FQA_OK
+    # fused QKV: other shapes, null meta, null pointers with rows; 0 rows ok
+    d = make_dims()
+    bad = make_dims()
+    bad.n_kv_heads = 4
+    meta = (C.c_int32 * 16)()
+    args = lambda dims, rows, meta_: (C.byref(dims), null, 64, null, 64, rows, 64, null, null,  # noqa: E731
+                                      null, null, null, 8, null, null, meta_, null, 1, 0, null,
+                                      0, null)
+    assert lib.fqa_qkv_proj_append(*args(bad, 4, meta)) == _lib.FQA_EUNSUPPORTED
+    assert lib.fqa_qkv_proj_append(*args(d, 4, None)) == _lib.FQA_EINVAL
+    assert lib.fqa_qkv_proj_append(*args(d, 4, meta)) == _lib.FQA_EINVAL
+    assert lib.fqa_qkv_proj_append(*args(d, -1, meta)) == _lib.FQA_EINVAL
+    assert lib.fqa_qkv_proj_append(*args(d, 0, meta)) == _lib.FQA_OK
