@@ -54,6 +54,9 @@ def parse():
     ap.add_argument("--sampler", action="store_true",
                     help="only measure fqa_sample (256 rows x 151936 logits: greedy, "
                          "temperature, temperature + top-p 0.9)")
+    ap.add_argument("--no-overlap", action="store_true",
+                    help="mixed steps: keep the decode on the step's stream (by default it "
+                         "runs on a second stream, queued after the prefill)")
     ap.add_argument("--gemm", action="store_true",
                     help="only measure fqa_gemm on the Qwen3-8B projections (decode and "
                          "prefill row counts) beside torch.matmul (hipBLASLt)")
@@ -151,11 +154,13 @@ def main():
         else:
             step.prepare_inputs(d_computed, d_n_new, d_off, d_pages, rows_bound=T)
 
+    side = None if args.no_overlap else torch.cuda.Stream(device=dev)
+
     def one_step():
         pack()
         for l in range(layers):
             step.run_layer(qkv, pool[l], wq_d, wk_d, out, decode=has_decode,
-                           prefill=has_prefill)
+                           prefill=has_prefill, side_stream=side)
 
     # eager once (also validates the pack), then capture the step
     one_step()

@@ -177,9 +177,20 @@ class AttnStep:
             self.pre_cap, _ptr(out), self.stream), "fqa_prefill")
 
     def run_layer(self, qkv, pool_layer, q_norm_w, k_norm_w, out, write_k=False,
-                  decode=True, prefill=True):
-        """The attention block of one layer (model_runtime.cu:263-278)."""
+                  decode=True, prefill=True, side_stream=None):
+        """The attention block of one layer (model_runtime.cu:263-278).  With side_stream
+        (and both kinds of rows), the decode runs on it concurrently with the prefill: the
+        two write disjoint output rows and only read the pool, and the decode is HBM-bound
+        while the prefill is MFMA-bound."""
         self.head_norm_rope_store_kv(qkv, pool_layer, q_norm_w, k_norm_w, write_k)
+        if decode and prefill and side_stream is not None:
+            cur = torch.cuda.current_stream(self.device)
+            side_stream.wait_stream(cur)
+            self.attn_prefill(qkv, pool_layer, out)
+            with torch.cuda.stream(side_stream):  # self.stream follows the current stream
+                self.attn_decode(qkv, pool_layer, out)
+            cur.wait_stream(side_stream)
+            return
         if decode:
             self.attn_decode(qkv, pool_layer, out)
         if prefill:

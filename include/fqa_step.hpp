@@ -105,6 +105,8 @@ class StepContext {
     cos_.Upload(c.data(), c.size(), nullptr);
     sin_.Upload(s.data(), s.size(), nullptr);
     HipCheck(hipDeviceSynchronize(), "rope upload");
+    HipCheck(hipEventCreateWithFlags(&fork_, hipEventDisableTiming), "event");
+    HipCheck(hipEventCreateWithFlags(&join_, hipEventDisableTiming), "event");
   }
 
   // StepContext::PrepareInputs: upload the per-request batch and pack it on the GPU.
@@ -152,18 +154,22 @@ class StepContext {
   }
   // RunLayer for any batch within the bounds: rows and requests bounded by max_rows and
   // slots, both attention kernels launched (each does nothing without its kind of rows).
+  // With `side`, the decode runs on it after the prefill was queued (see RunLayer).
   void RunLayerBounded(uint16_t* qkv, const float* q_norm, const float* k_norm,
-                       uint16_t* pool_layer, uint16_t* out, hipStream_t stream) const {
+                       uint16_t* pool_layer, uint16_t* out, hipStream_t stream,
+                       hipStream_t side = nullptr) const {
     Check(fqa_qknorm_rope_append(&dims_, qkv, q_norm, k_norm, cos_.D(), sin_.D(), max_ctx_,
                                  pos_.D(), slot_.D(), meta_.D(), max_rows_, pool_layer,
                                  pool_pages_, 0, stream),
           "fqa_qknorm_rope_append");
-    Check(fqa_decode(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_, dwaves_.D(),
-                     dseqs_.D(), meta_.D(), dec_cap_, slots_, ws_.D(), out, stream),
-          "fqa_decode");
+    if (side) Fork(stream, side);
     Check(fqa_prefill(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_, cu_.D(),
                       pos_.D(), items_.D(), meta_.D(), 32, pre_cap_, out, stream),
           "fqa_prefill");
+    Check(fqa_decode(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_, dwaves_.D(),
+                     dseqs_.D(), meta_.D(), dec_cap_, slots_, ws_.D(), out, side ? side : stream),
+          "fqa_decode");
+    if (side) Join(stream, side);
   }
 
   // LaunchHeadNormRope + KvStore::StoreKV for one layer (fused).
@@ -190,10 +196,21 @@ class StepContext {
                       pos_.D(), items_.D(), meta_.D(), 32, pre_cap_, out, stream),
           "fqa_prefill");
   }
-  // The attention block of one layer (model_runtime.cu:263-278).
+  // The attention block of one layer (model_runtime.cu:263-278).  With `side` and a
+  // mixed batch, the prefill is queued on `stream` first and the decode on `side` after
+  // it: the two write disjoint output rows and only read the pool, and the decode's
+  // workgroups fill the CUs the prefill's tail leaves idle (config 4: 4% per step).
+  // `stream` waits for `side` before returning.
   void RunLayer(uint16_t* qkv, const float* q_norm, const float* k_norm, uint16_t* pool_layer,
-                uint16_t* out, hipStream_t stream) const {
+                uint16_t* out, hipStream_t stream, hipStream_t side = nullptr) const {
     HeadNormRopeStoreKV(qkv, q_norm, k_norm, pool_layer, stream);
+    if (side && has_decode_ && has_prefill_) {
+      Fork(stream, side);
+      AttnPrefill(qkv, pool_layer, out, stream);
+      AttnDecode(qkv, pool_layer, out, side);
+      Join(stream, side);
+      return;
+    }
     AttnDecode(qkv, pool_layer, out, stream);
     AttnPrefill(qkv, pool_layer, out, stream);
   }
@@ -201,7 +218,25 @@ class StepContext {
   const int32_t* Meta() const { return meta_.D(); }
   int Rows() const { return rows_; }
 
+  StepContext(const StepContext&) = delete;
+  StepContext& operator=(const StepContext&) = delete;
+  ~StepContext() {
+    if (fork_) (void)hipEventDestroy(fork_);
+    if (join_) (void)hipEventDestroy(join_);
+  }
+
  private:
+  // side starts after everything queued on stream so far; stream continues after side.
+  // Events record and wait only (capture-safe).
+  void Fork(hipStream_t stream, hipStream_t side) const {
+    HipCheck(hipEventRecord(fork_, stream), "fork record");
+    HipCheck(hipStreamWaitEvent(side, fork_, 0), "fork wait");
+  }
+  void Join(hipStream_t stream, hipStream_t side) const {
+    HipCheck(hipEventRecord(join_, side), "join record");
+    HipCheck(hipStreamWaitEvent(stream, join_, 0), "join wait");
+  }
+
   fqa_pack_out PackOut() const {
     return fqa_pack_out{cu_.D(), qlen_.D(), pos_.D(), req_.D(), slot_.D(), bt_.D(),
                         drids_.D(), prids_.D(), dseqs_.D(), dwaves_.D(), items_.D(), meta_.D()};
@@ -220,6 +255,7 @@ class StepContext {
       meta_, nreq_;
   DeviceBuffer<unsigned char> ws_;
   DeviceBuffer<float> cos_, sin_;
+  hipEvent_t fork_ = nullptr, join_ = nullptr;
 };
 
 // Buffers of one layer's attention block.
@@ -238,13 +274,14 @@ struct LayerBuffers {
 // Launch.  The captured launches allocate nothing and record no memset.
 class StepGraph {
  public:
+  // With `side`, each layer's decode is a branch parallel to its prefill (RunLayer).
   StepGraph(const StepContext& ctx, const std::vector<LayerBuffers>& layers,
-            hipStream_t stream) {
+            hipStream_t stream, hipStream_t side = nullptr) {
     HipCheck(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "begin capture");
     try {
       ctx.Pack(stream);
       for (const LayerBuffers& l : layers)
-        ctx.RunLayerBounded(l.qkv, l.q_norm, l.k_norm, l.pool, l.out, stream);
+        ctx.RunLayerBounded(l.qkv, l.q_norm, l.k_norm, l.pool, l.out, stream, side);
     } catch (...) {
       hipGraph_t g = nullptr;
       (void)hipStreamEndCapture(stream, &g);

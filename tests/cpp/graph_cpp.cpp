@@ -1,7 +1,9 @@
 // graph_cpp.cpp — one scheduler-driven workload run twice over 3 layers: eagerly
 // (StepContext::PrepareInputs + RunLayer) and as a captured step graph replayed for every
 // batch (StepContext::UploadBatch + StepGraph::Launch, include/fqa_step.hpp).  Every step's
-// attention output and the final pools must be bit-identical.  For tests/test_gpu_graph.py.
+// attention output and the final pools must be bit-identical.  The graph runs each
+// layer's decode on a parallel branch (StepGraph's side stream).  For
+// tests/test_gpu_graph.py.
 //
 // argv: script norm_weights;  script as tests/cpp/serve_cpp.cpp.  Prints
 // "steps S layers L compared N mismatched M" and exits 0 iff M == 0.
@@ -60,8 +62,9 @@ int main(int argc, char** argv) {
   long long compared = 0, mismatched = 0;
   int steps_run = 0;
   try {
-    hipStream_t s;
+    hipStream_t s, side;
     fqa::HipCheck(hipStreamCreate(&s), "stream");
+    fqa::HipCheck(hipStreamCreate(&side), "stream");
     fqa::DeviceBuffer<float> d_w(256);
     d_w.Upload(w.data(), 256, s);
     const size_t pool_elems = (size_t)n_blocks * 8 * 4096;
@@ -82,7 +85,8 @@ int main(int argc, char** argv) {
       for (int l = 0; l < kLayers; ++l)
         lb.push_back({qkv[l].D(), d_w.D(), d_w.D() + 128, pool[l].D(), out[l].D()});
       std::unique_ptr<fqa::StepGraph> graph;
-      if (mode == 1) graph = std::make_unique<fqa::StepGraph>(ctx, lb, s);
+      // the graph puts each layer's decode on a parallel branch (a second stream)
+      if (mode == 1) graph = std::make_unique<fqa::StepGraph>(ctx, lb, s, side);
 
       fqa::BlockAllocator alloc(n_blocks);
       fqa::HostScheduler sched(alloc, fqa::SchedConfig{n_slots, budget, chunk, use_cache != 0});
@@ -162,6 +166,7 @@ int main(int argc, char** argv) {
         if (std::memcmp(eager_pools.data(), hp.data(), hp.size() * 2) != 0) ++mismatched;
       }
     }
+    (void)hipStreamDestroy(side);
     (void)hipStreamDestroy(s);
   } catch (const std::exception& e) {
     std::fprintf(stderr, "graph_cpp: %s\n", e.what());

@@ -41,7 +41,7 @@ def make_pool(pages: int, seed: int, dev, layers: int = 1):
     return pool
 
 
-def gpu_chain(cfg, qkv_host, pool, wq, wk, dev, kw, schedule=False):
+def gpu_chain(cfg, qkv_host, pool, wq, wk, dev, kw, schedule=False, side_stream=None):
     import torch
 
     from flashqwen_amd.step import AttnStep
@@ -59,7 +59,7 @@ def gpu_chain(cfg, qkv_host, pool, wq, wk, dev, kw, schedule=False):
     else:
         step.prepare_inputs(_t(cfg.computed, dev), _t(cfg.n_new, dev), _t(cfg.bt_off, dev),
                             _t(cfg.bt_pages, dev))
-    step.run_layer(qkv, pool[0], _t(wq, dev), _t(wk, dev), out)
+    step.run_layer(qkv, pool[0], _t(wq, dev), _t(wk, dev), out, side_stream=side_stream)
     torch.cuda.synchronize()
     return step, qkv, out
 
@@ -199,3 +199,33 @@ def test_pages_outside_pool_read_as_zeros(gpu):
                           tabs, base.pool_pages, base.max_ctx)
     kw = sc.pack_kwargs(cfg, dec_grid_waves=64, dec_min_pages=2)
     _check_step(cfg, cfg, dict(kw, device=gpu), 131, "bad-pages")
+
+
+@pytest.mark.gpu
+def test_mixed_step_decode_on_side_stream(gpu):
+    """Config 4 with the decode on a second stream, concurrent with the prefill: the output
+    and the pool are bit-identical to the one-stream step (the two write disjoint rows)."""
+    import torch
+
+    from oracle import oracle as orc
+
+    print("[test_mixed_step_decode_on_side_stream] config4", flush=True)
+    cfg = synth.config4()
+    sel_req, sel_n = orc.schedule(cfg.num_tokens, cfg.computed, cfg.token_budget,
+                                  cfg.prefill_chunk)
+    tabs = cfg.tables()
+    sub = synth._assemble("config4-selected", cfg.computed[sel_req], sel_n,
+                          [tabs[i] for i in sel_req], cfg.pool_pages, cfg.max_ctx)
+    kw = sc.pack_kwargs(sub, dec_grid_waves=2048, dec_min_pages=8)
+    rng = np.random.default_rng(105)
+    qkv_host = synth.rand_bf16(rng, (sub.rows, QKV_STRIDE))
+    wq, wk = synth.norm_weights()
+    res = []
+    for side in (None, torch.cuda.Stream(device=gpu)):
+        pool = make_pool(cfg.pool_pages, 105, gpu)
+        _, qkv, out = gpu_chain(cfg, qkv_host, pool, wq, wk, gpu, kw, schedule=True,
+                                side_stream=side)
+        res.append((out.view(torch.int16).cpu().numpy(), pool.view(torch.int16).cpu().numpy()))
+        del pool
+    assert np.array_equal(res[0][0], res[1][0])
+    assert np.array_equal(res[0][1], res[1][1])
