@@ -6,21 +6,19 @@
 // both K-contiguous (the reference's weight layout), y is [M, N].
 //
 // MI355X design:
-//  * One 256-thread workgroup (4 waves) per output tile of 256, 128, 64 or 32 rows by 128
-//    columns (the smallest that covers M; 256 above 128 rows).  A wave owns a block of
-//    32 x 32 v_mfma_f32_32x32x16_bf16 tiles (4 x 2 of them in the 256 x 128 tile: 128
-//    fp32 accumulators per lane, 6 KiB of fragment reads per 8 MFMAs).
-//  * K advances 64 at a time.  Both operand tiles of a k step move global -> LDS by DMA
-//    (global_load_lds_dwordx4, 1 KiB per wave instruction) into a ring of 3 to 8 steps
-//    (as deep as 160 KiB of LDS allows), all but one in flight ahead of the MFMAs: the
-//    small-M tiles are streams of W, and the deeper ring keeps ~64-100 KiB of W in flight
-//    per CU, what HBM latency needs at a CU's share of 8 TB/s.  A DMA lane's 16 bytes land
-//    at LDS byte 16 * lane, so the bank swizzle is applied on the read side of the DMA:
-//    LDS chunk c of row r holds global chunk c ^ (r & 7), and the ds_read_b128 fragment
-//    reads of 8 consecutive rows hit 8 distinct 16-byte bank groups.
+//  * One workgroup per output tile, chosen by row count (gemm_plan): 32, 64 or 128 rows by
+//    128 columns on 4 waves for decode-sized M, 256 x 128 on 8 waves up to 1024 rows,
+//    256 x 256 on 8 waves above.  A wave owns a block of v_mfma_f32_32x32x16_bf16 tiles
+//    (4 x 2 of them in the large tiles: 128 fp32 accumulators per lane).
+//  * Both operand tiles of a k step (64 or 32 wide) move global -> LDS by DMA
+//    (global_load_lds_dwordx4, 1 KiB per wave instruction) into a ring of 2 to 8 steps,
+//    as deep as 160 KiB of LDS allows, every slot in flight.  The step's one barrier sits
+//    before its last MFMAs, so the freed slot is refilled and the next step's first
+//    fragments are read while those MFMAs run.  A DMA lane's 16 bytes land at LDS byte
+//    16 * lane, so the bank swizzle (Tile::swz) is applied on the global side of the DMA.
 //  * Shapes with few tiles (decode steps) split K over `splits` workgroups per tile so
 //    that one round of workgroups fills the 256 CUs; each writes fp32 partials and a
-//    second kernel sums them into y.
+//    second kernel sums them into y (or a fused consumer reads them: fqa_qkv_proj_append).
 //  * Workgroups are dealt to the 8 XCDs round robin; tile_of() renumbers them so that the
 //    workgroups on one XCD walk 8 m tiles per n tile and share W and x tiles in its L2.
 
