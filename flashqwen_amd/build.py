@@ -84,6 +84,17 @@ def build_graph_driver() -> Path:
     return exe
 
 
+def build_decode_loop_driver() -> Path:
+    """tests/cpp/decode_loop_cpp: the serving loop with projections, lm_head and sampling
+    on the GPU (tokens produced on the device)."""
+    root = PKG.parent
+    src = root / "tests" / "cpp" / "decode_loop_cpp.cpp"
+    exe = src.with_suffix("")
+    _run([HIPCC, "-O2", "-std=c++17", "-o", str(exe), str(src), f"-L{PKG}", "-lfqa",
+          "-Wl,-rpath,$ORIGIN/../../flashqwen_amd"])
+    return exe
+
+
 def build_sched_driver() -> Path:
     """tests/cpp/sched_cpp: a host program driving include/fqa_sched.hpp (no HIP)."""
     root = PKG.parent

@@ -180,6 +180,18 @@ class StepContext {
                                  0, stream),
           "fqa_qknorm_rope_append");
   }
+  // LaunchGemm(QKV) + LaunchHeadNormRope + StoreKV for one layer, fused
+  // (fqa_qkv_proj_append): x [rows, hidden] bf16 (row stride ldx), w_qkv [6144, hidden].
+  // `workspace` holds fqa_gemm_workspace_bytes(max_rows, 6144, hidden) bytes.
+  void QkvProjAppend(const uint16_t* x, int64_t ldx, const uint16_t* w_qkv, int hidden,
+                     uint16_t* qkv, const float* q_norm, const float* k_norm,
+                     uint16_t* pool_layer, void* workspace, int64_t workspace_bytes,
+                     hipStream_t stream) const {
+    Check(fqa_qkv_proj_append(&dims_, x, ldx, w_qkv, hidden, rows_, hidden, qkv, q_norm, k_norm,
+                              cos_.D(), sin_.D(), max_ctx_, pos_.D(), slot_.D(), meta_.D(),
+                              pool_layer, pool_pages_, 0, workspace, workspace_bytes, stream),
+          "fqa_qkv_proj_append");
+  }
   // LaunchAttnDecodeCute.
   void AttnDecode(const uint16_t* qkv, const uint16_t* pool_layer, uint16_t* out,
                   hipStream_t stream) const {
