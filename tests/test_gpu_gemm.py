@@ -61,6 +61,8 @@ def _run_case(gpu, M, N, K, out_f32=False, ldx_pad=0, ldy_pad=0, seed=0):
     (256, 6144, 512),   # QKV width, split K
     (1024, 5120, 256),  # 160 tiles: no split
     (2048, 4096, 1024),  # 256 tiles
+    (2000, 256, 64),    # 256 x 256 tiles, a single k step
+    (1100, 128, 64),    # N below 256 at large M: 256 x 128 tiles, one k step
 ])
 def test_gemm_shapes(gpu, M, N, K):
     _run_case(gpu, M, N, K)
