@@ -153,3 +153,27 @@ def test_sample_and_fused_qkv_rejections_without_gpu():
     assert lib.fqa_qkv_proj_append(*args(d, 4, meta)) == _lib.FQA_EINVAL
     assert lib.fqa_qkv_proj_append(*args(d, -1, meta)) == _lib.FQA_EINVAL
     assert lib.fqa_qkv_proj_append(*args(d, 0, meta)) == _lib.FQA_OK
+
+
+def test_header_is_plain_c(tmp_path):
+    """include/fqa.h is the C ABI: it compiles as C99 with -Wall -Wextra -pedantic, and a C
+    program calling it links against libfqa.so."""
+    import shutil
+    import subprocess
+    from pathlib import Path
+
+    if shutil.which("gcc") is None:
+        pytest.skip("no gcc")
+    root = Path(__file__).resolve().parents[1]
+    src = tmp_path / "c_abi.c"
+    src.write_text('#include "fqa.h"\n'
+                   "int main(void) {\n"
+                   "  return fqa_gemm_workspace_bytes(256, 6144, 4096) > 0 && fqa_version() ? 0 : 1;\n"
+                   "}\n")
+    exe = tmp_path / "c_abi"
+    r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror",
+                        f"-I{root / 'include'}", str(src), "-o", str(exe),
+                        f"-L{root / 'flashqwen_amd'}", "-lfqa",
+                        f"-Wl,-rpath,{root / 'flashqwen_amd'}"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    assert subprocess.run([str(exe)]).returncode == 0
