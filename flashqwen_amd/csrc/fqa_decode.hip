@@ -36,6 +36,10 @@ namespace fqa {
 namespace {
 
 constexpr int kDecWavesPerBlock = 4;
+// Page buffers per wave.  2 buffers (135 VGPRs, 3 waves per SIMD possible) measured the
+// same as 4 on configs 2 and 5 at 2048 waves, slower at 3072 waves, and slower in mixed
+// steps, where the decode's waves then share CUs with the prefill's.
+constexpr int kDecBufs = 4;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecArgs {
@@ -121,6 +125,7 @@ __device__ __forceinline__ void process_page(PageFrag& f, const bf16x8 (&qf)[4],
 }
 
 // Stream pages [pb, pe) of (sequence `seq`, kv head kvh) into `st`.
+template <int kBufs>
 __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* btr, int kvh,
                                              int pb, int pe, int L, const bf16x8 (&qf)[4],
                                              int lane, DecState& st, int first_page) {
@@ -138,8 +143,8 @@ __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* bt
     ok = (uint32_t)page < pool32;
     load_page(f, a.pool + run_offset(ok ? page : 0, kvh), lane);
   };
-  // Four page buffers in registers: page p is processed while p+1..p+3 are in flight.
-  // The buffers rotate through a 4-way unrolled loop so every index is static.  (The
+  // kBufs page buffers in registers: page p is processed while p+1..p+kBufs-1 are in
+  // flight.  The buffers rotate through a kBufs-way unrolled loop so every index is static.  (The
   // refills are conditional, so the compiler drains the loads at each one and about one
   // page per wave is in flight in practice; unconditional refills that keep three in
   // flight were measured 2% slower on config 5 and equal on config 2: with 8 waves per
@@ -148,27 +153,22 @@ __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* bt
   // and add nothing to the numerator.  The online softmax merge is order-free, so such
   // keys are only counted here and merged into `st` once, after the loop.
   int n_zero = 0;
-  PageFrag f0, f1, f2, f3;
-  bool k0 = false, k1 = false, k2 = false, k3 = false;
-  load(f0, k0, pb);
-  if (pb + 1 < pe) load(f1, k1, pb + 1);
-  if (pb + 2 < pe) load(f2, k2, pb + 2);
-  for (int p = pb; p < pe; p += 4) {
-    if (p + 3 < pe) load(f3, k3, p + 3);
-    if (k0) process_page(f0, qf, p, L, g, a.scale_log2, st);
-    else n_zero += min(kPage, L - (p) * kPage);
-    if (p + 1 >= pe) break;
-    if (p + 4 < pe) load(f0, k0, p + 4);
-    if (k1) process_page(f1, qf, p + 1, L, g, a.scale_log2, st);
-    else n_zero += min(kPage, L - (p + 1) * kPage);
-    if (p + 2 >= pe) break;
-    if (p + 5 < pe) load(f1, k1, p + 5);
-    if (k2) process_page(f2, qf, p + 2, L, g, a.scale_log2, st);
-    else n_zero += min(kPage, L - (p + 2) * kPage);
-    if (p + 3 >= pe) break;
-    if (p + 6 < pe) load(f2, k2, p + 6);
-    if (k3) process_page(f3, qf, p + 3, L, g, a.scale_log2, st);
-    else n_zero += min(kPage, L - (p + 3) * kPage);
+  PageFrag f[kBufs];
+  bool ok[kBufs];
+#pragma unroll
+  for (int i = 0; i < kBufs; ++i) ok[i] = false;
+#pragma unroll
+  for (int i = 0; i + 1 < kBufs; ++i)
+    if (pb + i < pe) load(f[i], ok[i], pb + i);
+  for (int p = pb; p < pe; p += kBufs) {
+#pragma unroll
+    for (int i = 0; i < kBufs; ++i) {
+      if (i > 0 && p + i >= pe) break;
+      if (p + i + kBufs - 1 < pe)
+        load(f[(i + kBufs - 1) % kBufs], ok[(i + kBufs - 1) % kBufs], p + i + kBufs - 1);
+      if (ok[i]) process_page(f[i], qf, p + i, L, g, a.scale_log2, st);
+      else n_zero += min(kPage, L - (p + i) * kPage);
+    }
   }
   if (n_zero > 0) {  // n_zero keys with score 0 and value 0 (uniform, rare)
     const float m_new = fmaxf(st.m, 0.f);
@@ -186,6 +186,7 @@ __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* bt
 // the first may start mid-stream, the last may end mid-stream, the ones between are
 // whole.  Whole streams are written as bf16 output; a cut stream leaves its partial in
 // slot 2w (the share's first stream) or 2w+1 (its last).
+template <int kBufs>
 __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel(DecArgs a) {
   // Everything a wave's loop indexes with is wave-uniform; readfirstlane says so, so that
   // block-table reads become scalar loads (see stream_pages).
@@ -227,7 +228,7 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
     for (int b = 0; b < 8; ++b) st.acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
     st.m = -1e30f;
     st.l = 0.f;
-    stream_pages(a, a.bt + (long long)r * a.max_blocks, kvh, page, page + cnt, L, qf, lane, st,
+    stream_pages<kBufs>(a, a.bt + (long long)r * a.max_blocks, kvh, page, page + cnt, L, qf, lane, st,
                  sq.w);
     const float l_run = sum_rows4(st.l);
 
@@ -348,7 +349,7 @@ int fqa_decode(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
   float* ws = static_cast<float*>(workspace);
   DecArgs a{qkv, pool, pool_pages, block_tables, max_blocks, dec_waves, dec_seqs, meta, ws,
             ws + slots, ws + 2 * slots, out, dims->qkv_stride, dims->scale * kLog2e};
-  hipLaunchKernelGGL(decode_split_kernel,
+  hipLaunchKernelGGL(decode_split_kernel<kDecBufs>,
                      dim3((dec_wave_cap + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
                      dim3(kDecWavesPerBlock * kWave), 0, (hipStream_t)stream, a);
   const int waves2 = n_reqs_bound * kHkv;
