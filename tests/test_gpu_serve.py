@@ -42,20 +42,19 @@ def _read_steps(path: Path):
     return steps
 
 
-@pytest.mark.gpu
-def test_serving_loop_matches_oracle(gpu, tmp_path):
+def _serve_case(tmp_path, seed, n_seqs, n_blocks, slots, budget, chunk, steps, cancel_id):
     if not EXE.exists():
         pytest.fail(f"{EXE} not built (run __graft_entry__.build())")
-    rng = np.random.default_rng(77)
+    rng = np.random.default_rng(seed)
     base = [int(x) for x in rng.integers(0, 50000, size=70)]
     specs = []
-    for i in range(10):  # shared 70-token prompt heads, so later arrivals adopt cached blocks
+    for i in range(n_seqs):  # shared 70-token prompt heads: later arrivals adopt cached blocks
         tail = [int(x) for x in rng.integers(0, 50000, size=int(rng.integers(1, 60)))]
         prompt = (base + tail) if i % 2 == 0 else tail + base[:20]
-        specs.append(dict(id=i + 1, arrival=int(i // 2) * 2, cancel=9 if i == 7 else -1,
+        specs.append(dict(id=i + 1, arrival=int(i // 2) * 2,
+                          cancel=9 if i + 1 == cancel_id else -1,
                           max_new=int(rng.integers(2, 9)), max_ctx=512, stop=[],
                           prompt=prompt))
-    n_blocks, slots, budget, chunk, steps = 20, 6, 96, 48, 16  # tight pool: 3 preemptions
     script = _script((n_blocks, slots, budget, chunk, True), steps, specs) + "512\n"
     (tmp_path / "s.txt").write_text(script)
     wq, wk = synth.norm_weights()
@@ -116,3 +115,16 @@ def test_serving_loop_matches_oracle(gpu, tmp_path):
         sch.retired = []
     assert [(st["t"], st["computed"].tolist(), st["n_new"].tolist()) for st in got] == model_batches
     assert any(preempts)
+
+
+@pytest.mark.gpu
+def test_serving_loop_matches_oracle(gpu, tmp_path):
+    """10 sequences over 16 steps on a 20-page pool (3 preemptions)."""
+    _serve_case(tmp_path, 77, 10, 20, 6, 96, 48, 16, cancel_id=8)
+
+
+@pytest.mark.gpu
+def test_serving_loop_longer(gpu, tmp_path):
+    """24 sequences over 40 steps: more slots, a larger budget and chunk, a 26-page pool
+    (10 preemptions in the scheduler model; all 24 sequences retire)."""
+    _serve_case(tmp_path, 78, 24, 26, 8, 128, 64, 40, cancel_id=5)
