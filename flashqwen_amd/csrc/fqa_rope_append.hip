@@ -22,6 +22,11 @@
 // where a range ends) go through the same XCD's L2.
 // Memory-bound: per row 12 KiB read, 8 KiB (q) + 4 KiB (k, v) written.
 //
+// fqa_qkv_proj_append runs the same kernel on the QKV projection's split-K partials
+// (kPart): a row's values are the sum of the fp32 partials in split order, rounded to
+// bf16 exactly as the projection's own reduction would round them, so the results match
+// fqa_gemm + fqa_qknorm_rope_append bit for bit without the bf16 qkv round trip.
+//
 #include "fqa_common.h"
 #include "fqa_gemm_internal.h"
 
