@@ -118,7 +118,12 @@ __device__ __forceinline__ void wait_vm() {
 // moving LDS accesses across it.  Callers wait for what they need first.
 __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-__global__ void __launch_bounds__(256, 3) prefill_kernel(PreArgs a) {
+// kRG row groups of 32 rows per workgroup (4 kRG waves): wave w is query head w % 4 of the
+// kv head for rows 32 (w / 4) ..  of the item; the K/V staging of a half is split over
+// all the waves, so a 64-row item (kRG = 2) stages each half once for twice the work.
+template <int kRG>
+__global__ void __launch_bounds__(256 * kRG, kRG == 1 ? 3 : 1) prefill_kernel(PreArgs a) {
+  constexpr int kLoads = 4 / kRG;  // global->LDS loads per wave per half
   __shared__ __attribute__((aligned(1024))) char lds[kRing * kHalfBytes];
   auto ring = [&](int t) { return lds + (t % kRing) * kHalfBytes; };
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
@@ -129,6 +134,7 @@ __global__ void __launch_bounds__(256, 3) prefill_kernel(PreArgs a) {
   const int n_items = a.meta[FQA_META_PRE_ITEMS];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hw = w & 3, rg = w >> 2;  // query head within the kv head, row group
   const int4 it = *reinterpret_cast<const int4*>(a.items + 4 * (long long)item);
   asm volatile("" ::"s"(it.x), "s"(it.w), "s"(n_items));  // both loads before the check
   if (item >= n_items) return;
@@ -144,14 +150,14 @@ __global__ void __launch_bounds__(256, 3) prefill_kernel(PreArgs a) {
   const int n_pages = (nkeys + kPage - 1) / kPage;
 
   const int col = lane & 31, hf = lane >> 5;
-  const int i_row = q0 + col;  // row within the request
+  const int i_row = q0 + 32 * rg + col;  // row within the request
   const bool row_ok = i_row < q1;
   // A request's new rows sit at positions computed .. computed+qlen-1 (the pack writes
   // positions[] that way, scheduler.h:66-72), and n_keys = computed + q1.
   const int computed = nkeys - q1;
   const int qpos = row_ok ? computed + i_row : -1;
-  const int min_pos = computed + q0;  // first row: smallest position of the tile
-  const int h = kvh * kG + w;
+  const int min_pos = computed + q0 + 32 * rg;  // first row: smallest position of the wave
+  const int h = kvh * kG + hw;
 
   bf16x8 qf[8];
   {
@@ -182,16 +188,18 @@ __global__ void __launch_bounds__(256, 3) prefill_kernel(PreArgs a) {
   // scalar-cache line holds the ids of 8 halves).  Ids kept in VGPRs instead would be
   // global loads, and the compiler would then wait for every outstanding global->LDS
   // load before touching those registers.
-  const int st_ps = w >> 1, st_v = w & 1;
-  uint32_t st_off[4];  // byte offset inside the 8 KiB run of this lane's chunk, per load
+  // With kRG row groups the wave moves kiBs qd = rg * kLoads .. of its region.
+  const int st_ps = (w >> 1) & 1, st_v = w & 1;
+  uint32_t st_off[kLoads];  // byte offset inside the 8 KiB run of this lane's chunk, per load
 #pragma unroll
-  for (int qd = 0; qd < 4; ++qd) {
+  for (int j = 0; j < kLoads; ++j) {
+    const int qd = rg * kLoads + j;
     if (st_v) {
       const int d = 32 * qd + (lane >> 1);
-      st_off[qd] = kVOff * 2 + d * 32 + (((lane & 1) ^ ((d >> 3) & 1)) << 4);
+      st_off[j] = kVOff * 2 + d * 32 + (((lane & 1) ^ ((d >> 3) & 1)) << 4);
     } else {
       // global [16 tokens][128 dims]: token t's chunk c at t*256 + c*16
-      st_off[qd] = (lane & 15) * 256 + (4 * qd + (lane >> 4)) * 16;
+      st_off[j] = (lane & 15) * 256 + (4 * qd + (lane >> 4)) * 16;
     }
   }
   // Valid tokens (0..16) of the two page slots of the half in each ring buffer, 5 bits
@@ -223,7 +231,7 @@ __global__ void __launch_bounds__(256, 3) prefill_kernel(PreArgs a) {
       const bool ok = valid > 0 && (uint32_t)id < pool_pages32;
       const int sh = (R * 2 + ps) * 5;
       pvbits = (pvbits & ~(31ull << sh)) | ((unsigned long long)(ok ? valid : 0) << sh);
-      // Every wave issues exactly 4 loads per half (a bad page reads page 0, zeroed
+      // Every wave issues exactly kLoads loads per half (a bad page reads page 0, zeroed
       // later), so the vmcnt counts in half_step hold.
       if (ps == st_ps) {
         dm.run = a.pool + run_offset(ok ? id : 0, kvh);
@@ -235,7 +243,8 @@ __global__ void __launch_bounds__(256, 3) prefill_kernel(PreArgs a) {
   auto stage_issue = [&](int hx, const Ids& ids) {
     const Dma dm = stage_prep(hx, ids);
 #pragma unroll
-    for (int qd = 0; qd < 4; ++qd) dma16(dm.run, st_off[qd], dm.dst + qd * 1024);
+    for (int j = 0; j < kLoads; ++j)
+      dma16(dm.run, st_off[j], dm.dst + (rg * kLoads + j) * 1024);
   };
   // Zero what must not count in ring buffer R: V^T tokens past a page's valid count, and
   // all of K for a page that is missing or outside the pool.  Runs after the barrier
@@ -244,17 +253,19 @@ __global__ void __launch_bounds__(256, 3) prefill_kernel(PreArgs a) {
     const int R = hx % kRing;
     if (pv(R, 0) == kPage && pv(R, 1) == kPage) return;  // uniform
     char* base = ring(hx);
-    const int ps = tid >> 7, d = tid & 127;
-    const int valid = pv(R, ps);
-    uint4* p0 = reinterpret_cast<uint4*>(base + lds_v(ps, d, 0));
-    uint4* p1 = reinterpret_cast<uint4*>(base + lds_v(ps, d, 1));
-    const uint4 v0 = *p0, v1 = *p1;  // both reads before any write
-    *p0 = keep_tokens8(v0, 0, valid);
-    *p1 = keep_tokens8(v1, 8, valid);
+    if (tid < 256) {  // threads 0..255 cover both page slots
+      const int ps = tid >> 7, d = tid & 127;
+      const int valid = pv(R, ps);
+      uint4* p0 = reinterpret_cast<uint4*>(base + lds_v(ps, d, 0));
+      uint4* p1 = reinterpret_cast<uint4*>(base + lds_v(ps, d, 1));
+      const uint4 v0 = *p0, v1 = *p1;  // both reads before any write
+      *p0 = keep_tokens8(v0, 0, valid);
+      *p1 = keep_tokens8(v1, 8, valid);
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int c = tid * 2 + k, kps = c >> 8;  // 256 K chunks per page
-      if (pv(R, kps) == 0) *reinterpret_cast<uint4*>(base + kps * kRunBytes + (c & 255) * 16) = make_uint4(0, 0, 0, 0);
+      for (int k = 0; k < 2; ++k) {
+        const int c = tid * 2 + k, kps = c >> 8;  // 256 K chunks per page
+        if (pv(R, kps) == 0) *reinterpret_cast<uint4*>(base + kps * kRunBytes + (c & 255) * 16) = make_uint4(0, 0, 0, 0);
+      }
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     barrier();
@@ -283,7 +294,7 @@ __global__ void __launch_bounds__(256, 3) prefill_kernel(PreArgs a) {
     constexpr bool kNext = decltype(next_tag)::value;
     // B(t): half t+1's loads have landed in every wave, and every wave has finished
     // reading buffer R3 (half t-1).
-    if (t + kAhead - 1 < n_half) wait_vm<(kAhead - 2) * 4>(); else wait_vm<0>();
+    if (t + kAhead - 1 < n_half) wait_vm<(kAhead - 2) * kLoads>(); else wait_vm<0>();
     barrier();
     if (t + kAhead < n_half) {
       stage_issue(t + kAhead, ids_next);
@@ -402,7 +413,7 @@ __global__ void __launch_bounds__(256, 3) prefill_kernel(PreArgs a) {
   for (int hx = 1; hx < kAhead; ++hx)
     if (hx < n_half) stage_issue(hx, load_ids(hx));
   if (n_half > kAhead) ids_next = load_ids(kAhead);
-  if (n_half >= kAhead) wait_vm<(kAhead - 1) * 4>(); else wait_vm<0>();
+  if (n_half >= kAhead) wait_vm<(kAhead - 1) * kLoads>(); else wait_vm<0>();
   barrier();
   stage_fix(0);
   s_cur = s_tile(ring(0));
@@ -443,14 +454,18 @@ extern "C" int fqa_prefill(const fqa_dims* dims, const uint16_t* qkv, const uint
                            int32_t pre_item_cap, uint16_t* out, void* stream) {
   if (!dims) return FQA_EINVAL;
   if (!dims_ok(dims)) return FQA_EUNSUPPORTED;
-  if (pre_tile_q != kQT) return FQA_EUNSUPPORTED;
+  if (pre_tile_q != kQT && pre_tile_q != 2 * kQT) return FQA_EUNSUPPORTED;
   if (pre_item_cap < 0 || max_blocks < 1 || pool_pages < 1 || !meta) return FQA_EINVAL;
   if (pre_item_cap == 0) return FQA_OK;
   if (!qkv || !pool || !block_tables || !cu_seqlens || !positions || !pre_items || !out)
     return FQA_EINVAL;
   PreArgs a{qkv, pool, pool_pages, block_tables, max_blocks, cu_seqlens, positions, pre_items,
             meta, out, dims->qkv_stride, dims->scale * kLog2e};
-  hipLaunchKernelGGL(prefill_kernel, dim3(pre_item_cap * kHkv), dim3(256), 0,
-                     (hipStream_t)stream, a);
+  if (pre_tile_q == kQT)
+    hipLaunchKernelGGL(prefill_kernel<1>, dim3(pre_item_cap * kHkv), dim3(256), 0,
+                       (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(prefill_kernel<2>, dim3(pre_item_cap * kHkv), dim3(512), 0,
+                       (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
 }

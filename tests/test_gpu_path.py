@@ -138,7 +138,7 @@ def _check_step(cfg, sub, kw, seed, label, schedule=False, kernel_only=True):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("cfgno,tile", [(1, 32), (2, 32), (3, 32)])
+@pytest.mark.parametrize("cfgno,tile", [(1, 32), (2, 32), (3, 32), (3, 64)])
 def test_step_parity(gpu, cfgno, tile):
     print(f"[test_step_parity] config{cfgno} tile{tile}", flush=True)
     cfg = synth.CONFIGS[cfgno]()
