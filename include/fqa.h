@@ -231,7 +231,8 @@ int fqa_decode(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
  * from one LDS-staged copy of each K/V tile.  Mask: key pos <= query pos (cached
  * prefix included).  Output rows out[cu_seqlens[r] + i].  Row i of request r is at
  * position computed[r] + i, as fqa_pack writes positions[] (scheduler.h:66-72); the kernel
- * derives it from the work item rather than loading positions[]. */
+ * derives it from the work item rather than loading positions[].  pre_tile_q must be the
+ * pack's: 32 (fastest) or 64; other values return FQA_EUNSUPPORTED. */
 int fqa_prefill(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
                 int64_t pool_pages, const int32_t* block_tables, int32_t max_blocks,
                 const int32_t* cu_seqlens, const int32_t* positions,

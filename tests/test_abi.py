@@ -79,7 +79,7 @@ def test_rejected_calls_return_codes_without_launching():
     assert lib.fqa_qknorm_rope_append(C.byref(bad), *([null] * 5 + [1] + [null] * 3 + [1, null, 1,
                                                         0, null])) == _lib.FQA_EUNSUPPORTED
     # unsupported prefill tile; null pointers with work to do
-    assert lib.fqa_prefill(C.byref(d), null, null, 1, null, 1, null, null, null, null, 64, 1, null,
+    assert lib.fqa_prefill(C.byref(d), null, null, 1, null, 1, null, null, null, null, 128, 1, null,
                            null) == _lib.FQA_EUNSUPPORTED
     assert lib.fqa_decode(C.byref(d), null, null, 1, null, 1, null, null, null, 4, 4, null, null,
                           null) == _lib.FQA_EINVAL
