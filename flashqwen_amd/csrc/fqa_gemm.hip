@@ -155,15 +155,18 @@ __global__ void __launch_bounds__(T::kThreads, 1) gemm_kernel(GemmArgs a) {
     const int tr = T::kRowsPerDma * (w * T::kDmaB + i) + drow;
     off_b[i] = (uint32_t)((long long)(col0 + tr) * a.ldw * 2) + (dlc ^ T::swz(tr)) * 16;
   }
-  auto issue = [&](int j) {  // this workgroup's j-th k step
+  // load q (0 .. kDmaA + kDmaB - 1) of this wave's share of the workgroup's j-th k step
+  auto issue_one = [&](int j, int q) {
     const uint32_t dst = lds_base + (j % T::kRing) * T::kStage;
-    const uint16_t* xa = xk + (long long)j * kstride;
-    const uint16_t* wb = wk + (long long)j * kstride;
+    if (q < T::kDmaA)
+      dma16(xk + (long long)j * kstride, off_a[q], dst + (w * T::kDmaA + q) * 1024);
+    else
+      dma16(wk + (long long)j * kstride, off_b[q - T::kDmaA],
+            dst + T::kABytes + (w * T::kDmaB + q - T::kDmaA) * 1024);
+  };
+  auto issue = [&](int j) {
 #pragma unroll
-    for (int i = 0; i < T::kDmaA; ++i) dma16(xa, off_a[i], dst + (w * T::kDmaA + i) * 1024);
-#pragma unroll
-    for (int i = 0; i < T::kDmaB; ++i)
-      dma16(wb, off_b[i], dst + T::kABytes + (w * T::kDmaB + i) * 1024);
+    for (int q = 0; q < T::kDmaA + T::kDmaB; ++q) issue_one(j, q);
   };
 
   // fragment reads: lane reads row (lane & 31) of a 32-row block, k chunk 2 kk + lane/32,
@@ -213,16 +216,23 @@ __global__ void __launch_bounds__(T::kThreads, 1) gemm_kernel(GemmArgs a) {
         wait_steps<kPer, T::kRing - 2>(min(T::kRing - 2, n_my - 2 - s));
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of step s done
         barrier();
-        if (s + T::kRing < n_my) issue(s + T::kRing);
         read_frags(0, s + 1, 0);
       }
       __builtin_amdgcn_sched_barrier(0);  // keep those reads ahead of this sub-step's MFMAs
+      // On the last sub-step the freed slot's refill (step s + kRing) is issued one load
+      // after each MFMA, so the wave's load issue overlaps its own MFMAs.
+      const bool refill = kk + 1 == T::kKK && s + T::kRing < n_my;
+      constexpr int kMfma = T::kTM * T::kTN;
 #pragma unroll
-      for (int rb = 0; rb < T::kTM; ++rb)
-#pragma unroll
-        for (int cb = 0; cb < T::kTN; ++cb)
+      for (int q = 0; q < (kMfma > kPer ? kMfma : kPer); ++q) {
+        if (q < kMfma) {
+          const int rb = q / T::kTN, cb = q % T::kTN;
           acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfg[kk & 1][cb], af[kk & 1][rb],
                                                                 acc[rb][cb], 0, 0, 0);
+        }
+        if (q < kPer && refill) issue_one(s + T::kRing, q);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
 
