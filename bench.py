@@ -433,6 +433,22 @@ def bench_gemm(args):
         uf, fu = timed(unfused), timed(fused)
         out[f"qkv_append_M{M}"] = {"fused_us": round(fu, 2), "unfused_us": round(uf, 2)}
         print("qkv+append", M, out[f"qkv_append_M{M}"], flush=True)
+    # lm_head + greedy pick: fused (no logits written) against fqa_gemm (fp32) + fqa_sample
+    from flashqwen_amd.gemm import gemm_argmax
+    from flashqwen_amd.sample import sample
+
+    N, K = GEMM_SHAPES["lm_head"]
+    w = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    for M in [r for r in rows if r <= 256]:
+        x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+        logits = torch.empty(M, N, device="cuda", dtype=torch.float32)
+        zero = torch.zeros(M, device="cuda")
+        one = torch.ones(M, device="cuda")
+        tok = torch.empty(M, dtype=torch.int32, device="cuda")
+        fu = timed(lambda: gemm_argmax(x, w, out=tok))
+        uf = timed(lambda: sample(gemm(x, w, out=logits, out_f32=True), zero, one, zero, tok))
+        out[f"lm_head_greedy_M{M}"] = {"fused_us": round(fu, 2), "unfused_us": round(uf, 2)}
+        print("lm_head+greedy", M, out[f"lm_head_greedy_M{M}"], flush=True)
     print(json.dumps({"gemm": out, "peak_TFLOPs": 2516.6, "peak_GBps": HBM_PEAK_GBS}))
 
 

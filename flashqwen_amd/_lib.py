@@ -114,6 +114,8 @@ SIGNATURES = {
         [C.POINTER(FqaDims), P, I64, P, I64, I32, I32, P, P, P, P, P, I32, P, P, P, P, I64, I32,
          P, I64, P],
     ),
+    "fqa_gemm_argmax_workspace_bytes": (I64, [I32, I32, I32]),
+    "fqa_gemm_argmax": (C.c_int, [P, I64, P, I64, I32, I32, I32, P, P, I64, P]),
     "fqa_version": (C.c_char_p, []),
 }
 

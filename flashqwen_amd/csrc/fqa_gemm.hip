@@ -71,6 +71,8 @@ struct GemmArgs {
   int M, N, K;
   int splits;
   int m_tiles, n_tiles;
+  float* amax_v;  // argmax mode: per (n tile, row) the tile's largest value and its column
+  int* amax_i;
 };
 
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
@@ -121,7 +123,7 @@ __device__ __forceinline__ void tile_of(const GemmArgs& a, int& tm, int& tn, int
   tn = r / gs;
 }
 
-template <class T, bool kF32Out, bool kPartial>
+template <class T, bool kF32Out, bool kPartial, bool kArgmax = false>
 __global__ void __launch_bounds__(T::kThreads, 1) gemm_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds[T::kRing * T::kStage];
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
@@ -236,6 +238,61 @@ __global__ void __launch_bounds__(T::kThreads, 1) gemm_kernel(GemmArgs a) {
     }
   }
 
+  if constexpr (kArgmax) {
+    // per row of the tile: the largest value and its column (the smallest on ties), over
+    // this lane's values, then lane ^ 32 (the other column half of the same row), then
+    // the tile's kWN column waves through LDS (free once every wave's reads are done)
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    barrier();
+    float* sv = reinterpret_cast<float*>(lds);
+    int* si = reinterpret_cast<int*>(lds + T::kBM * T::kWN * 4);
+#pragma unroll
+    for (int rb = 0; rb < T::kTM; ++rb) {
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+#pragma unroll
+      for (int cb = 0; cb < T::kTN; ++cb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float v = acc[rb][cb][4 * q + e];
+            const int n = col0 + (wn * T::kTN + cb) * 32 + 8 * q + 4 * (lane >> 5) + e;
+            if (v > bv || (v == bv && n < bi)) {
+              bv = v;
+              bi = n;
+            }
+          }
+      const float ov = __shfl_xor(bv, 32, kWave);
+      const int oi = __shfl_xor(bi, 32, kWave);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+      const int r = (wm * T::kTM + rb) * 32 + (lane & 31);  // row within the tile
+      if (lane < 32) {
+        sv[r * T::kWN + wn] = bv;
+        si[r * T::kWN + wn] = bi;
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    barrier();
+    for (int r = threadIdx.x; r < T::kBM; r += T::kThreads) {
+      const int m = row0 + r;
+      if (m >= a.M) continue;
+      float bv = sv[r * T::kWN];
+      int bi = si[r * T::kWN];
+      for (int k = 1; k < T::kWN; ++k)
+        if (sv[r * T::kWN + k] > bv || (sv[r * T::kWN + k] == bv && si[r * T::kWN + k] < bi)) {
+          bv = sv[r * T::kWN + k];
+          bi = si[r * T::kWN + k];
+        }
+      a.amax_v[(long long)tn * a.M + m] = bv;
+      a.amax_i[(long long)tn * a.M + m] = bi;
+    }
+    return;
+  }
+
   // The MFMAs compute the transposed block (W fragments as the 32-row operand), so
   // accumulator (rb, cb) registers 4q..4q+3 of lane hold row 32 rb + lane % 32 and the 4
   // consecutive columns 32 cb + 8 q + 4 (lane / 32) + 0..3 of the wave's block: one
@@ -261,6 +318,33 @@ __global__ void __launch_bounds__(T::kThreads, 1) gemm_kernel(GemmArgs a) {
               make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
       }
   }
+}
+
+// Row m's token: the largest of its per-tile maxima, the smallest column on ties (tiles
+// cover increasing columns).  One wave per row.
+__global__ void __launch_bounds__(256) gemm_argmax_reduce_kernel(GemmArgs a, int32_t* out) {
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (m >= a.M) return;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int t = lane; t < a.n_tiles; t += kWave) {
+    const float v = a.amax_v[(long long)t * a.M + m];
+    const int i = a.amax_i[(long long)t * a.M + m];
+    if (v > bv || (v == bv && i < bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, kWave);
+    const int oi = __shfl_xor(bi, o, kWave);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) out[m] = bi < a.N ? bi : 0;  // all -inf / NaN: token 0, as fqa_sample
 }
 
 // y = sum over the splits of the fp32 partials, 4 columns per thread.
@@ -319,6 +403,11 @@ bool gemm_shape_ok(int M, int N, int K) {
   return M >= 0 && N > 0 && K > 0 && N % 128 == 0 && K % kGK == 0;
 }
 
+template <class T>
+void launch_argmax(const GemmArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL((gemm_kernel<T, false, false, true>),
+                     dim3((unsigned)(a.m_tiles * a.n_tiles)), dim3(T::kThreads), 0, st, a);
+}
 template <class T>
 void launch_gemm(const GemmArgs& a, bool f32, hipStream_t st) {
   const dim3 grid((unsigned)(a.m_tiles * a.n_tiles * a.splits));
@@ -408,5 +497,52 @@ extern "C" int fqa_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, 
     else
       hipLaunchKernelGGL((gemm_reduce_kernel<false>), dim3(blocks), dim3(256), 0, st, a);
   }
+  return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
+}
+
+// The argmax plan: the projection's tiles without a K split (every tile sees whole rows
+// of its columns).
+static bool argmax_plan(int32_t M, int32_t N, int32_t K, GemmPlan& p) {
+  if (!gemm_shape_ok(M, N, K) || M == 0) return false;
+  p = gemm_plan(M, N, K);
+  p.splits = 1;
+  return true;
+}
+
+extern "C" int64_t fqa_gemm_argmax_workspace_bytes(int32_t M, int32_t N, int32_t K) {
+  GemmPlan p;
+  if (!argmax_plan(M, N, K, p)) return 0;
+  return (int64_t)p.n_tiles * M * 8;
+}
+
+extern "C" int fqa_gemm_argmax(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                               int32_t M, int32_t N, int32_t K, int32_t* out, void* workspace,
+                               int64_t workspace_bytes, void* stream) {
+  if (M < 0 || N <= 0 || K <= 0) return FQA_EINVAL;
+  if (!gemm_shape_ok(M, N, K)) return FQA_EUNSUPPORTED;
+  if (M == 0) return FQA_OK;
+  if (!x || !w || !out || !workspace) return FQA_EINVAL;
+  if (ldx < K || ldw < K || ldx % 8 || ldw % 8) return FQA_EINVAL;
+  if (((uintptr_t)x & 15) || ((uintptr_t)w & 15) || ((uintptr_t)workspace & 15)) return FQA_EINVAL;
+  if ((int64_t)(M - 1) * ldx * 2 >= (int64_t)1 << 32 || (int64_t)(N - 1) * ldw * 2 >= (int64_t)1 << 32)
+    return FQA_EUNSUPPORTED;
+  GemmPlan p;
+  argmax_plan(M, N, K, p);
+  if (workspace_bytes < (int64_t)p.n_tiles * M * 8) return FQA_EINVAL;
+  if ((int64_t)p.m_tiles * p.n_tiles > 0x7fffffff) return FQA_EINVAL;
+  GemmArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), nullptr, nullptr,
+             ldx, ldw, 0, M, N, K, 1, p.m_tiles, p.n_tiles,
+             static_cast<float*>(workspace),
+             reinterpret_cast<int*>(static_cast<char*>(workspace) + (int64_t)p.n_tiles * M * 4)};
+  hipStream_t st = (hipStream_t)stream;
+  switch (p.tile) {
+    case 0: launch_argmax<TileL>(a, st); break;
+    case 4: launch_argmax<TileL8>(a, st); break;
+    case 1: launch_argmax<TileM>(a, st); break;
+    case 2: launch_argmax<TileS>(a, st); break;
+    default: launch_argmax<TileT>(a, st); break;
+  }
+  hipLaunchKernelGGL(gemm_argmax_reduce_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st, a,
+                     out);
   return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
 }

@@ -50,3 +50,27 @@ def gemm(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None,
                           out.stride(0), M, N, K, int(out_f32), ws_ptr, ws_len, stream),
           "fqa_gemm")
     return out
+
+
+def gemm_argmax(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None,
+                workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy tokens of x . W^T (lm_head + argmax, smallest index on ties) without writing
+    the logits: x [M, K] bf16, w [N, K] bf16 -> [M] int32, on the current stream."""
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or x.dim() != 2 or w.dim() != 2:
+        raise ValueError("x and w must be 2-D bf16 tensors")
+    if x.stride(1) != 1 or w.stride(1) != 1 or x.shape[1] != w.shape[1]:
+        raise ValueError("x and w need unit column stride and equal inner sizes")
+    M, K = x.shape
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty(M, dtype=torch.int32, device=x.device)
+    lib = load()
+    need = int(lib.fqa_gemm_argmax_workspace_bytes(M, N, K))
+    if workspace is None:
+        workspace = _workspace(x.device, max(need, 16))
+    ws_len = workspace.numel() * workspace.element_size()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    check(lib.fqa_gemm_argmax(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), M, N, K,
+                              out.data_ptr(), workspace.data_ptr(), ws_len, stream),
+          "fqa_gemm_argmax")
+    return out

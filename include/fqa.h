@@ -16,6 +16,7 @@
  *   fqa_sample              <- LaunchSampleBatch (greedy / temperature + top-p) (kernels.cu:184-327)
  *   fqa_gemm                <- LaunchGemm (QKV, o_proj, gate-up, down, lm_head) (kernels.cu:9-16)
  *   fqa_qkv_proj_append     <- LaunchGemm(QKV) + LaunchHeadNormRope + StoreKV (model_runtime.cu:261-268)
+ *   fqa_gemm_argmax         <- LaunchGemm(lm_head) + ArgmaxKernel, greedy rows (model_runtime.cu:322-325)
  *
  * Conventions (all entry points):
  *   - Plain device pointers and sizes; every launch goes on the caller's hipStream_t
@@ -272,6 +273,18 @@ int64_t fqa_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K);
 int fqa_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
              int32_t M, int32_t N, int32_t K, int32_t y_f32, void* workspace,
              int64_t workspace_bytes, void* stream);
+
+/* lm_head fused with the greedy pick (LaunchGemm(lm_head) + ArgmaxKernel,
+ * model_runtime.cu:322-325, kernels.cu:184-327): out[m] = the column of the largest value of
+ * row m of x . W^T (fp32 accumulation, the values fqa_gemm computes with y_f32 = 1), the
+ * smallest column among equal values, as fqa_sample's greedy rows pick.  The logits are
+ * never written: each output tile leaves its row maxima in `workspace`
+ * (fqa_gemm_argmax_workspace_bytes(M, N, K) bytes, 16-byte aligned) and a second kernel
+ * reduces them.  Shape rules as fqa_gemm. */
+int64_t fqa_gemm_argmax_workspace_bytes(int32_t M, int32_t N, int32_t K);
+int fqa_gemm_argmax(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t M,
+                    int32_t N, int32_t K, int32_t* out, void* workspace, int64_t workspace_bytes,
+                    void* stream);
 
 /* The QKV projection fused with fqa_qknorm_rope_append (model_runtime.cu:261-268:
  * LaunchGemm into buf_.qkv, LaunchHeadNormRope, StoreKV): qkv = x . w_qkv^T for `rows`

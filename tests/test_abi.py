@@ -177,3 +177,14 @@ def test_header_is_plain_c(tmp_path):
                         f"-Wl,-rpath,{root / 'flashqwen_amd'}"], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
     assert subprocess.run([str(exe)]).returncode == 0
+
+
+def test_gemm_argmax_rejections_without_gpu():
+    from flashqwen_amd import _lib
+
+    lib = _lib.load()
+    assert lib.fqa_gemm_argmax(None, 64, None, 64, 4, 100, 64, None, None, 0, None) == _lib.FQA_EUNSUPPORTED
+    assert lib.fqa_gemm_argmax(None, 64, None, 64, 4, 128, 64, None, None, 0, None) == _lib.FQA_EINVAL
+    assert lib.fqa_gemm_argmax(None, 64, None, 64, 0, 128, 64, None, None, 0, None) == _lib.FQA_OK
+    # lm_head at 256 rows: 1187 tiles of 256 x 128, one (max, column) pair per tile and row
+    assert lib.fqa_gemm_argmax_workspace_bytes(256, 151936, 4096) == 1187 * 256 * 8

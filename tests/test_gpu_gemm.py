@@ -115,3 +115,29 @@ def test_gemm_lm_head_fp32(gpu):
     ref = _ref(x, w[cols])
     got = y.cpu().numpy()[:, cols].astype(np.float64)
     assert np.all(np.abs(got - ref) <= 1e-5 * np.abs(ref) + 1e-4)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", [(1, 151936, 4096), (64, 151936, 4096), (256, 151936, 4096),
+                                   (300, 1280, 256), (2000, 4096, 128)])
+def test_gemm_argmax_equals_greedy_of_logits(gpu, M, N, K):
+    """fqa_gemm_argmax picks, per row, the column fqa_gemm's fp32 logits peak at (smallest
+    index on ties); duplicated W rows create exact ties."""
+    import torch
+
+    from flashqwen_amd.gemm import gemm, gemm_argmax
+
+    print(f"[gemm_argmax] M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M + N)
+    x = _bf16(rng, (M, K)).to(gpu)
+    w = _bf16(rng, (N, K), 0.02)
+    w[N - 1] = w[N // 3]  # an exact tie between two columns
+    w[N // 2] = w[N // 3]
+    w = w.to(gpu)
+    x[0] = (w[N // 3].float() * 40).to(torch.bfloat16)  # row 0 peaks at the tied columns
+    got = gemm_argmax(x, w)
+    logits = gemm(x, w, out_f32=True)
+    torch.cuda.synchronize()
+    want = np.argmax(logits.cpu().numpy(), axis=1)  # first maximum
+    assert np.array_equal(got.cpu().numpy(), want)
+    assert int(got[0]) == N // 3
