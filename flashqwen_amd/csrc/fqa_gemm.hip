@@ -71,7 +71,7 @@ struct GemmArgs {
   int M, N, K;
   int splits;
   int m_tiles, n_tiles;
-  float* amax_v;  // argmax mode: per (n tile, row) the tile's largest value and its column
+  float* amax_v;  // argmax mode: per (row, n tile) the tile's largest value and its column
   int* amax_i;
 };
 
@@ -287,8 +287,10 @@ __global__ void __launch_bounds__(T::kThreads, 1) gemm_kernel(GemmArgs a) {
           bv = sv[r * T::kWN + k];
           bi = si[r * T::kWN + k];
         }
-      a.amax_v[(long long)tn * a.M + m] = bv;
-      a.amax_i[(long long)tn * a.M + m] = bi;
+      // row-major by row, so the reduction reads each row's maxima contiguously (these
+      // scattered 4-byte stores are a few hundred per tile of a long kernel)
+      a.amax_v[(long long)m * a.n_tiles + tn] = bv;
+      a.amax_i[(long long)m * a.n_tiles + tn] = bi;
     }
     return;
   }
@@ -327,13 +329,25 @@ __global__ void __launch_bounds__(256) gemm_argmax_reduce_kernel(GemmArgs a, int
   if (m >= a.M) return;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int t = lane; t < a.n_tiles; t += kWave) {
-    const float v = a.amax_v[(long long)t * a.M + m];
-    const int i = a.amax_i[(long long)t * a.M + m];
-    if (v > bv || (v == bv && i < bi)) {
-      bv = v;
-      bi = i;
+  const float* rv = a.amax_v + (long long)m * a.n_tiles;
+  const int* ri = a.amax_i + (long long)m * a.n_tiles;
+  // 8 tiles per lane per round, all loads issued before any compare (clamped indices;
+  // the repeats of the last tile change nothing)
+  for (int t0 = 0; t0 < a.n_tiles; t0 += 8 * kWave) {
+    float v[8];
+    int i[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int t = min(t0 + k * kWave + lane, a.n_tiles - 1);
+      v[k] = rv[t];
+      i[k] = ri[t];
     }
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (v[k] > bv || (v[k] == bv && i[k] < bi)) {
+        bv = v[k];
+        bi = i[k];
+      }
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
