@@ -119,10 +119,11 @@ def test_gemm_lm_head_fp32(gpu):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,N,K", [(1, 151936, 4096), (64, 151936, 4096), (256, 151936, 4096),
-                                   (300, 1280, 256), (2000, 4096, 128)])
+                                   (300, 1280, 256), (2000, 4096, 128), (5, 128 * 600, 64)])
 def test_gemm_argmax_equals_greedy_of_logits(gpu, M, N, K):
     """fqa_gemm_argmax picks, per row, the column fqa_gemm's fp32 logits peak at (smallest
-    index on ties); duplicated W rows create exact ties."""
+    index on ties); duplicated W rows create exact ties.  600 column tiles cross the
+    reduce's 512-tile round; row 1 peaks in the last tile."""
     import torch
 
     from flashqwen_amd.gemm import gemm, gemm_argmax
@@ -135,9 +136,13 @@ def test_gemm_argmax_equals_greedy_of_logits(gpu, M, N, K):
     w[N // 2] = w[N // 3]
     w = w.to(gpu)
     x[0] = (w[N // 3].float() * 40).to(torch.bfloat16)  # row 0 peaks at the tied columns
+    if M > 1:  # row 1 peaks in the last column tile
+        x[1] = (w[N - 2].float() * 40).to(torch.bfloat16)
     got = gemm_argmax(x, w)
     logits = gemm(x, w, out_f32=True)
     torch.cuda.synchronize()
     want = np.argmax(logits.cpu().numpy(), axis=1)  # first maximum
     assert np.array_equal(got.cpu().numpy(), want)
     assert int(got[0]) == N // 3
+    if M > 1:
+        assert int(got[1]) == N - 2
