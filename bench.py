@@ -35,9 +35,12 @@ BF16_PEAK_TFLOPS = 2500.0
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=500)
-    ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=5, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--no-prefill-lines", action="store_true",
+                    help="config 5: skip the config 3/4 prefill measurements added under "
+                         "the line's 'prefill' key")
     ap.add_argument("--kernel-reps", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -91,6 +94,38 @@ def main():
         bench_gemm(args)
         return
 
+    line = run_config(args, args.config, steps=args.steps, warmup=args.warmup,
+                      with_cpu=not args.no_cpu)
+    if line is None:  # --profile-kernels
+        return
+    if args.config == 5 and not args.no_prefill_lines:
+        # the metric's second half: prefill MFMA utilisation on the two prefill configs,
+        # measured in the same process after config 5's pool is released
+        import gc
+
+        import torch
+
+        gc.collect()
+        torch.cuda.empty_cache()
+        pre = {}
+        for c in (3, 4):
+            sub = run_config(args, c, steps=max(args.steps, 20), warmup=args.warmup,
+                             with_cpu=False)
+            pre[f"config{c}"] = {"workload": sub["config"]["workload"],
+                                 "ms_per_step": sub["ms_per_step"],
+                                 "tokens_per_s": sub["value"],
+                                 "rows_per_step": sub["config"]["rows_per_step"],
+                                 "roofline": sub["roofline"],
+                                 "kernels_us": sub["kernels_us"]}
+            gc.collect()
+            torch.cuda.empty_cache()
+        line["prefill"] = pre
+    print(json.dumps(line))
+
+
+def run_config(args, config, *, steps, warmup, with_cpu):
+    """Build config `config`, time `steps` whole steps (after `warmup`) and each kernel, and
+    return the JSON line's fields (None in --profile-kernels mode)."""
     import torch
 
     from flashqwen_amd import synth
@@ -98,10 +133,10 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.config == 5:
+    if config == 5:
         cfg = synth.config5(layers=args.layers or 36)
     else:
-        cfg = synth.CONFIGS[args.config]()
+        cfg = synth.CONFIGS[config]()
     layers = cfg.layers
     scheduled = cfg.num_tokens is not None
 
@@ -201,6 +236,8 @@ def main():
                                                                           wk_d)}
     if has_decode:
         kernels["decode"] = lambda: step.attn_decode(qkv, pool[0], out)
+        # the same plan's pages read with the same loads and no arithmetic: the floor
+        kernels["decode_read_floor"] = lambda: step.decode_read_floor(pool[0])
     if has_prefill:
         kernels["prefill"] = lambda: step.attn_prefill(qkv, pool[0], out)
     kgraphs = {k: kernel_graph(f, reps) for k, f in kernels.items()}
@@ -213,14 +250,14 @@ def main():
                 kg.replay()
         torch.cuda.synchronize()
         print(json.dumps({"profile_kernels": list(kgraphs)}))
-        return
+        return None
 
     # ---- timed region: K whole steps -----------------------------------------------------
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ms_events = time_graph(graph, args.steps)
+    ms_events = time_graph(graph, steps)
     wall = time.perf_counter() - t0
     ms_step = ms_events
 
@@ -232,12 +269,12 @@ def main():
 
     # ---- roofline of the dominant kernel ---------------------------------------------------
     meta = step.meta_host()
-    if has_decode and (not has_prefill or args.config == 5):
+    if has_decode and (not has_prefill or config == 5):
         logical, unique = synth.decode_bytes(_selected(cfg, comp_sel, n_sel))
         bt_bytes = int(meta[9]) * 4
         bytes_per = logical + bt_bytes
         achieved = bytes_per / (kern_ms["decode"] * 1e-3) / 1e9
-        traffic, tsrc = _profile_traffic(args.config,
+        traffic, tsrc = _profile_traffic(config,
                                          ["decode_split_kernel", "decode_combine_kernel"])
         roof = {"kernel": "fqa_decode (decode_split_kernel + decode_combine_kernel)",
                 "bound": "hbm",
@@ -245,11 +282,13 @@ def main():
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "traffic_source": tsrc,
                 "bytes_per_launch": bytes_per, "unique_kv_bytes": unique,
-                "launch_us": round(kern_ms["decode"] * 1e3, 2)}
+                "launch_us": round(kern_ms["decode"] * 1e3, 2),
+                "read_floor_us": round(kern_ms["decode_read_floor"] * 1e3, 2),
+                "frac_of_read_floor": round(kern_ms["decode_read_floor"] / kern_ms["decode"], 4)}
     else:
         flops = synth.prefill_flops(comp_sel, n_sel)
         achieved = flops / (kern_ms["prefill"] * 1e-3) / 1e12
-        traffic, tsrc = _profile_traffic(args.config, ["prefill_kernel"])
+        traffic, tsrc = _profile_traffic(config, ["prefill_kernel"])
         roof = {"kernel": "fqa_prefill (prefill_kernel)", "bound": "mfma",
                 "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": traffic,
@@ -261,7 +300,7 @@ def main():
 
     # ---- CPU baseline (OpenMP fp32 oracle, bounded sample) ------------------------------
     cpu = None
-    if not args.no_cpu:
+    if with_cpu:
         cpu = cpu_baseline(cfg, comp_sel, n_sel, T, args.cpu_seconds)
 
     tokens_per_step = T
@@ -271,15 +310,15 @@ def main():
         "value": round(value, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) bf16 q/k/v and pool, seeded page placement)",
-        "config": {"workload": f"config{args.config}: {_describe(args.config)}",
+        "config": {"workload": f"config{config}: {_describe(config)}",
                    "rows_per_step": T, "requests": int(len(n_sel)), "layers": layers,
                    "pool_pages_per_layer": cfg.pool_pages, "head_shape": "32q/8kv/128",
                    "dec_wave_runs": int(meta[6]), "dec_waves": int(meta[4]),
@@ -289,7 +328,8 @@ def main():
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),
     }
-    print(json.dumps(line))
+    return line
+
 
 
 def bench_sampler(args):

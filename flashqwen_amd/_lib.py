@@ -14,6 +14,7 @@ FQA_OK = 0
 FQA_EINVAL = -1
 FQA_EUNSUPPORTED = -2
 FQA_ELAUNCH = -3
+FQA_ENOSPACE = -4
 FQA_PAGE_TOKENS = 16
 FQA_MAX_REQS = 2048
 
@@ -87,6 +88,9 @@ class FqaPackCfg(C.Structure):
 SIGNATURES = {
     "fqa_rope_tables": (C.c_int, [I32, I32, C.c_float, P, P]),
     "fqa_pool_bytes": (I64, [C.POINTER(FqaDims), I64]),
+    "fqa_pool_pages": (C.c_int, [C.POINTER(FqaDims), C.c_uint64, C.c_uint64, C.c_float, I32, I32,
+                                 C.POINTER(I64)]),
+    "fqa_pool_pages_device": (C.c_int, [C.POINTER(FqaDims), C.c_float, I32, I32, C.POINTER(I64)]),
     "fqa_dec_wave_bound": (I32, [I32, I32]),
     "fqa_dec_default_waves": (I32, [I32]),
     "fqa_pre_item_bound": (I32, [I32, I32, I32]),
@@ -116,6 +120,7 @@ SIGNATURES = {
     ),
     "fqa_gemm_argmax_workspace_bytes": (I64, [I32, I32, I32]),
     "fqa_gemm_argmax": (C.c_int, [P, I64, P, I64, I32, I32, I32, P, P, I64, P]),
+    "fqa_decode_read_floor": (C.c_int, [P, I64, P, I32, P, P, P, I32, P, P]),
     "fqa_version": (C.c_char_p, []),
 }
 
@@ -146,5 +151,6 @@ class FqaError(RuntimeError):
 
 def check(rc: int, what: str) -> None:
     if rc != FQA_OK:
-        names = {FQA_EINVAL: "EINVAL", FQA_EUNSUPPORTED: "EUNSUPPORTED", FQA_ELAUNCH: "ELAUNCH"}
+        names = {FQA_EINVAL: "EINVAL", FQA_EUNSUPPORTED: "EUNSUPPORTED", FQA_ELAUNCH: "ELAUNCH",
+                 FQA_ENOSPACE: "ENOSPACE"}
         raise FqaError(f"{what} failed: {names.get(rc, rc)}")

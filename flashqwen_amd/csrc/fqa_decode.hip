@@ -262,6 +262,60 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
   }
 }
 
+// The HBM read floor of a decode plan: the same wavefront grid walks the same shares of
+// the same (page, kv head) runs with the same per-lane loads as decode_split_kernel, but
+// does no arithmetic beyond folding the loaded words into one value per lane.  Four
+// pages are always in flight per wave (past the end of a stream the last page is read
+// again).  The time of this kernel is what reading the decode's bytes in its access
+// pattern costs on the device; decode_split_kernel's time over it is the price of the
+// attention math and the bookkeeping.  `a.ws_m` receives one word per lane (the sink).
+__global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_read_floor_kernel(DecArgs a) {
+  const int w = blockIdx.x * kDecWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (w >= a.meta[FQA_META_DEC_WAVES]) return;
+  const int lane = threadIdx.x & 63;
+  const int4 desc = *reinterpret_cast<const int4*>(a.waves + 8 * (long long)w);
+  int di = __builtin_amdgcn_readfirstlane(desc.x), kvh = __builtin_amdgcn_readfirstlane(desc.y);
+  int page = __builtin_amdgcn_readfirstlane(desc.z), left = __builtin_amdgcn_readfirstlane(desc.w);
+  const uint32_t pool32 = (uint32_t)min(a.pool_pages, (long long)0x7fffffff);
+  uint32_t sink = 0;
+  while (left > 0) {
+    const int4 sq = *reinterpret_cast<const int4*>(a.seqs + 4 * (long long)di);
+    const int r = __builtin_amdgcn_readfirstlane(sq.x), L = __builtin_amdgcn_readfirstlane(sq.z);
+    const int pages = (L + kPage - 1) / kPage;
+    const int cnt = min(pages - page, left);
+    const __attribute__((address_space(4))) int32_t* btc =
+        (const __attribute__((address_space(4))) int32_t*)(a.bt + (long long)r * a.max_blocks);
+    for (int p = page; p < page + cnt; p += 4) {
+      PageFrag f[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int id = btc[min(p + i, page + cnt - 1)];
+        load_page(f[i], a.pool + run_offset((uint32_t)id < pool32 ? id : 0, kvh), lane);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const uint4 k = __builtin_bit_cast(uint4, f[i].k[ks]);
+          sink ^= k.x ^ k.y ^ k.z ^ k.w;
+        }
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+          const uint2 v = __builtin_bit_cast(uint2, f[i].v[b]);
+          sink ^= v.x ^ v.y;
+        }
+      }
+    }
+    left -= cnt;
+    page = 0;
+    if (++kvh == kHkv) {
+      kvh = 0;
+      ++di;
+    }
+  }
+  reinterpret_cast<uint32_t*>(a.ws_m)[(long long)w * kWave + lane] = sink;
+}
+
 // Log-sum-exp merge of a cut stream's partials (attn_cute.cu:225-238): one wave per
 // (decode sequence, kv head) stream, lane -> (head = lane/16, 8 dims).  The shares that
 // cut stream s = [S0, S1) are w_first..w_last (share w = [w*W/G, (w+1)*W/G)); the
@@ -355,6 +409,20 @@ int fqa_decode(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
   const int waves2 = n_reqs_bound * kHkv;
   hipLaunchKernelGGL(decode_combine_kernel,
                      dim3((waves2 + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
+                     dim3(kDecWavesPerBlock * kWave), 0, (hipStream_t)stream, a);
+  return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
+}
+
+int fqa_decode_read_floor(const uint16_t* pool, int64_t pool_pages, const int32_t* block_tables,
+                          int32_t max_blocks, const int32_t* dec_waves, const int32_t* dec_seqs,
+                          const int32_t* meta, int32_t dec_wave_cap, void* sink, void* stream) {
+  if (dec_wave_cap < 0 || max_blocks < 1 || pool_pages < 1 || !meta) return FQA_EINVAL;
+  if (dec_wave_cap == 0) return FQA_OK;
+  if (!pool || !block_tables || !dec_waves || !dec_seqs || !sink) return FQA_EINVAL;
+  DecArgs a{nullptr, pool, pool_pages, block_tables, max_blocks, dec_waves, dec_seqs, meta,
+            static_cast<float*>(sink), nullptr, nullptr, nullptr, kQkvStride, 0.f};
+  hipLaunchKernelGGL(decode_read_floor_kernel,
+                     dim3((dec_wave_cap + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
                      dim3(kDecWavesPerBlock * kWave), 0, (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
 }

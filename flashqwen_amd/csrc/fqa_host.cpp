@@ -1,4 +1,6 @@
 // fqa_host.cpp — host-side helpers of the C ABI (no device work).
+#include <hip/hip_runtime_api.h>
+
 #include <cmath>
 
 #include "../../include/fqa.h"
@@ -27,6 +29,38 @@ int fqa_rope_tables(int32_t max_pos, int32_t head_dim, float theta, float* cos_t
 int64_t fqa_pool_bytes(const fqa_dims* dims, int64_t pages) {
   if (!dims || pages < 0) return FQA_EINVAL;
   return pages * dims->n_kv_heads * 2 * (int64_t)dims->page_size * dims->head_dim * 2;
+}
+
+// KvStore's pool sizing (kv_store.cu:10-33): the pool gets what is left of
+// total * fraction after `used` bytes, in whole blocks of layers x 2 x 16 x kv_dim bf16.
+// The product total * fraction is taken in float, as the reference's expression
+// `totalb * gpu_mem_fraction` (size_t times float) is, so the page count is the same.
+// Fewer pages than one max_ctx sequence needs is FQA_ENOSPACE (the reference throws).
+int fqa_pool_pages(const fqa_dims* dims, uint64_t total_bytes, uint64_t used_bytes,
+                   float fraction, int32_t layers, int32_t max_ctx, int64_t* pages) {
+  if (!dims || !pages || layers < 1 || max_ctx < 1 || !(fraction > 0.f) || fraction > 1.f ||
+      dims->page_size < 1 || dims->n_kv_heads < 1 || dims->head_dim < 1)
+    return FQA_EINVAL;
+  *pages = 0;
+  const uint64_t budget = static_cast<uint64_t>(static_cast<float>(total_bytes) * fraction);
+  const uint64_t avail = budget > used_bytes ? budget - used_bytes : 0;
+  const uint64_t per_block = static_cast<uint64_t>(layers) * 2 * dims->page_size *
+                             dims->n_kv_heads * dims->head_dim * 2;
+  const uint64_t n = avail / per_block;
+  const int64_t need = (max_ctx + dims->page_size - 1) / dims->page_size;
+  // the reference stores the count in an int; block ids here are int32 as well
+  *pages = n > 0x7fffffffULL ? 0x7fffffff : static_cast<int64_t>(n);
+  return *pages < need ? FQA_ENOSPACE : FQA_OK;
+}
+
+// The same sizing from the current device's hipMemGetInfo (what the reference's
+// constructor does with cudaMemGetInfo): used = total - free.
+int fqa_pool_pages_device(const fqa_dims* dims, float fraction, int32_t layers,
+                          int32_t max_ctx, int64_t* pages) {
+  if (!pages) return FQA_EINVAL;
+  size_t freeb = 0, totalb = 0;
+  if (hipMemGetInfo(&freeb, &totalb) != hipSuccess) return FQA_ELAUNCH;
+  return fqa_pool_pages(dims, totalb, totalb - freeb, fraction, layers, max_ctx, pages);
 }
 
 const char* fqa_version(void) { return "fqa 0.1 gfx950"; }

@@ -168,6 +168,14 @@ class AttnStep:
             _ptr(self.dec_seqs), _ptr(self.meta), self.dec_wave_cap, self.n_reqs_bound,
             _ptr(self.workspace), _ptr(out), self.stream), "fqa_decode")
 
+    def decode_read_floor(self, pool_layer):
+        """Read the decode plan's pages with fqa_decode's loads and no arithmetic (the HBM
+        floor of this plan); the sink is the decode workspace."""
+        check(self.lib.fqa_decode_read_floor(
+            _ptr(pool_layer), self.pool_pages, _ptr(self.block_tables), self.max_blocks,
+            _ptr(self.dec_waves), _ptr(self.dec_seqs), _ptr(self.meta), self.dec_wave_cap,
+            _ptr(self.workspace), self.stream), "fqa_decode_read_floor")
+
     def attn_prefill(self, qkv, pool_layer, out):
         """LaunchAttnPrefillCute: varlen causal FA-2."""
         check(self.lib.fqa_prefill(

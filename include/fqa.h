@@ -53,6 +53,7 @@ extern "C" {
 #define FQA_EINVAL (-1)       /* null pointer, negative size, size over a stated maximum */
 #define FQA_EUNSUPPORTED (-2) /* shape other than 32/8/128/16 */
 #define FQA_ELAUNCH (-3)      /* hipGetLastError() after a launch */
+#define FQA_ENOSPACE (-4)     /* fqa_pool_pages: the pool cannot hold one max_ctx sequence */
 
 #define FQA_PAGE_TOKENS 16
 #define FQA_MAX_REQS 2048 /* max requests in one step (reference: `slots`, args.h:13) */
@@ -159,6 +160,22 @@ int fqa_rope_tables(int32_t max_pos, int32_t head_dim, float theta, float* cos_t
 /* Bytes of one layer's pool for `pages` pages (replaces KvStore's per-block sizing,
  * kv_store.cu:24-26). */
 int64_t fqa_pool_bytes(const fqa_dims* dims, int64_t pages);
+
+/* Pages of a pool sized the way KvStore's constructor sizes it (kv_store.cu:10-33): the
+ * bytes left of total_bytes * fraction (the product taken in float, as the reference's
+ * `totalb * gpu_mem_fraction`) after used_bytes, in whole blocks of
+ * layers x 2 x page_size x n_kv_heads x head_dim bf16 (one block = one page of every
+ * layer).  *pages receives the count (capped at 2^31 - 1) in every case; the return is
+ * FQA_ENOSPACE when it is below ceil(max_ctx / page_size) (the reference throws), FQA_OK
+ * otherwise.  At Qwen3-8B's 36 layers one page costs 2.25 MiB, so a 288 GB device at
+ * fraction 0.9 with 20 GB used holds ~101k pages (1.6M tokens). */
+int fqa_pool_pages(const fqa_dims* dims, uint64_t total_bytes, uint64_t used_bytes,
+                   float fraction, int32_t layers, int32_t max_ctx, int64_t* pages);
+
+/* fqa_pool_pages with total and used bytes from the current device's hipMemGetInfo
+ * (used = total - free), as the reference's constructor reads cudaMemGetInfo. */
+int fqa_pool_pages_device(const fqa_dims* dims, float fraction, int32_t layers,
+                          int32_t max_ctx, int64_t* pages);
 
 /* Upper bounds for plan capacities and launch grids, from host-known sizes. */
 int32_t fqa_dec_wave_bound(int32_t n_reqs, int32_t dec_grid_waves);
@@ -305,6 +322,16 @@ int fqa_qkv_proj_append(const fqa_dims* dims, const uint16_t* x, int64_t ldx,
                         const int32_t* meta, uint16_t* pool, int64_t pool_pages,
                         int32_t write_k_inplace, void* workspace, int64_t workspace_bytes,
                         void* stream);
+
+/* The HBM read floor of a decode plan (a measurement aid, no counterpart in the
+ * reference): the same grid walks the same shares of the same (page, kv head) runs of
+ * fqa_pack's decode plan with fqa_decode's per-lane loads, but computes nothing; each
+ * lane folds its loaded words into one 32-bit value written to `sink`
+ * (dec_wave_cap x 64 x 4 bytes).  Its time bounds what fqa_decode can reach on that
+ * plan. */
+int fqa_decode_read_floor(const uint16_t* pool, int64_t pool_pages, const int32_t* block_tables,
+                          int32_t max_blocks, const int32_t* dec_waves, const int32_t* dec_seqs,
+                          const int32_t* meta, int32_t dec_wave_cap, void* sink, void* stream);
 
 /* Library version string. */
 const char* fqa_version(void);
