@@ -373,6 +373,34 @@ bool dims_ok(const fqa_dims* d) {
          d->page_size == kPage && d->qkv_stride >= kQkvStride && d->qkv_stride % 8 == 0;
 }
 
+// The checks and launches of fqa_decode with the partials in `ws` (fp32 m, l, acc for
+// 2 * dec_wave_cap * 4 head slots).
+int decode_launch(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
+                  int64_t pool_pages, const int32_t* block_tables, int32_t max_blocks,
+                  const int32_t* dec_waves, const int32_t* dec_seqs, const int32_t* meta,
+                  int32_t dec_wave_cap, int32_t n_reqs_bound, float* ws, uint16_t* out,
+                  hipStream_t stream) {
+  if (!dims) return FQA_EINVAL;
+  if (!dims_ok(dims)) return FQA_EUNSUPPORTED;
+  if (dec_wave_cap < 0 || n_reqs_bound < 0 || n_reqs_bound > FQA_MAX_REQS || max_blocks < 1 ||
+      pool_pages < 1 || !meta)
+    return FQA_EINVAL;
+  if (dec_wave_cap == 0 || n_reqs_bound == 0) return FQA_OK;
+  if (!qkv || !pool || !block_tables || !dec_waves || !dec_seqs || !ws || !out)
+    return FQA_EINVAL;
+  const long long slots = 2LL * dec_wave_cap * kG;
+  DecArgs a{qkv, pool, pool_pages, block_tables, max_blocks, dec_waves, dec_seqs, meta, ws,
+            ws + slots, ws + 2 * slots, out, dims->qkv_stride, dims->scale * kLog2e};
+  hipLaunchKernelGGL(decode_split_kernel<kDecBufs>,
+                     dim3((dec_wave_cap + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
+                     dim3(kDecWavesPerBlock * kWave), 0, stream, a);
+  const int waves2 = n_reqs_bound * kHkv;
+  hipLaunchKernelGGL(decode_combine_kernel,
+                     dim3((waves2 + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
+                     dim3(kDecWavesPerBlock * kWave), 0, stream, a);
+  return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
+}
+
 }  // namespace
 }  // namespace fqa
 
@@ -391,26 +419,9 @@ int fqa_decode(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
                const int32_t* dec_waves, const int32_t* dec_seqs, const int32_t* meta,
                int32_t dec_wave_cap, int32_t n_reqs_bound, void* workspace, uint16_t* out,
                void* stream) {
-  if (!dims) return FQA_EINVAL;
-  if (!dims_ok(dims)) return FQA_EUNSUPPORTED;
-  if (dec_wave_cap < 0 || n_reqs_bound < 0 || n_reqs_bound > FQA_MAX_REQS || max_blocks < 1 ||
-      pool_pages < 1 || !meta)
-    return FQA_EINVAL;
-  if (dec_wave_cap == 0 || n_reqs_bound == 0) return FQA_OK;
-  if (!qkv || !pool || !block_tables || !dec_waves || !dec_seqs || !workspace || !out)
-    return FQA_EINVAL;
-  const long long slots = 2LL * dec_wave_cap * kG;
-  float* ws = static_cast<float*>(workspace);
-  DecArgs a{qkv, pool, pool_pages, block_tables, max_blocks, dec_waves, dec_seqs, meta, ws,
-            ws + slots, ws + 2 * slots, out, dims->qkv_stride, dims->scale * kLog2e};
-  hipLaunchKernelGGL(decode_split_kernel<kDecBufs>,
-                     dim3((dec_wave_cap + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
-                     dim3(kDecWavesPerBlock * kWave), 0, (hipStream_t)stream, a);
-  const int waves2 = n_reqs_bound * kHkv;
-  hipLaunchKernelGGL(decode_combine_kernel,
-                     dim3((waves2 + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
-                     dim3(kDecWavesPerBlock * kWave), 0, (hipStream_t)stream, a);
-  return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
+  return decode_launch(dims, qkv, pool, pool_pages, block_tables, max_blocks, dec_waves,
+                       dec_seqs, meta, dec_wave_cap, n_reqs_bound,
+                       static_cast<float*>(workspace), out, (hipStream_t)stream);
 }
 
 int fqa_decode_read_floor(const uint16_t* pool, int64_t pool_pages, const int32_t* block_tables,
