@@ -17,6 +17,7 @@ FQA_ELAUNCH = -3
 FQA_ENOSPACE = -4
 FQA_PAGE_TOKENS = 16
 FQA_MAX_REQS = 2048
+FQA_DECODE_NOALLOC_MAX_WAVES = 4096
 
 META_ROWS, META_N_DECODE, META_N_PREFILL, META_MAX_QLEN = 0, 1, 2, 3
 META_DEC_WAVES, META_PRE_ITEMS, META_DEC_WAVE_PAGES, META_STATUS = 4, 5, 6, 7
@@ -105,6 +106,10 @@ SIGNATURES = {
     "fqa_decode": (
         C.c_int,
         [C.POINTER(FqaDims), P, P, I64, P, I32, P, P, P, I32, I32, P, P, P],
+    ),
+    "fqa_decode_noalloc": (
+        C.c_int,
+        [C.POINTER(FqaDims), P, P, I64, P, I32, P, P, P, I32, I32, P, P],
     ),
     "fqa_prefill": (
         C.c_int,

@@ -30,6 +30,8 @@
 //  * Pages rotate through four register buffers: while page p is processed the loads of
 //    p+1..p+3 are in flight, 24 KiB per wave (HBM latency x bandwidth needs ~64 KiB in
 //    flight per CU; at 2 waves per SIMD this gives ~190 KiB).
+#include <mutex>
+
 #include "fqa_common.h"
 
 namespace fqa {
@@ -401,6 +403,37 @@ int decode_launch(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* poo
   return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
 }
 
+
+// ---- fqa_decode_noalloc: the decode partials in a file-scope device array ----------
+// Callers that cannot allocate (graph capture, serving loops that forbid hipMalloc) get
+// the partials in `scratch`, sized for FQA_DECODE_NOALLOC_MAX_WAVES wavefronts
+// (17,039,360 bytes), which every device the library runs on holds until the process
+// ends.  Host code never passes `scratch` itself (in host code the name is a stand-in,
+// not a device address): its device address is looked up once per device with
+// hipGetSymbolAddress and kept in scratch_ptr[].  The split kernel writes every partial
+// slot the combine reads in the same call, so nothing has to start at zero.
+constexpr size_t kScratchBytes =
+    2ull * FQA_DECODE_NOALLOC_MAX_WAVES * kG * (2 + kD) * sizeof(float);
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up on its first use on the device.
+int scratch_address(float** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return FQA_ELAUNCH;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return FQA_ELAUNCH;
+    scratch_ptr[dev] = p;
+  }
+  *out = static_cast<float*>(scratch_ptr[dev]);
+  return FQA_OK;
+}
+
 }  // namespace
 }  // namespace fqa
 
@@ -422,6 +455,21 @@ int fqa_decode(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
   return decode_launch(dims, qkv, pool, pool_pages, block_tables, max_blocks, dec_waves,
                        dec_seqs, meta, dec_wave_cap, n_reqs_bound,
                        static_cast<float*>(workspace), out, (hipStream_t)stream);
+}
+
+int fqa_decode_noalloc(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
+                       int64_t pool_pages, const int32_t* block_tables, int32_t max_blocks,
+                       const int32_t* dec_waves, const int32_t* dec_seqs, const int32_t* meta,
+                       int32_t dec_wave_cap, int32_t n_reqs_bound, uint16_t* out,
+                       void* stream) {
+  if (dec_wave_cap > FQA_DECODE_NOALLOC_MAX_WAVES) return FQA_EINVAL;
+  float* ws = nullptr;
+  if (dec_wave_cap > 0 && n_reqs_bound > 0) {
+    const int rc = scratch_address(&ws);
+    if (rc != FQA_OK) return rc;
+  }
+  return decode_launch(dims, qkv, pool, pool_pages, block_tables, max_blocks, dec_waves,
+                       dec_seqs, meta, dec_wave_cap, n_reqs_bound, ws, out, (hipStream_t)stream);
 }
 
 int fqa_decode_read_floor(const uint16_t* pool, int64_t pool_pages, const int32_t* block_tables,

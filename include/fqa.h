@@ -244,6 +244,22 @@ int fqa_decode(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
                int32_t dec_wave_cap, int32_t n_reqs_bound, void* workspace, uint16_t* out,
                void* stream);
 
+/* fqa_decode without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops and harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  The partials live in a fixed device array of the library
+ * (17,039,360 bytes per device, held until the process ends); dec_wave_cap above
+ * FQA_DECODE_NOALLOC_MAX_WAVES is FQA_EINVAL.  The array's device address is looked up
+ * on the first call on each device (hipGetSymbolAddress); no call allocates or frees.
+ * Every call on one device shares that device's array: calls that overlap in time on one
+ * device (different streams, or different host threads) race and must be serialised by
+ * the caller.  Results are bit-identical to fqa_decode's. */
+#define FQA_DECODE_NOALLOC_MAX_WAVES 4096
+int fqa_decode_noalloc(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
+                       int64_t pool_pages, const int32_t* block_tables, int32_t max_blocks,
+                       const int32_t* dec_waves, const int32_t* dec_seqs, const int32_t* meta,
+                       int32_t dec_wave_cap, int32_t n_reqs_bound, uint16_t* out,
+                       void* stream);
+
 /* Varlen causal FlashAttention-2 prefill on bf16 MFMA over the pack's prefill plan:
  * one workgroup per (query tile, kv head) computes all 4 query heads of the kv head
  * from one LDS-staged copy of each K/V tile.  Mask: key pos <= query pos (cached
