@@ -103,6 +103,8 @@ SIGNATURES = {
         C.c_int,
         [C.POINTER(FqaDims), P, P, P, P, P, I32, P, P, P, I32, P, I64, I32, P],
     ),
+    "fqa_qknorm_rope": (C.c_int, [C.POINTER(FqaDims), P, P, P, P, P, I32, P, P, I32, P]),
+    "fqa_store_kv": (C.c_int, [C.POINTER(FqaDims), P, P, P, P, I32, P, I64, P]),
     "fqa_decode": (
         C.c_int,
         [C.POINTER(FqaDims), P, P, I64, P, I32, P, P, P, I32, I32, P, P, P],

@@ -95,6 +95,17 @@ def build_decode_loop_driver() -> Path:
     return exe
 
 
+def build_compat_driver() -> Path:
+    """tests/cpp/compat_cpp: the reference's RunLayersBody attention calls, compiled against
+    include/fqa_compat.hpp (the reference's Launch* signatures)."""
+    root = PKG.parent
+    src = root / "tests" / "cpp" / "compat_cpp.cpp"
+    exe = src.with_suffix("")
+    _run([HIPCC, "-O2", "-std=c++17", "-Wall", "-o", str(exe), str(src), f"-L{PKG}", "-lfqa",
+          "-Wl,-rpath,$ORIGIN/../../flashqwen_amd"])
+    return exe
+
+
 def build_sched_driver() -> Path:
     """tests/cpp/sched_cpp: a host program driving include/fqa_sched.hpp (no HIP)."""
     root = PKG.parent

@@ -103,7 +103,12 @@ __device__ __forceinline__ void unpack4(uint2 v, float* f) {
   f[3] = __uint_as_float(v.y & 0xffff0000u);
 }
 
-template <int HPG, bool kPart>
+// What the kernel does with a row (kMode): the fused norm + RoPE + append; the norm + RoPE
+// alone (q and k in place, nothing appended: LaunchHeadNormRope); or the append alone of
+// the row's k and v as they are in qkv (KvStore::StoreKV).
+enum { kFused = 0, kNormOnly = 1, kStoreOnly = 2 };
+
+template <int HPG, bool kPart, int kMode = kFused>
 __global__ void __launch_bounds__(256) qknorm_rope_append_kernel(AppendArgs a) {
   constexpr int W = 10 / HPG;                  // waves per row
   constexpr int NKV = (kHkv + W - 1) / W;      // v heads per wave
@@ -116,7 +121,7 @@ __global__ void __launch_bounds__(256) qknorm_rope_append_kernel(AppendArgs a) {
   const int pos = a.positions[row];
   const bool pos_ok = pos >= 0 && pos < a.rope_max_pos;
   if (!kPart && !pos_ok) return;  // no table row: leave the row untouched
-  const int slot = a.slots[row];
+  const int slot = kMode == kNormOnly ? -1 : a.slots[row];
   const long long page = slot / kPage;
   const bool page_ok = slot >= 0 && page < a.pool_pages;
   const int tok = slot % kPage;
@@ -128,6 +133,7 @@ __global__ void __launch_bounds__(256) qknorm_rope_append_kernel(AppendArgs a) {
 #pragma unroll
   for (int i = 0; i < HPG; ++i) {
     const int col = (g + 4 * (sw * HPG + i)) * kD;
+    if (kMode == kStoreOnly && col < kHq * kD) continue;  // q heads: not stored
     lo[i] = load4<kPart>(a, row, col + 4 * j);
     hi[i] = load4<kPart>(a, row, col + 64 + 4 * j);
   }
@@ -141,6 +147,16 @@ __global__ void __launch_bounds__(256) qknorm_rope_append_kernel(AppendArgs a) {
     }
     return;
   }
+  if constexpr (kMode == kStoreOnly) {
+#pragma unroll
+    for (int i = 0; i < HPG; ++i) {
+      const int head = g + 4 * (sw * HPG + i);
+      if (head < kHq || !page_ok) continue;
+      uint16_t* kd = a.pool + run_offset(page, head - kHq) + tok * kD;
+      *reinterpret_cast<uint2*>(kd + 4 * j) = lo[i];
+      *reinterpret_cast<uint2*>(kd + 64 + 4 * j) = hi[i];
+    }
+  } else {
   const float4 c4 = *reinterpret_cast<const float4*>(a.cos_tab + (long long)pos * 64 + 4 * j);
   const float4 s4 = *reinterpret_cast<const float4*>(a.sin_tab + (long long)pos * 64 + 4 * j);
   const float4 q1 = *reinterpret_cast<const float4*>(a.wq + 4 * j);
@@ -186,6 +202,8 @@ __global__ void __launch_bounds__(256) qknorm_rope_append_kernel(AppendArgs a) {
       *reinterpret_cast<uint2*>(kd + 64 + 4 * j) = ohi;
     }
   }
+  }  // kMode != kStoreOnly
+  if constexpr (kMode == kNormOnly) return;
 
   // ---- v ------------------------------------------------------------------------------
   if (!page_ok) return;
@@ -245,15 +263,15 @@ bool dims_ok(const fqa_dims* d) {
          d->page_size == kPage && d->qkv_stride >= kQkvStride && d->qkv_stride % 4 == 0;
 }
 
-template <bool kPart>
+template <bool kPart, int kMode = kFused>
 void launch_append(const AppendArgs& a, int hpg, dim3 grid, hipStream_t st) {
   const dim3 block(256);
   if (hpg == 1)
-    hipLaunchKernelGGL((qknorm_rope_append_kernel<1, kPart>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((qknorm_rope_append_kernel<1, kPart, kMode>), grid, block, 0, st, a);
   else if (hpg == 2)
-    hipLaunchKernelGGL((qknorm_rope_append_kernel<2, kPart>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((qknorm_rope_append_kernel<2, kPart, kMode>), grid, block, 0, st, a);
   else
-    hipLaunchKernelGGL((qknorm_rope_append_kernel<10, kPart>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((qknorm_rope_append_kernel<10, kPart, kMode>), grid, block, 0, st, a);
 }
 
 // Validates the append arguments and launches the append kernel (kPart: reading the
@@ -263,13 +281,14 @@ int append_launch(const fqa_dims* dims, uint16_t* qkv, const float* q_norm_w,
                   int32_t rope_max_pos, const int32_t* positions, const int32_t* slot_mapping,
                   const int32_t* meta, int32_t rows_bound, uint16_t* pool, int64_t pool_pages,
                   int32_t write_k_inplace, const float* part, int splits, int part_rows,
-                  hipStream_t st) {
+                  hipStream_t st, int mode = kFused) {
   if (!dims) return FQA_EINVAL;
   if (!dims_ok(dims)) return FQA_EUNSUPPORTED;
   if (rows_bound < 0 || pool_pages < 1 || rope_max_pos < 1 || !meta) return FQA_EINVAL;
   if (rows_bound == 0) return FQA_OK;
-  if (!qkv || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !positions || !slot_mapping ||
-      !pool)
+  const bool norm = mode != kStoreOnly, store = mode != kNormOnly;
+  if (!qkv || !positions || (norm && (!q_norm_w || !k_norm_w || !cos_tab || !sin_tab)) ||
+      (store && (!slot_mapping || !pool)))
     return FQA_EINVAL;
   // Heads per lane group: 1 (10 waves per row) for decode-sized steps, 10 (one wave per
   // row) for prefill-sized ones; measured crossover between.
@@ -284,6 +303,10 @@ int append_launch(const fqa_dims* dims, uint16_t* qkv, const float* q_norm_w,
   const dim3 grid(8 * blocks_per_xcd);
   if (part)
     launch_append<true>(a, hpg, grid, st);
+  else if (mode == kNormOnly)
+    launch_append<false, kNormOnly>(a, hpg, grid, st);
+  else if (mode == kStoreOnly)
+    launch_append<false, kStoreOnly>(a, hpg, grid, st);
   else
     launch_append<false>(a, hpg, grid, st);
   return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
@@ -304,6 +327,24 @@ extern "C" int fqa_qknorm_rope_append(const fqa_dims* dims, uint16_t* qkv, const
   return append_launch(dims, qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, rope_max_pos, positions,
                        slot_mapping, meta, rows_bound, pool, pool_pages, write_k_inplace, nullptr,
                        1, 0, (hipStream_t)stream);
+}
+
+extern "C" int fqa_qknorm_rope(const fqa_dims* dims, uint16_t* qkv, const float* q_norm_w,
+                               const float* k_norm_w, const float* cos_tab, const float* sin_tab,
+                               int32_t rope_max_pos, const int32_t* positions,
+                               const int32_t* meta, int32_t rows_bound, void* stream) {
+  return append_launch(dims, qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, rope_max_pos, positions,
+                       nullptr, meta, rows_bound, nullptr, 1, 1, nullptr, 1, 0,
+                       (hipStream_t)stream, kNormOnly);
+}
+
+extern "C" int fqa_store_kv(const fqa_dims* dims, const uint16_t* qkv, const int32_t* positions,
+                            const int32_t* slot_mapping, const int32_t* meta, int32_t rows_bound,
+                            uint16_t* pool, int64_t pool_pages, void* stream) {
+  // The kernel reads qkv only in this mode (q and k are not written back).
+  return append_launch(dims, const_cast<uint16_t*>(qkv), nullptr, nullptr, nullptr, nullptr,
+                       0x7fffffff, positions, slot_mapping, meta, rows_bound, pool, pool_pages,
+                       0, nullptr, 1, 0, (hipStream_t)stream, kStoreOnly);
 }
 
 extern "C" int fqa_qkv_proj_append(const fqa_dims* dims, const uint16_t* x, int64_t ldx,

@@ -10,9 +10,12 @@
  *                              SplitDecodePrefill                             (model_runtime.cu:47-91, 295-302)
  *   fqa_rope_tables         <- RopeTables::Build                              (model_runtime.cu:111-126)
  *   fqa_qknorm_rope_append  <- LaunchHeadNormRope + KvStore::StoreKV          (kernels.cu:97-139, kv_store.cu:48-75)
+ *   fqa_qknorm_rope         <- LaunchHeadNormRope alone                       (kernels.cu:97-139)
+ *   fqa_store_kv            <- KvStore::StoreKV alone                         (kv_store.cu:48-75)
  *   fqa_decode              <- LaunchAttnDecodeCute (split + combine)         (attn_cute.cu:165-261)
  *   fqa_prefill             <- LaunchAttnPrefillCute                          (attn_cute.cu:30-163)
- *   fqa_pool_bytes          <- KvStore pool sizing                            (kv_store.cu:10-46)
+ *   fqa_pool_bytes, fqa_pool_pages(_device)
+ *                           <- KvStore pool sizing                            (kv_store.cu:10-46)
  *   fqa_sample              <- LaunchSampleBatch (greedy / temperature + top-p) (kernels.cu:184-327)
  *   fqa_gemm                <- LaunchGemm (QKV, o_proj, gate-up, down, lm_head) (kernels.cu:9-16)
  *   fqa_qkv_proj_append     <- LaunchGemm(QKV) + LaunchHeadNormRope + StoreKV (model_runtime.cu:261-268)
@@ -229,6 +232,25 @@ int fqa_qknorm_rope_append(const fqa_dims* dims, uint16_t* qkv, const float* q_n
                            int32_t rope_max_pos, const int32_t* positions, const int32_t* slot_mapping,
                            const int32_t* meta, int32_t rows_bound, uint16_t* pool,
                            int64_t pool_pages, int32_t write_k_inplace, void* stream);
+
+/* The two halves of fqa_qknorm_rope_append as separate launches, for callers that keep the
+ * reference's two calls (LaunchHeadNormRope, kernels.cu:133-139, decl. kernels.cuh:28-31;
+ * KvStore::StoreKV, kv_store.cu:66-75, decl. kv_store.h:29-31).
+ * fqa_qknorm_rope: the norm + RoPE of the q and k heads of each row, written back in place
+ * into qkv (q and k, as the reference leaves them); nothing is appended.  Rows whose
+ * position is outside [0, rope_max_pos) are left untouched.
+ * fqa_store_kv: the paged append of each row's k and v exactly as they are in qkv (k
+ * normalised by fqa_qknorm_rope before, as the reference's order has it) at
+ * slot_mapping[t]; qkv is only read.  Rows with a negative position or a slot outside
+ * the pool append nothing.  Running the two in this order leaves qkv and the pool exactly
+ * as fqa_qknorm_rope_append with write_k_inplace = 1 does. */
+int fqa_qknorm_rope(const fqa_dims* dims, uint16_t* qkv, const float* q_norm_w,
+                    const float* k_norm_w, const float* cos_tab, const float* sin_tab,
+                    int32_t rope_max_pos, const int32_t* positions, const int32_t* meta,
+                    int32_t rows_bound, void* stream);
+int fqa_store_kv(const fqa_dims* dims, const uint16_t* qkv, const int32_t* positions,
+                 const int32_t* slot_mapping, const int32_t* meta, int32_t rows_bound,
+                 uint16_t* pool, int64_t pool_pages, void* stream);
 
 /* GQA-shared split-K flash decoding over the pack's stream-K decode plan: wavefront w
  * streams its share of page runs; each (page, kv head) run is read once for all 4 query
