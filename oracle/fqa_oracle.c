@@ -288,7 +288,8 @@ void fqo_qknorm_rope_append(int n_q, int n_kv, int D, int stride, float eps, uin
     int64_t slot = slot_mapping[t];
     int64_t page = slot / PAGE;
     int tok = (int)(slot % PAGE);
-    int page_ok = page >= 0 && page < pool_pages;
+    /* slot >= 0: C division truncates, so slots -15..-1 would give page 0 */
+    int page_ok = slot >= 0 && page < pool_pages;
     for (int g = 0; g < n_q + n_kv; ++g) {
       uint16_t* v = qkv + (int64_t)t * stride + (int64_t)g * D;
       const float* w = g < n_q ? wq : wk;

@@ -5,8 +5,11 @@
 // layer's decode on a parallel branch (StepGraph's side stream).  For
 // tests/test_gpu_graph.py.
 //
-// argv: script norm_weights;  script as tests/cpp/serve_cpp.cpp.  Prints
-// "steps S layers L compared N mismatched M" and exits 0 iff M == 0.
+// argv: script norm_weights [out];  script as tests/cpp/serve_cpp.cpp.  Prints
+// "steps S layers L compared N mismatched M" and exits 0 iff M == 0.  With `out`, the
+// graph run's steps are written for the oracle check (little-endian, per step):
+//   int32 t, R, T; computed[R], n_new[R], bt_off[R+1], bt_pages[bt_off[R]];
+//   per layer: uint16 qkv[T*6144] (the step's input), uint16 attn[T*4096]; int32 meta[16]
 #include <cstdio>
 #include <cstring>
 #include <fstream>
@@ -35,7 +38,9 @@ struct Spec {
 };
 
 int main(int argc, char** argv) {
-  if (argc != 3) return 2;
+  if (argc != 3 && argc != 4) return 2;
+  FILE* dump = argc == 4 ? std::fopen(argv[3], "wb") : nullptr;
+  if (argc == 4 && !dump) return 2;
   std::ifstream in(argv[1]);
   int n_blocks, n_slots, budget, chunk, use_cache, n_steps, n_seqs;
   in >> n_blocks >> n_slots >> budget >> chunk >> use_cache >> n_steps >> n_seqs;
@@ -111,8 +116,10 @@ int main(int argc, char** argv) {
         fqa::SchedBatch b;
         if (!sched.BuildBatch(b)) continue;
         const int T = b.rows;
+        std::vector<std::vector<uint16_t>> inputs(kLayers);
         for (int l = 0; l < kLayers; ++l) {  // the step's inputs, outside any graph
-          std::vector<uint16_t> h((size_t)T * 6144);
+          std::vector<uint16_t>& h = inputs[l];
+          h.resize((size_t)T * 6144);
           for (int row = 0; row < T; ++row)
             for (int c = 0; c < 6144; ++c) {
               const uint64_t x = mix(((uint64_t)t << 44) ^ ((uint64_t)l << 40) ^
@@ -120,7 +127,7 @@ int main(int argc, char** argv) {
               h[(size_t)row * 6144 + c] = bf16_of((float)(x >> 40) * (4.0f / 16777216.0f) - 2.0f);
             }
           qkv[l].Upload(h.data(), h.size(), s);
-          fqa::HipCheck(hipStreamSynchronize(s), "sync");  // h goes out of scope
+          fqa::HipCheck(hipStreamSynchronize(s), "sync");
         }
         fqa::BatchInput bi{b.computed, b.n_new, b.block_tables};
         if (mode == 0) {
@@ -130,11 +137,29 @@ int main(int argc, char** argv) {
           ctx.UploadBatch(bi, s);
           graph->Launch(s);
         }
+        if (mode == 1 && dump) {
+          const int R = (int)b.computed.size();
+          std::vector<int32_t> off(R + 1, 0), pages;
+          for (int r = 0; r < R; ++r) {
+            pages.insert(pages.end(), b.block_tables[r].begin(), b.block_tables[r].end());
+            off[r + 1] = (int32_t)pages.size();
+          }
+          const int32_t hdr[3] = {t, R, T};
+          std::fwrite(hdr, 4, 3, dump);
+          std::fwrite(b.computed.data(), 4, R, dump);
+          std::fwrite(b.n_new.data(), 4, R, dump);
+          std::fwrite(off.data(), 4, R + 1, dump);
+          std::fwrite(pages.data(), 4, pages.size(), dump);
+        }
         for (int l = 0; l < kLayers; ++l) {
           std::vector<uint16_t> h((size_t)T * 4096);
           fqa::HipCheck(hipMemcpyAsync(h.data(), out[l].D(), h.size() * 2, hipMemcpyDeviceToHost,
                                        s), "d2h");
           fqa::HipCheck(hipStreamSynchronize(s), "sync");
+          if (mode == 1 && dump) {
+            std::fwrite(inputs[l].data(), 2, inputs[l].size(), dump);
+            std::fwrite(h.data(), 2, h.size(), dump);
+          }
           if (mode == 0) {
             eager_out.push_back(std::move(h));
           } else {
@@ -144,6 +169,11 @@ int main(int argc, char** argv) {
               ++mismatched;
           }
           ++k;
+        }
+        if (mode == 1 && dump) {
+          int32_t meta[16];
+          fqa::HipCheck(hipMemcpy(meta, ctx.Meta(), 64, hipMemcpyDeviceToHost), "meta");
+          std::fwrite(meta, 4, 16, dump);
         }
         std::vector<int32_t> sampled;
         for (int si : b.sample_seqs)
@@ -172,6 +202,7 @@ int main(int argc, char** argv) {
     std::fprintf(stderr, "graph_cpp: %s\n", e.what());
     return 1;
   }
+  if (dump) std::fclose(dump);
   std::printf("steps %d layers %d compared %lld mismatched %lld\n", steps_run, kLayers, compared,
               mismatched);
   return mismatched == 0 ? 0 : 3;

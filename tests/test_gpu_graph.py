@@ -3,7 +3,8 @@ StepGraph, the reference's GraphCache): one graph, captured once, replayed for e
 batch of a scheduler-driven workload over 3 layers (prefills, decodes, preemption, so the
 batch shape changes from step to step), with uploads and synchronisation between the
 replays.  Every step's attention output and the final pools must be bit-identical to the
-eager run of the same workload (tests/cpp/graph_cpp)."""
+eager run of the same workload (tests/cpp/graph_cpp), and every replay's output of every
+layer is checked against the CPU oracle replaying the same steps on its own pools."""
 from __future__ import annotations
 
 import subprocess
@@ -13,6 +14,7 @@ import numpy as np
 import pytest
 
 from flashqwen_amd import synth
+from tests import stepcase as sc
 from tests.test_sched import _script
 
 EXE = Path(__file__).resolve().parent / "cpp" / "graph_cpp"
@@ -34,9 +36,46 @@ def test_step_graph_replays_match_eager(gpu, tmp_path):
     wq, wk = synth.norm_weights()
     np.concatenate([wq.astype(np.float32), wk.astype(np.float32)]).tofile(tmp_path / "w.bin")
     print("[test_step_graph_replays_match_eager] 10 seqs, 16 steps, 3 layers", flush=True)
-    r = subprocess.run([str(EXE), str(tmp_path / "s.txt"), str(tmp_path / "w.bin")],
-                       capture_output=True, text=True, timeout=120)
+    r = subprocess.run([str(EXE), str(tmp_path / "s.txt"), str(tmp_path / "w.bin"),
+                        str(tmp_path / "graph.bin")], capture_output=True, text=True, timeout=120)
     print(r.stdout.strip(), r.stderr.strip())
     assert r.returncode == 0, (r.returncode, r.stdout, r.stderr)
     steps = int(r.stdout.split()[1])
     assert steps >= 10
+
+    # the captured path against the oracle: every replay, every layer
+    layers, n_blocks, budget, slots = 3, 20, 96, 6
+    raw = np.fromfile(tmp_path / "graph.bin", np.uint8)
+    o = 0
+
+    def take(dtype, n):
+        nonlocal o
+        a = raw[o:o + n * np.dtype(dtype).itemsize].view(dtype)
+        o += n * np.dtype(dtype).itemsize
+        return a
+
+    pools = [np.zeros(sc.pool_elems(n_blocks), np.uint16) for _ in range(layers)]
+    n_checked = 0
+    while o < raw.size:
+        t, R, T = (int(x) for x in take(np.int32, 3))
+        computed, n_new = take(np.int32, R), take(np.int32, R)
+        off = take(np.int32, R + 1)
+        pages = take(np.int32, int(off[-1]))
+        per_layer = [(take(np.uint16, T * synth.QKV_STRIDE).reshape(T, -1),
+                      take(np.uint16, T * 4096).reshape(T, -1)) for _ in range(layers)]
+        meta = take(np.int32, 16)
+        tables = [pages[off[i]:off[i + 1]] for i in range(R)]
+        cfg = synth._assemble(f"step{t}", computed, n_new, tables, n_blocks, 512)
+        kw = sc.pack_kwargs(cfg, max_rows=budget, dec_grid_waves=int(meta[4]) or 1,
+                            dec_min_pages=8, max_reqs=slots)
+        for l, (qkv_in, attn) in enumerate(per_layer):
+            ref = sc.oracle_chain(cfg, qkv_in, pools[l], wq, wk, kw)
+            if l == 0:
+                assert meta[:4].tolist() == ref["pack"]["meta"][:4].tolist(), t
+                assert meta[7] == 0
+            mx, mean = sc.att_errors(attn, ref["out"])
+            assert mx <= sc.ATT_MAX_ABS and mean <= sc.ATT_MEAN_ABS, (t, l, mx, mean)
+            pools[l] = ref["pool"]
+            n_checked += 1
+        print(f"graph step {t}: R={R} T={T} checked {layers} layers (last max-abs {mx:.2e})")
+    assert n_checked == steps * layers

@@ -153,12 +153,14 @@ def test_append_placement_and_bounds():
     cos, sin = orc.rope_tables(64)
     qkv, wq, wk, pos, slots, pool, pp = _norm_case(rows=5, positions=[1, 2, 3, 63, 64])
     slots[2] = pp * PAGE + 3  # page out of range: nothing written for this row
+    slots[1] = -16 + 11  # page id -1, token 11: negative slot, nothing written (C division
+    # truncates -5 / 16 to page 0; a slot test, not a page test, must reject it)
     q = qkv.copy()
     orc.qknorm_rope_append(q, wq, wk, cos, sin, pos, slots, 5, pool, pp, write_k=True)
     # row 4 has no table row (pos 64 >= 64): untouched
     assert np.array_equal(q[4], qkv[4])
     written = set()
-    for t in (0, 1, 3):
+    for t in (0, 3):
         pg, tk = int(slots[t] // PAGE), int(slots[t] % PAGE)
         for kvh in range(N_KV):
             for d in range(HEAD_DIM):
