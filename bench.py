@@ -431,7 +431,8 @@ def bench_gemm(args):
             del x, y
         del w
     # the QKV projection with the norm/RoPE/append fused (fqa_qkv_proj_append) against
-    # fqa_gemm + fqa_qknorm_rope_append, one decode row per sequence on its own page
+    # fqa_gemm + fqa_qknorm_rope_append: up to 256 rows one decode row per sequence on its
+    # own page, above that 512-token prompts on full pages
     import ctypes as C
 
     from flashqwen_amd import _lib
@@ -444,12 +445,18 @@ def bench_gemm(args):
     w = (torch.randn(N, K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
     qn = torch.ones(128, device="cuda")
     cos, sin = (torch.from_numpy(t).cuda() for t in rope_tables(4096))
-    for M in [r for r in rows if r <= 1024]:
+    for M in rows:
         x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
         qkv = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
         pool = alloc_pool(M + 16)[0]
-        pos = torch.arange(M, dtype=torch.int32, device="cuda") + 1000
-        slots = torch.arange(M, dtype=torch.int32, device="cuda") * 16 + 7
+        if M <= 256:  # decode rows: one row per sequence, each on its own page
+            pos = torch.arange(M, dtype=torch.int32, device="cuda") + 1000
+            slots = torch.arange(M, dtype=torch.int32, device="cuda") * 16 + 7
+        else:  # prefill rows: 512-token prompts on scattered full pages
+            r = torch.arange(M, dtype=torch.int32, device="cuda")
+            pos = r % 512
+            pages = torch.randperm(M + 16, generator=g, device="cuda")[: (M + 15) // 16]
+            slots = (pages[r // 16] * 16 + r % 16).to(torch.int32)
         meta = torch.zeros(16, dtype=torch.int32, device="cuda")
         meta[_lib.META_ROWS] = M
         nb = workspace_bytes(M, N, K)

@@ -59,6 +59,7 @@ struct DecArgs {
   uint16_t* out;
   int stride;
   float scale_log2;  // softmax scale * log2(e): scores live in the exp2 domain
+  int wave_cap;      // rows of `waves`
 };
 
 struct PageFrag {
@@ -193,16 +194,20 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
   // Everything a wave's loop indexes with is wave-uniform; readfirstlane says so, so that
   // block-table reads become scalar loads (see stream_pages).
   const int w = blockIdx.x * kDecWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (w >= a.meta[FQA_META_DEC_WAVES]) return;
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   auto uni4 = [](int4 v) {
     return make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
                      __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
   };
-  const int4 desc = uni4(*reinterpret_cast<const int4*>(a.waves + 8 * (long long)w));
-  // {r, row, L, page id}
-  int4 sq = uni4(reinterpret_cast<const int4*>(a.waves + 8 * (long long)w)[1]);
+  // The wave's descriptor is read together with the wave count (one round trip, not two):
+  // the row is in bounds for every wave of the grid, live or not.
+  const int4* wd = reinterpret_cast<const int4*>(a.waves + 8 * (long long)min(w, a.wave_cap - 1));
+  const int4 desc = uni4(wd[0]);
+  int4 sq = uni4(wd[1]);  // {r, row, L, page id}
+  const int n_waves = a.meta[FQA_META_DEC_WAVES];
+  asm volatile("" ::"s"(desc.x), "s"(n_waves));  // both loads issued before the branch
+  if (w >= n_waves) return;
   int di = desc.x, kvh = desc.y, page = desc.z, left = desc.w;
   for (int seg = 0; left > 0; ++seg) {
     if (seg > 0) {
@@ -273,9 +278,12 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
 // attention math and the bookkeeping.  `a.ws_m` receives one word per lane (the sink).
 __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_read_floor_kernel(DecArgs a) {
   const int w = blockIdx.x * kDecWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (w >= a.meta[FQA_META_DEC_WAVES]) return;
   const int lane = threadIdx.x & 63;
-  const int4 desc = *reinterpret_cast<const int4*>(a.waves + 8 * (long long)w);
+  const int4 desc =
+      *reinterpret_cast<const int4*>(a.waves + 8 * (long long)min(w, a.wave_cap - 1));
+  const int n_waves = a.meta[FQA_META_DEC_WAVES];
+  asm volatile("" ::"s"(desc.x), "s"(n_waves));  // one round trip, as decode_split_kernel
+  if (w >= n_waves) return;
   int di = __builtin_amdgcn_readfirstlane(desc.x), kvh = __builtin_amdgcn_readfirstlane(desc.y);
   int page = __builtin_amdgcn_readfirstlane(desc.z), left = __builtin_amdgcn_readfirstlane(desc.w);
   const uint32_t pool32 = (uint32_t)min(a.pool_pages, (long long)0x7fffffff);
@@ -326,10 +334,14 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_read_floor_k
 __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_combine_kernel(DecArgs a) {
   const int wave = blockIdx.x * kDecWavesPerBlock + (threadIdx.x >> 6);
   const int di = wave >> 3, kvh = wave & 7;
-  if (di >= a.meta[FQA_META_N_DECODE]) return;
+  // di < n_reqs_bound, the rows of `seqs`: the sequence is read with the counts (one round
+  // trip, not two)
+  const int4 sq = *reinterpret_cast<const int4*>(a.seqs + 4 * (long long)di);
+  const int n_dec = a.meta[FQA_META_N_DECODE];
+  asm volatile("" ::"v"(sq.x), "s"(n_dec));
+  if (di >= n_dec) return;
   const long long G = a.meta[FQA_META_DEC_WAVES];
   const long long W = 8LL * a.meta[FQA_META_DEC_PAGES];
-  const int4 sq = *reinterpret_cast<const int4*>(a.seqs + 4 * (long long)di);
   const int pages = (sq.z + kPage - 1) / kPage;
   const long long S0 = sq.w + (long long)kvh * pages, S1 = S0 + pages;
   const long long wf = ((S0 + 1) * G - 1) / W, wl = (S1 * G - 1) / W;
@@ -392,7 +404,7 @@ int decode_launch(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* poo
     return FQA_EINVAL;
   const long long slots = 2LL * dec_wave_cap * kG;
   DecArgs a{qkv, pool, pool_pages, block_tables, max_blocks, dec_waves, dec_seqs, meta, ws,
-            ws + slots, ws + 2 * slots, out, dims->qkv_stride, dims->scale * kLog2e};
+            ws + slots, ws + 2 * slots, out, dims->qkv_stride, dims->scale * kLog2e, dec_wave_cap};
   hipLaunchKernelGGL(decode_split_kernel<kDecBufs>,
                      dim3((dec_wave_cap + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
                      dim3(kDecWavesPerBlock * kWave), 0, stream, a);
@@ -479,7 +491,7 @@ int fqa_decode_read_floor(const uint16_t* pool, int64_t pool_pages, const int32_
   if (dec_wave_cap == 0) return FQA_OK;
   if (!pool || !block_tables || !dec_waves || !dec_seqs || !sink) return FQA_EINVAL;
   DecArgs a{nullptr, pool, pool_pages, block_tables, max_blocks, dec_waves, dec_seqs, meta,
-            static_cast<float*>(sink), nullptr, nullptr, nullptr, kQkvStride, 0.f};
+            static_cast<float*>(sink), nullptr, nullptr, nullptr, kQkvStride, 0.f, dec_wave_cap};
   hipLaunchKernelGGL(decode_read_floor_kernel,
                      dim3((dec_wave_cap + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
                      dim3(kDecWavesPerBlock * kWave), 0, (hipStream_t)stream, a);

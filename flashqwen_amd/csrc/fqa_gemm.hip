@@ -22,6 +22,7 @@
 //  * Workgroups are dealt to the 8 XCDs round robin; tile_of() renumbers them so that the
 //    workgroups on one XCD walk 8 m tiles per n tile and share W and x tiles in its L2.
 
+#include "fqa_append_math.h"
 #include "fqa_common.h"
 #include "fqa_gemm_internal.h"
 
@@ -73,6 +74,7 @@ struct GemmArgs {
   int m_tiles, n_tiles;
   float* amax_v;  // argmax mode: per (row, n tile) the tile's largest value and its column
   int* amax_i;
+  GemmAppend app;  // append mode: y is the qkv buffer (row stride ldy)
 };
 
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
@@ -123,9 +125,25 @@ __device__ __forceinline__ void tile_of(const GemmArgs& a, int& tm, int& tn, int
   tn = r / gs;
 }
 
-template <class T, bool kF32Out, bool kPartial, bool kArgmax = false>
+// Append mode: the bf16 output tile is staged in LDS with this row pitch (16 bytes of
+// padding rotate consecutive rows across the banks).
+template <class T>
+constexpr int kTilePitch = T::kBN * 2 + 16;
+// ... followed by the tile rows' positions and slots (int32 each)
+template <class T>
+constexpr int kAppendLds = T::kBM * kTilePitch<T> + T::kBM * 8;
+template <class T, bool kAppend>
+constexpr int kGemmLds = kAppend && kAppendLds<T> > T::kRing * T::kStage
+                             ? kAppendLds<T>
+                             : T::kRing * T::kStage;
+
+template <class T>
+__device__ void append_epilogue(const GemmArgs& a, char* lds, const float16_t (&acc)[T::kTM][T::kTN],
+                                int row0, int col0, int wm, int wn, int w, int lane);
+
+template <class T, bool kF32Out, bool kPartial, bool kArgmax = false, bool kAppend = false>
 __global__ void __launch_bounds__(T::kThreads, 1) gemm_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(1024))) char lds[T::kRing * T::kStage];
+  __shared__ __attribute__((aligned(1024))) char lds[kGemmLds<T, kAppend>];
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -238,6 +256,10 @@ __global__ void __launch_bounds__(T::kThreads, 1) gemm_kernel(GemmArgs a) {
     }
   }
 
+  if constexpr (kAppend) {
+    append_epilogue<T>(a, lds, acc, row0, col0, wm, wn, w, lane);
+    return;
+  }
   if constexpr (kArgmax) {
     // per row of the tile: the largest value and its column (the smallest on ties), over
     // this lane's values, then lane ^ 32 (the other column half of the same row), then
@@ -319,6 +341,165 @@ __global__ void __launch_bounds__(T::kThreads, 1) gemm_kernel(GemmArgs a) {
           *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.y) + m * a.ldy + n) =
               make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
       }
+  }
+}
+
+// The QKV projection's epilogue fused with the per-head norm + RoPE + paged append
+// (fqa_qknorm_rope_append on the tile's rows, same results bit for bit): the tile's
+// values are rounded to bf16 (what fqa_gemm would write) and staged in LDS, then
+//  * q / k tiles: one 16-lane group per (row, head) runs norm_rope_head on the row's
+//    head (the append kernel's lane layout and arithmetic), q goes to qkv, k to its page
+//    (and to qkv with write_k); rows without a RoPE table row keep the projection's values;
+//  * v tiles: a page whose 16 rows are all in the tile is written by its first row as
+//    whole V^T rows (a register transpose of the 16 staged rows); other rows store their
+//    token's column.
+// v is not written to qkv.  Rows at or past meta[FQA_META_ROWS] are not written.
+template <class T>
+__device__ void append_epilogue(const GemmArgs& a, char* lds, const float16_t (&acc)[T::kTM][T::kTN],
+                                int row0, int col0, int wm, int wn, int w, int lane) {
+  constexpr int kTP = kTilePitch<T>;
+  constexpr int kNH = T::kBN / kD;  // heads in the tile
+  const GemmAppend& p = a.app;
+  int* s_pos = reinterpret_cast<int*>(lds + T::kBM * kTP);
+  int* s_slot = s_pos + T::kBM;
+  const int T_rows = min(p.meta[FQA_META_ROWS], a.M);
+  // the rows' positions and slots, loaded while the tile goes to LDS (-1: no such row)
+  int my_pos = -1, my_slot = -1;
+  if (threadIdx.x < T::kBM && row0 + (int)threadIdx.x < T_rows) {
+    my_pos = p.positions[row0 + threadIdx.x];
+    my_slot = p.slots[row0 + threadIdx.x];
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's reads of the ring are done
+  barrier();                           // ... and every wave's: the LDS is free
+#pragma unroll
+  for (int rb = 0; rb < T::kTM; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < T::kTN; ++cb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = (wm * T::kTM + rb) * 32 + (lane & 31);
+        const int c = (wn * T::kTN + cb) * 32 + 8 * q + 4 * (lane >> 5);
+        *reinterpret_cast<uint2*>(lds + r * kTP + c * 2) =
+            make_uint2(pack_bf16x2(acc[rb][cb][4 * q], acc[rb][cb][4 * q + 1]),
+                       pack_bf16x2(acc[rb][cb][4 * q + 2], acc[rb][cb][4 * q + 3]));
+      }
+  if (threadIdx.x < T::kBM) {
+    s_pos[threadIdx.x] = my_pos;
+    s_slot[threadIdx.x] = my_slot;
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  barrier();
+
+  const int head0 = col0 / kD;
+  uint16_t* qkv = static_cast<uint16_t*>(a.y);
+  if (head0 < kHq + kHkv) {  // q or k heads (a tile never mixes kinds: 4096, 5120 | kBN)
+    const int g = lane >> 4, j = lane & 15;
+    const bool is_k = head0 >= kHq;
+    const float* wv = is_k ? p.wk : p.wq;
+    const float4 w1 = *reinterpret_cast<const float4*>(wv + 4 * j);
+    const float4 w2 = *reinterpret_cast<const float4*>(wv + 64 + 4 * j);
+    const float wa[4] = {w1.x, w1.y, w1.z, w1.w}, wb[4] = {w2.x, w2.y, w2.z, w2.w};
+    // (row, head) pairs in batches of kB per lane group: every load of a batch (staged
+    // values, positions, then the cos/sin rows) is issued before any is used
+    constexpr int kB = 8;
+    constexpr int kPerGroup = T::kBM * kNH / (T::kWaves * 4);
+    static_assert(kPerGroup % kB == 0, "batches");
+    for (int b0 = 0; b0 < kPerGroup; b0 += kB) {
+      int rt[kB], pos[kB];
+      uint2 lo[kB], hv[kB];
+      float4 c4[kB], s4[kB];
+#pragma unroll
+      for (int b = 0; b < kB; ++b) {
+        const int hr = (b0 + b) * T::kWaves * 4 + w * 4 + g;  // (row, head) of this group
+        rt[b] = hr / kNH;
+        const int hi = hr % kNH;
+        pos[b] = s_pos[rt[b]];
+        const char* src = lds + rt[b] * kTP + (hi * kD + 4 * j) * 2;
+        lo[b] = *reinterpret_cast<const uint2*>(src);
+        hv[b] = *reinterpret_cast<const uint2*>(src + 128);
+      }
+#pragma unroll
+      for (int b = 0; b < kB; ++b) {
+        const int pc = pos[b] >= 0 && pos[b] < p.rope_max_pos ? pos[b] : 0;
+        c4[b] = *reinterpret_cast<const float4*>(p.cos_tab + (long long)pc * 64 + 4 * j);
+        s4[b] = *reinterpret_cast<const float4*>(p.sin_tab + (long long)pc * 64 + 4 * j);
+      }
+#pragma unroll
+      for (int b = 0; b < kB; ++b) {
+        const int hr = (b0 + b) * T::kWaves * 4 + w * 4 + g;
+        const int row = row0 + rt[b], head = head0 + hr % kNH;
+        const bool pos_ok = pos[b] >= 0 && pos[b] < p.rope_max_pos;  // false: no such row too
+        const float cs[4] = {c4[b].x, c4[b].y, c4[b].z, c4[b].w};
+        const float sn[4] = {s4[b].x, s4[b].y, s4[b].z, s4[b].w};
+        uint2 olo, ohi;
+        norm_rope_head(lo[b], hv[b], wa, wb, cs, sn, p.eps, olo, ohi);  // all lanes
+        if (row >= T_rows) continue;
+        if (!pos_ok) {  // no table row: the projection's values, as unfused
+          olo = lo[b];
+          ohi = hv[b];
+        }
+        if (!is_k || p.write_k) {
+          uint16_t* d = qkv + (long long)row * a.ldy + head * kD + 4 * j;
+          *reinterpret_cast<uint2*>(d) = olo;
+          *reinterpret_cast<uint2*>(d + 64) = ohi;
+        }
+        if (is_k && pos_ok) {
+          const int slot = s_slot[rt[b]];
+          const long long page = slot / kPage;
+          if (slot >= 0 && page < p.pool_pages) {
+            uint16_t* kd = p.pool + run_offset(page, head - kHq) + (slot % kPage) * kD + 4 * j;
+            *reinterpret_cast<uint2*>(kd) = olo;
+            *reinterpret_cast<uint2*>(kd + 64) = ohi;
+          }
+        }
+      }
+    }
+    return;
+  }
+  // v heads: one wave per row; lane l holds dims 2l, 2l+1 of each head
+  for (int rt = w; rt < T::kBM; rt += T::kWaves) {
+    const int row = row0 + rt;
+    if (row >= T_rows) break;
+    const int pos = s_pos[rt];
+    if (pos < 0 || pos >= p.rope_max_pos) continue;  // the append skips such rows
+    const int slot = s_slot[rt];
+    const long long page = slot / kPage;
+    if (slot < 0 || page >= p.pool_pages) continue;
+    const int tok = slot % kPage, lt = rt - tok;  // the page's first row, in the tile
+    // A page whose rows all lie in the tile (and that the append kernel would write whole:
+    // same test) is written by its first row; any other row writes its own column.  Both
+    // give the same bytes.
+    bool whole = lt >= 0 && lt + kPage <= T::kBM && row0 + lt + kPage <= T_rows;
+    if (whole)
+      whole = s_slot[lt] == slot - tok && s_slot[lt + kPage - 1] == slot - tok + kPage - 1 &&
+              s_pos[lt] >= 0 && s_pos[lt + kPage - 1] < p.rope_max_pos;
+    if (whole && tok != 0) continue;
+#pragma unroll
+    for (int hi = 0; hi < kNH; ++hi) {
+      const int kvh = head0 + hi - kHq - kHkv;
+      uint16_t* vt = p.pool + run_offset(page, kvh) + kVOff + 2 * lane * kPage;
+      if (whole) {
+        uint32_t x[kPage];
+#pragma unroll
+        for (int t = 0; t < kPage; ++t)
+          x[t] = *reinterpret_cast<const uint32_t*>(lds + (rt + t) * kTP + (hi * kD + 2 * lane) * 2);
+        uint32_t y0[8], y1[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          y0[k] = __builtin_amdgcn_perm(x[2 * k + 1], x[2 * k], 0x05040100u);
+          y1[k] = __builtin_amdgcn_perm(x[2 * k + 1], x[2 * k], 0x07060302u);
+        }
+        uint4* v4 = reinterpret_cast<uint4*>(vt);
+        v4[0] = make_uint4(y0[0], y0[1], y0[2], y0[3]);
+        v4[1] = make_uint4(y0[4], y0[5], y0[6], y0[7]);
+        v4[2] = make_uint4(y1[0], y1[1], y1[2], y1[3]);
+        v4[3] = make_uint4(y1[4], y1[5], y1[6], y1[7]);
+      } else {
+        const uint32_t x = *reinterpret_cast<const uint32_t*>(lds + rt * kTP + (hi * kD + 2 * lane) * 2);
+        vt[tok] = (uint16_t)x;
+        vt[kPage + tok] = (uint16_t)(x >> 16);
+      }
+    }
   }
 }
 
@@ -483,11 +664,25 @@ static void gemm_launch_main(const GemmArgs& a, const GemmPlan& p, bool f32, hip
 
 int gemm_launch_partials(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y,
                          int64_t ldy, int32_t M, int32_t N, int32_t K, void* workspace,
-                         int64_t workspace_bytes, hipStream_t st) {
+                         int64_t workspace_bytes, hipStream_t st, const GemmAppend* app,
+                         bool* appended) {
   GemmArgs a;
   GemmPlan p;
+  if (appended) *appended = false;
   const int rc = gemm_prepare(x, ldx, w, ldw, y, ldy, M, N, K, workspace, workspace_bytes, a, p);
   if (rc != FQA_OK || M == 0) return rc;
+  if (app && p.splits == 1 && N == kQkvStride && (p.tile == 0 || p.tile == 4)) {
+    a.app = *app;
+    const dim3 grid((unsigned)(a.m_tiles * a.n_tiles));
+    if (p.tile == 0)
+      hipLaunchKernelGGL((gemm_kernel<TileL, false, false, false, true>), grid,
+                         dim3(TileL::kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((gemm_kernel<TileL8, false, false, false, true>), grid,
+                         dim3(TileL8::kThreads), 0, st, a);
+    if (appended) *appended = true;
+    return 1;
+  }
   gemm_launch_main(a, p, false, st);
   return p.splits;
 }

@@ -28,6 +28,7 @@
 // fqa_gemm + fqa_qknorm_rope_append bit for bit without the bf16 qkv round trip.
 //
 #include "fqa_common.h"
+#include "fqa_append_math.h"
 #include "fqa_gemm_internal.h"
 
 namespace fqa {
@@ -96,13 +97,6 @@ __device__ __forceinline__ uint32_t load2(const AppendArgs& a, long long row, in
   }
 }
 
-__device__ __forceinline__ void unpack4(uint2 v, float* f) {
-  f[0] = __uint_as_float(v.x << 16);
-  f[1] = __uint_as_float(v.x & 0xffff0000u);
-  f[2] = __uint_as_float(v.y << 16);
-  f[3] = __uint_as_float(v.y & 0xffff0000u);
-}
-
 // What the kernel does with a row (kMode): the fused norm + RoPE + append; the norm + RoPE
 // alone (q and k in place, nothing appended: LaunchHeadNormRope); or the append alone of
 // the row's k and v as they are in qkv (KvStore::StoreKV).
@@ -168,29 +162,12 @@ __global__ void __launch_bounds__(256) qknorm_rope_append_kernel(AppendArgs a) {
   for (int i = 0; i < HPG; ++i) {
     const int head = g + 4 * (sw * HPG + i);
     const bool is_k = head >= kHq;  // heads 32..39: only i >= 8
-    float x1[4], x2[4];
-    unpack4(lo[i], x1);
-    unpack4(hi[i], x2);
-    float ss = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) ss += x1[e] * x1[e] + x2[e] * x2[e];
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, kWave);
-    const float inv = 1.0f / sqrtf(ss / (float)kD + a.eps);
     const float wa[4] = {is_k ? k1.x : q1.x, is_k ? k1.y : q1.y, is_k ? k1.z : q1.z,
                          is_k ? k1.w : q1.w};
     const float wb[4] = {is_k ? k2.x : q2.x, is_k ? k2.y : q2.y, is_k ? k2.z : q2.z,
                          is_k ? k2.w : q2.w};
-    float o1[4], o2[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float y1 = x1[e] * inv * wa[e];
-      const float y2 = x2[e] * inv * wb[e];
-      o1[e] = y1 * cs[e] - y2 * sn[e];
-      o2[e] = y2 * cs[e] + y1 * sn[e];
-    }
-    const uint2 olo = make_uint2(pack_bf16x2(o1[0], o1[1]), pack_bf16x2(o1[2], o1[3]));
-    const uint2 ohi = make_uint2(pack_bf16x2(o2[0], o2[1]), pack_bf16x2(o2[2], o2[3]));
+    uint2 olo, ohi;
+    norm_rope_head(lo[i], hi[i], wa, wb, cs, sn, a.eps, olo, ohi);
     uint16_t* hs = src + head * kD;
     if (!is_k || a.write_k) {
       *reinterpret_cast<uint2*>(hs + 4 * j) = olo;
@@ -364,9 +341,14 @@ extern "C" int fqa_qkv_proj_append(const fqa_dims* dims, const uint16_t* x, int6
       !pool)
     return FQA_EINVAL;
   hipStream_t st = (hipStream_t)stream;
+  const GemmAppend app{q_norm_w, k_norm_w, cos_tab, sin_tab, rope_max_pos, positions,
+                       slot_mapping, meta, pool, pool_pages, dims->eps, write_k_inplace};
+  bool appended = false;
   const int splits = gemm_launch_partials(x, ldx, w_qkv, ldw, qkv, dims->qkv_stride, rows,
-                                          kQkvStride, hidden, workspace, workspace_bytes, st);
+                                          kQkvStride, hidden, workspace, workspace_bytes, st,
+                                          &app, &appended);
   if (splits < 0) return splits;
+  if (appended) return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
   return append_launch(dims, qkv, q_norm_w, k_norm_w, cos_tab, sin_tab, rope_max_pos, positions,
                        slot_mapping, meta, rows, pool, pool_pages, write_k_inplace,
                        splits > 1 ? static_cast<const float*>(workspace) : nullptr, splits, rows,

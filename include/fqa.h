@@ -345,13 +345,17 @@ int fqa_gemm_argmax(const void* x, int64_t ldx, const void* w, int64_t ldw, int3
  * LaunchGemm into buf_.qkv, LaunchHeadNormRope, StoreKV): qkv = x . w_qkv^T for `rows`
  * rows (x [rows, hidden] bf16, row stride ldx; w_qkv [6144, hidden], row stride ldw), then
  * per row the norm + RoPE + append of fqa_qknorm_rope_append with the same arguments and
- * results (rows_bound = rows; meta[FQA_META_ROWS] must not exceed rows).  When the
- * projection splits K (decode-sized row counts), the append kernel reads the fp32 split
- * partials directly, summed in the order fqa_gemm's reduction uses, so the bf16 qkv of the
- * unfused path is never written and read back; the results are bit-identical to fqa_gemm
- * followed by fqa_qknorm_rope_append.  In that case only q (and k with write_k_inplace) of
- * qkv is written; v goes to the pool only.  workspace: fqa_gemm_workspace_bytes(rows, 6144,
- * hidden) bytes. */
+ * results (rows_bound = rows; meta[FQA_META_ROWS] must not exceed rows).  The bf16 qkv of
+ * the unfused path is never written and read back:
+ *   - when the projection splits K (decode-sized row counts), the append kernel reads the
+ *     fp32 split partials directly, summed in the order fqa_gemm's reduction uses;
+ *   - otherwise (513..1024 rows, and from 1281 rows on: the tiles alone fill the device)
+ *     the projection's epilogue rounds its tile to bf16 in LDS and applies the norm, RoPE
+ *     and append there.
+ * Either way the results are bit-identical to fqa_gemm followed by fqa_qknorm_rope_append,
+ * and only q (and k with write_k_inplace) of qkv is written, for rows below
+ * meta[FQA_META_ROWS]; v goes to the pool only.  workspace: fqa_gemm_workspace_bytes(rows,
+ * 6144, hidden) bytes. */
 int fqa_qkv_proj_append(const fqa_dims* dims, const uint16_t* x, int64_t ldx,
                         const uint16_t* w_qkv, int64_t ldw, int32_t rows, int32_t hidden,
                         uint16_t* qkv, const float* q_norm_w, const float* k_norm_w,

@@ -79,5 +79,5 @@ def test_config5_36_layers_full_pool(gpu):
         print(f"  layer {l}: max-abs {mx:.3e} mean-abs {mean:.3e}", flush=True)
         assert mx <= sc.ATT_MAX_ABS and mean <= sc.ATT_MEAN_ABS, (l, mx, mean)
         del pool_l
-    del pool, qkv, out
+    del pool, flat, qkv, out
     torch.cuda.empty_cache()

@@ -38,6 +38,15 @@ def _case(gpu, M, K, write_k, seed):
     slots[:32] = np.arange(32, 64)
     rest = rng.permutation(np.arange(64, P * 16))[: M - 32]
     slots[32:] = rest
+    if M >= 300:
+        # full pages inside a 256-row tile (rows 96..111) and across its end (rows 248..263):
+        # whole-page V^T stores in the fused epilogue only where the page is in one tile
+        for r0, page in ((96, P - 3), (248, P - 2)):
+            pos[r0:r0 + 16] = np.arange(512, 528)
+            slots[r0:r0 + 16] = np.arange(page * 16, page * 16 + 16)
+        slots[32:] = np.where(np.isin(slots[32:], np.arange((P - 3) * 16, (P - 1) * 16)) &
+                              ~np.isin(np.arange(32, M), np.r_[96:112, 248:264]),
+                              -1, slots[32:])
     pos[M // 2] = max_pos + 5          # no table row
     slots[M // 3] = P * 16 + 40        # page outside the pool
     pos_t = torch.from_numpy(pos).to(gpu)
@@ -77,8 +86,12 @@ def _case(gpu, M, K, write_k, seed):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,K,write_k", [(40, 1024, 0), (256, 1024, 1), (256, 4096, 0),
-                                         (1300, 512, 0)])
+                                         (1000, 1024, 1), (1300, 512, 0), (2100, 1024, 1),
+                                         (8192, 4096, 0)])
 def test_qkv_fused_equals_unfused(gpu, M, K, write_k):
+    """Split row counts: the append kernel reads the projection's partials.  Unsplit ones
+    (1000 rows on 256 x 128 tiles, 1300 and more on 256 x 256 tiles): the projection's
+    epilogue does the norm, RoPE and append itself."""
     nb = _case(gpu, M, K, write_k, seed=M + K)
     if M <= 256:
         assert nb > 0  # the split path (partials read by the append kernel) was exercised

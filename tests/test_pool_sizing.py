@@ -90,12 +90,16 @@ def test_device_sizing_matches_mem_get_info(gpu):
 
     lib = _lib.load()
     torch.cuda.synchronize()
+    torch.cuda.empty_cache()
     free, total = torch.cuda.mem_get_info(gpu)
     out = C.c_int64()
     rc = lib.fqa_pool_pages_device(C.byref(make_dims()), 0.9, 36, 32768, C.byref(out))
     rc2, want = pages_of(total, total - free, 0.9)
     assert rc == rc2 == _lib.FQA_OK
     assert abs(out.value - want) <= 1  # free memory may move by a page-size crumb
-    # an MI355X holds well over 80k pages of every layer at 90%
-    assert out.value > 80000, (out.value, total)
+    # the pool fits the 90% cap beside what is in use, and the next page would not
+    per = 36 * 2 * 16 * 1024 * 2
+    assert out.value * per + (total - free) <= 0.9 * total + per
+    assert (out.value + 2) * per + (total - free) > 0.9 * total
+    assert total > 250 * GB  # an MI355X: 288 GB of HBM
     print(f"device total {total / GB:.1f} GB, free {free / GB:.1f} GB -> {out.value} pages")
