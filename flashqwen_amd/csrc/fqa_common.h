@@ -111,4 +111,17 @@ __device__ __forceinline__ int wave_extreme(int x, int id) {
   return __builtin_amdgcn_readlane(x, 63);
 }
 
+// Greedy tie order of the reference's ArgmaxKernel (engine/src/kernels.cu:184-214): 256
+// threads scan columns i = tid (mod 256) keeping the first strict maximum, then a tree
+// reduction keeps the lower slot unless the upper one is strictly larger.  Among equal
+// maxima that tree prefers the thread whose bit-reversed id is smallest (slot pairs that
+// differ in bit 0 are merged last), and within a thread the smallest column.  So column
+// i wins a tie against column j iff greedy_key(i) < greedy_key(j) (columns below 2^24).
+__device__ __forceinline__ uint32_t greedy_key(int i) {
+  return ((__builtin_bitreverse32((uint32_t)i & 255u) >> 24) << 24) | ((uint32_t)i >> 8);
+}
+// ... and a row whose largest logit is not above -1e30 (the reference's starting value)
+// gives column 0.
+constexpr float kGreedyFloor = -1e30f;
+
 }  // namespace fqa

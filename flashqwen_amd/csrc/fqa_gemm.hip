@@ -261,7 +261,7 @@ __global__ void __launch_bounds__(T::kThreads, 1) gemm_kernel(GemmArgs a) {
     return;
   }
   if constexpr (kArgmax) {
-    // per row of the tile: the largest value and its column (the smallest on ties), over
+    // per row of the tile: the largest value and its column (ties in the reference's greedy order, greedy_key), over
     // this lane's values, then lane ^ 32 (the other column half of the same row), then
     // the tile's kWN column waves through LDS (free once every wave's reads are done)
     __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -272,6 +272,7 @@ __global__ void __launch_bounds__(T::kThreads, 1) gemm_kernel(GemmArgs a) {
     for (int rb = 0; rb < T::kTM; ++rb) {
       float bv = -INFINITY;
       int bi = 0x7fffffff;
+      uint32_t bk = 0xffffffffu;
 #pragma unroll
       for (int cb = 0; cb < T::kTN; ++cb)
 #pragma unroll
@@ -280,14 +281,16 @@ __global__ void __launch_bounds__(T::kThreads, 1) gemm_kernel(GemmArgs a) {
           for (int e = 0; e < 4; ++e) {
             const float v = acc[rb][cb][4 * q + e];
             const int n = col0 + (wn * T::kTN + cb) * 32 + 8 * q + 4 * (lane >> 5) + e;
-            if (v > bv || (v == bv && n < bi)) {
+            const uint32_t k = greedy_key(n);
+            if (v > bv || (v == bv && k < bk)) {
               bv = v;
               bi = n;
+              bk = k;
             }
           }
       const float ov = __shfl_xor(bv, 32, kWave);
       const int oi = __shfl_xor(bi, 32, kWave);
-      if (ov > bv || (ov == bv && oi < bi)) {
+      if (ov > bv || (ov == bv && greedy_key(oi) < greedy_key(bi))) {
         bv = ov;
         bi = oi;
       }
@@ -305,7 +308,8 @@ __global__ void __launch_bounds__(T::kThreads, 1) gemm_kernel(GemmArgs a) {
       float bv = sv[r * T::kWN];
       int bi = si[r * T::kWN];
       for (int k = 1; k < T::kWN; ++k)
-        if (sv[r * T::kWN + k] > bv || (sv[r * T::kWN + k] == bv && si[r * T::kWN + k] < bi)) {
+        if (sv[r * T::kWN + k] > bv ||
+            (sv[r * T::kWN + k] == bv && greedy_key(si[r * T::kWN + k]) < greedy_key(bi))) {
           bv = sv[r * T::kWN + k];
           bi = si[r * T::kWN + k];
         }
@@ -503,8 +507,8 @@ __device__ void append_epilogue(const GemmArgs& a, char* lds, const float16_t (&
   }
 }
 
-// Row m's token: the largest of its per-tile maxima, the smallest column on ties (tiles
-// cover increasing columns).  One wave per row.
+// Row m's token: the largest of its per-tile maxima, ties in the reference's greedy order
+// (greedy_key).  One wave per row.
 __global__ void __launch_bounds__(256) gemm_argmax_reduce_kernel(GemmArgs a, int32_t* out) {
   const int m = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (m >= a.M) return;
@@ -525,7 +529,7 @@ __global__ void __launch_bounds__(256) gemm_argmax_reduce_kernel(GemmArgs a, int
     }
 #pragma unroll
     for (int k = 0; k < 8; ++k)
-      if (v[k] > bv || (v[k] == bv && i[k] < bi)) {
+      if (v[k] > bv || (v[k] == bv && greedy_key(i[k]) < greedy_key(bi))) {
         bv = v[k];
         bi = i[k];
       }
@@ -534,12 +538,12 @@ __global__ void __launch_bounds__(256) gemm_argmax_reduce_kernel(GemmArgs a, int
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(bv, o, kWave);
     const int oi = __shfl_xor(bi, o, kWave);
-    if (ov > bv || (ov == bv && oi < bi)) {
+    if (ov > bv || (ov == bv && greedy_key(oi) < greedy_key(bi))) {
       bv = ov;
       bi = oi;
     }
   }
-  if (lane == 0) out[m] = bi < a.N ? bi : 0;  // all -inf / NaN: token 0, as fqa_sample
+  if (lane == 0) out[m] = bv > kGreedyFloor ? bi : 0;  // nothing above -1e30: 0, as fqa_sample
 }
 
 // y = sum over the splits of the fp32 partials, 4 columns per thread.

@@ -133,39 +133,48 @@ __global__ void __launch_bounds__(kSThreads) sample_kernel(SampArgs a) {
     }
   };
 
-  if (it <= 0.f) {  // greedy: largest logit, smallest index among equals
+  if (it <= 0.f) {  // greedy: largest logit, the reference's tie order (greedy_key)
     float best = -INFINITY;
     int bi = N;
+    uint32_t bk = 0xffffffffu;
     for_each([&](int i, float v) {
-      if (v > best) {  // strictly greater: the first index in this lane's order
+      const uint32_t k = greedy_key(i);
+      if (v > best || (v == best && k < bk)) {
         best = v;
         bi = i;
+        bk = k;
       }
     });
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       const float ov = __shfl_xor(best, o, kWave);
       const int oi = __shfl_xor(bi, o, kWave);
-      if (ov > best || (ov == best && oi < bi)) {
+      const uint32_t ok = __shfl_xor(bk, o, kWave);
+      if (ov > best || (ov == best && ok < bk)) {
         best = ov;
         bi = oi;
+        bk = ok;
       }
     }
     __shared__ int wbi[kSWaves];
+    __shared__ uint32_t wbk[kSWaves];
     if (lane == 0) {
       sh[w] = best;
       wbi[w] = bi;
+      wbk[w] = bk;
     }
     __syncthreads();
     if (t == 0) {
       float b = sh[0];
       int i0 = wbi[0];
+      uint32_t k0 = wbk[0];
       for (int k = 1; k < kSWaves; ++k)
-        if (sh[k] > b || (sh[k] == b && wbi[k] < i0)) {
+        if (sh[k] > b || (sh[k] == b && wbk[k] < k0)) {
           b = sh[k];
           i0 = wbi[k];
+          k0 = wbk[k];
         }
-      a.out[row] = i0 < N ? i0 : 0;  // all -inf/NaN: token 0
+      a.out[row] = b > kGreedyFloor ? i0 : 0;  // nothing above -1e30 (all -inf/NaN): 0
     }
     return;
   }

@@ -298,8 +298,10 @@ int fqa_prefill(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
 /* Token sampling over fp32 logits, one row per sampling request (LaunchSampleBatch,
  * kernels.cu:184-327; SampleParams, sampler.h): row b of `logits` (row stride
  * `row_stride` floats, `vocab` entries) yields out[b]:
- *   inv_temp[b] <= 0: greedy, the index of the largest logit (the smallest such index
- *     when several are equal; the reference's tie order follows its thread layout);
+ *   inv_temp[b] <= 0: greedy, the index of the largest logit; equal logits resolve as the
+ *     reference's ArgmaxKernel resolves them (kernels.cu:184-214: 256 strided scans and a
+ *     tree reduction), i.e. the column with the smallest (bit-reversed column % 256,
+ *     column / 256); a row with nothing above -1e30 (its starting value) gives 0;
  *   inv_temp[b] > 0: weights w_i = exp((l_i - max) * inv_temp[b]); with top_p[b] < 1 only
  *     the largest weights are kept, the fewest whose mass reaches top_p[b] * sum(w) (all
  *     weights equal to the smallest kept one included); the token is the first index i
@@ -331,9 +333,16 @@ int fqa_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, in
 
 /* lm_head fused with the greedy pick (LaunchGemm(lm_head) + ArgmaxKernel,
  * model_runtime.cu:322-325, kernels.cu:184-327): out[m] = the column of the largest value of
- * row m of x . W^T (fp32 accumulation, the values fqa_gemm computes with y_f32 = 1), the
- * smallest column among equal values, as fqa_sample's greedy rows pick.  The logits are
- * never written: each output tile leaves its row maxima in `workspace`
+ * row m of x . W^T (fp32 accumulation over the whole of K per tile, never split), ties and
+ * rows without a value above -1e30 resolved as fqa_sample's greedy rows resolve them.  Where
+ * fqa_gemm's plan for the same shape does not split K (every lm_head shape: 1187 column
+ * tiles at vocab 151936), the values are the fp32 logits fqa_gemm writes with y_f32 = 1,
+ * so the pick equals fqa_sample's greedy pick on those logits; where fqa_gemm splits K its
+ * logits are summed in another order and can differ in the last bit.  Every row of x is
+ * picked greedily: in a batch that mixes greedy and sampled rows, either gather the greedy
+ * rows of x into a compact x first, or pick every row and then run fqa_gemm (fp32) +
+ * fqa_sample on the sampled rows only and let their picks overwrite.
+ * The logits are never written: each output tile leaves its row maxima in `workspace`
  * (fqa_gemm_argmax_workspace_bytes(M, N, K) bytes, 16-byte aligned) and a second kernel
  * reduces them.  Shape rules as fqa_gemm. */
 int64_t fqa_gemm_argmax_workspace_bytes(int32_t M, int32_t N, int32_t K);

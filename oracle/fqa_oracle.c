@@ -469,10 +469,30 @@ void fqo_sample(const float* logits, int n_rows, int vocab, int64_t stride,
   for (int b = 0; b < n_rows; ++b) {
     const float* lg = logits + (int64_t)b * stride;
     if (inv_temp[b] <= 0.f) {
-      int bi = 0;
-      for (int i = 1; i < vocab; ++i)
-        if (lg[i] > lg[bi]) bi = i;
-      out[b] = bi;
+      /* ArgmaxKernel (kernels.cu:184-214) step by step: 256 threads, thread t scans
+       * columns t, t+256, ... keeping the first strict maximum above its start (-1e30,
+       * column 0); then the tree reduction keeps the lower slot unless the upper one is
+       * strictly larger. */
+      float sval[256];
+      int sidx[256];
+      for (int t = 0; t < 256; ++t) {
+        float best = -1e30f;
+        int bi = 0;
+        for (int i = t; i < vocab; i += 256)
+          if (lg[i] > best) {
+            best = lg[i];
+            bi = i;
+          }
+        sval[t] = best;
+        sidx[t] = bi;
+      }
+      for (int st = 128; st > 0; st >>= 1)
+        for (int t = 0; t < st; ++t)
+          if (sval[t + st] > sval[t]) {
+            sval[t] = sval[t + st];
+            sidx[t] = sidx[t + st];
+          }
+      out[b] = sidx[0];
       if (kept_thr) kept_thr[b] = 0.0;
       if (kept_mass) kept_mass[b] = 0.0;
       continue;

@@ -9,6 +9,9 @@ shared mistake is unlikely:
   pack          EmitChunk rows (scheduler.h:66-72), PackBlockTables + SplitDecodePrefill
                 (model_runtime.cu:54-91), slot = bt[p/16]*16 + p%16 (kv_store.cu:56-60),
                 plus this library's decode/prefill plans as documented in include/fqa.h.
+  argmax_kernel ArgmaxKernel (engine/src/kernels.cu:184-214) simulated thread by thread:
+                its strided scans and its shared-memory tree, which fix the greedy tie
+                order.
 """
 from __future__ import annotations
 
@@ -124,3 +127,28 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
     meta[9] = P
     res["meta"] = meta
     return res
+
+
+def argmax_kernel(row):
+    """One row of ArgmaxKernel with its 256 threads: thread t keeps the first column of
+    t, t+256, ... whose logit is strictly above its running best (start -1e30, column 0);
+    then for s = 128, 64, .., 1 slot t < s takes slot t+s's pair when that value is
+    strictly larger."""
+    import numpy as np
+
+    lg = np.asarray(row, np.float32)
+    sval, sidx = [], []
+    for t in range(256):
+        best, bi = np.float32(-1e30), 0
+        for i in range(t, len(lg), 256):
+            if lg[i] > best:
+                best, bi = lg[i], i
+        sval.append(best)
+        sidx.append(bi)
+    s = 128
+    while s > 0:
+        for t in range(s):
+            if sval[t + s] > sval[t]:
+                sval[t], sidx[t] = sval[t + s], sidx[t + s]
+        s >>= 1
+    return sidx[0]

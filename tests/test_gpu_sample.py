@@ -10,6 +10,8 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
+from tests import pyref
+
 VOCAB = 151936  # Qwen3 vocabulary
 
 
@@ -51,13 +53,20 @@ def test_greedy_rows_bit_exact(gpu):
     rng = np.random.default_rng(11)
     B = 64
     lg = (rng.standard_normal((B, VOCAB)) * 4).astype(np.float32)
-    lg[3, [5, 90000]] = 50.0          # a tie: the smaller index wins
+    # ties resolve in the reference's order (its thread tree, not the smallest index)
+    lg[3, [5, 90000]] = 50.0          # threads 5 and 144: 90000 wins
+    lg[9, [100, 300, 70001]] = 50.0   # threads 100, 44, 113
+    lg[13, [512, 256, 1024]] = 50.0   # one thread: its first column, 256
     lg[7, :] = -np.inf                # all -inf: token 0
+    lg[11, :] = -2e30                 # nothing above the kernel's -1e30 start: token 0
+    lg[11, 77] = -1.5e30
     it = np.zeros(B, np.float32)
     got = _run(lg, it, np.ones(B, np.float32), rng.random(B).astype(np.float32))
     ref = orc.sample(lg, it, np.ones(B, np.float32), np.zeros(B, np.float32))[0]
     assert np.array_equal(got, ref)
-    assert got[3] == 5 and got[7] == 0
+    for r in (3, 9, 13):
+        assert got[r] == pyref.argmax_kernel(lg[r]), r
+    assert got[3] == 90000 and got[13] == 256 and got[7] == 0 and got[11] == 0
 
 
 @pytest.mark.gpu

@@ -420,9 +420,10 @@ def test_schedule_config4_known_batch():
 # ---- sampling (fqo_sample, kernels.cu:184-327) ------------------------------------------
 
 def _sample_numpy(lg, it, tp, u):
-    """Independent formulation: numpy sort + cumsum + searchsorted, fp64."""
+    """Independent formulation: numpy sort + cumsum + searchsorted, fp64; greedy rows by
+    the thread-by-thread simulation of ArgmaxKernel."""
     if it <= 0:
-        return int(np.argmax(lg))
+        return pyref.argmax_kernel(lg)
     w = np.exp((lg.astype(np.float64) - lg.max()) * it)
     thr = 0.0
     if tp < 1:
@@ -465,10 +466,19 @@ def test_sample_closed_forms():
     lg = rng.standard_normal((4, N)).astype(np.float32)
     for b in range(4):
         assert orc.sample(lg[b:b + 1], [1.3], [1e-6], [rng.random()])[0][0] == int(np.argmax(lg[b]))
-    # greedy: the first index of the maximum
+    # greedy ties in the reference's order: columns 17 and 400 sit on threads 17 and 144.
+    # Step s moves slot t+s into slot t < s when strictly larger: 144 -> 16 (s = 128),
+    # 16 -> 0 and 17 -> 1 (s = 16); at s = 1 slot 1's tie does not displace slot 0, so
+    # column 400 wins although 17 is smaller
     lg = rng.standard_normal((1, N)).astype(np.float32)
     lg[0, [17, 400]] = 9.0
-    assert orc.sample(lg, [0.0], [1.0], [0.3])[0][0] == 17
+    assert orc.sample(lg, [0.0], [1.0], [0.3])[0][0] == 400
+    # the same column on one thread: the first in its scan (256 and 512 on thread 0)
+    lg = rng.standard_normal((1, N)).astype(np.float32)
+    lg[0, [512, 256]] = 9.0
+    assert orc.sample(lg, [0.0], [1.0], [0.3])[0][0] == 256
+    # nothing above the kernel's -1e30 start: column 0
+    assert orc.sample(np.full((1, N), -3e30, np.float32), [0.0], [1.0], [0.3])[0][0] == 0
 
 
 def test_sample_against_numpy():
@@ -483,3 +493,26 @@ def test_sample_against_numpy():
         u = float(rng.random())
         got = orc.sample(lg, [it], [tp], [u])[0][0]
         assert got == _sample_numpy(lg[0], it, tp, u), (trial, N, it, tp, u)
+
+
+def test_greedy_tie_key_matches_the_thread_tree():
+    """The GPU kernels order greedy ties by a key, (bit-reversed column % 256, column / 256);
+    on random tie sets it picks what ArgmaxKernel's 256 strided scans and tree reduction
+    pick (pyref.argmax_kernel), and the C oracle agrees with both."""
+    def key(i):
+        return (int(f"{i & 255:08b}"[::-1], 2), i >> 8)
+
+    rng = np.random.default_rng(8)
+    N = 3000
+    rows = []
+    for trial in range(40):
+        lg = rng.standard_normal(N).astype(np.float32)
+        ties = rng.choice(N, size=int(rng.integers(2, 7)), replace=False)
+        lg[ties] = 7.5
+        want = min(ties.tolist(), key=key)
+        assert pyref.argmax_kernel(lg) == want, (trial, sorted(ties.tolist()))
+        rows.append(lg)
+    rows = np.stack(rows)
+    got = orc.sample(rows, np.zeros(len(rows), np.float32), np.ones(len(rows), np.float32),
+                     np.zeros(len(rows), np.float32))[0]
+    assert [int(g) for g in got] == [pyref.argmax_kernel(r) for r in rows]
