@@ -4,7 +4,9 @@
 // (StepContext::QkvProjAppend), the attention (decode + prefill) and the o_proj
 // projection (fqa_gemm) run on the GPU; the last row of every sequence that completes
 // its prompt or decode step goes through lm_head (fqa_gemm, fp32 logits) and fqa_sample,
-// and the sampled tokens go back to the scheduler (Apply).  Random weights, no MLP or
+// the greedy rows' tokens come from the fused lm_head + greedy pick (fqa_gemm_argmax over
+// all the rows, the sampled rows' picks then taken from fqa_sample), and the tokens go
+// back to the scheduler (Apply).  Random weights, no MLP or
 // residual: the loop exercises the boundary entry points end to end.  For
 // tests/test_gpu_decode_loop.py.
 //
@@ -105,7 +107,9 @@ int main(int argc, char** argv) {
     fqa::DeviceBuffer<float> norm_w(256), logits((size_t)n_slots * vocab), d_it(n_slots),
         d_tp(n_slots), d_u(n_slots);
     norm_w.Upload(ones.data(), 256, s);
-    fqa::DeviceBuffer<int32_t> d_tok(n_slots);
+    fqa::DeviceBuffer<int32_t> d_tok(n_slots), d_greedy(n_slots);
+    const int64_t am_bytes = fqa_gemm_argmax_workspace_bytes(n_slots, vocab, hidden);
+    fqa::DeviceBuffer<unsigned char> am_ws((size_t)std::max<int64_t>(am_bytes, 16));
     int64_t ws_bytes = 0;  // the largest split-K workspace any step's shapes need
     for (int m = 1; m <= budget; ++m)
       ws_bytes = std::max({ws_bytes, fqa_gemm_workspace_bytes(m, 6144, hidden),
@@ -181,10 +185,18 @@ int main(int argc, char** argv) {
                      "lm_head");
           fqa::Check(fqa_sample(logits.D(), n, vocab, vocab, d_it.D(), d_tp.D(), d_u.D(), d_tok.D(), s),
                      "fqa_sample");
+          // every row through the fused lm_head + greedy pick; the greedy rows keep it
+          fqa::Check(fqa_gemm_argmax(xs.D(), hidden, d_lm.D(), hidden, n, vocab, hidden,
+                                     d_greedy.D(), am_ws.D(), am_bytes, s),
+                     "fqa_gemm_argmax");
           std::vector<uint16_t> hs((size_t)n * hidden);
+          std::vector<int32_t> greedy(n);
           fqa::HipCheck(hipMemcpyAsync(sampled.data(), d_tok.D(), n * 4, hipMemcpyDeviceToHost, s), "d2h");
+          fqa::HipCheck(hipMemcpyAsync(greedy.data(), d_greedy.D(), n * 4, hipMemcpyDeviceToHost, s), "d2h");
           fqa::HipCheck(hipMemcpyAsync(hs.data(), xs.D(), hs.size() * 2, hipMemcpyDeviceToHost, s), "d2h");
           fqa::HipCheck(hipStreamSynchronize(s), "sync");
+          for (int i = 0; i < n; ++i)
+            if (it[i] <= 0.0f) sampled[i] = greedy[i];
           const int32_t hdr[2] = {t, n};
           std::fwrite(hdr, 4, 2, out);
           for (int i = 0; i < n; ++i) {

@@ -1,6 +1,7 @@
 """The serving loop with tokens produced on the GPU (tests/cpp/decode_loop_cpp): host
 scheduler -> pack -> per layer fqa_qkv_proj_append, attention, o_proj (fqa_gemm) ->
-lm_head (fqa_gemm, fp32) -> fqa_sample -> Apply.  Checks: every greedy token is the
+lm_head (fqa_gemm, fp32) -> fqa_sample for the sampled rows, fqa_gemm_argmax (lm_head
+fused with the greedy pick) for the greedy ones -> Apply.  Checks: every greedy token is the
 argmax of the float64 logits of the hidden row lm_head read (or, within fp32 rounding of
 a tie, one of the two largest); every sampled token passes the sampler's own checks
 against the fp64 oracle (tests/test_gpu_sample.py); two runs produce the same bytes."""
