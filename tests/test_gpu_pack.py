@@ -225,3 +225,27 @@ def test_schedule_gather_pack(gpu, seed):
     assert_pack_equal(step, ref, Rb, kw)
     if seed == 0:
         assert T == 6464 and Rb == 261
+
+
+@pytest.mark.gpu
+def test_pack_at_maximum_sizes(gpu):
+    """FQA_MAX_REQS (2048) requests in one step, mixed decode and prefill, over a table
+    stride of 8192 pages (max_ctx 131072), with the decode plan on the full grid: bit-exact
+    against the oracle."""
+    rng = np.random.default_rng(2048)
+    R, max_ctx, pool = 2048, 131072, 1 << 20
+    comp, nnew, tabs = [], [], []
+    for i in range(R):
+        if i % 8 == 0:  # a prefill chunk on a cached prefix
+            c, n = int(rng.integers(0, 100000)), int(rng.integers(2, 40))
+        else:  # a decode, some at the longest context
+            c, n = (max_ctx - 1 if i % 97 == 1 else int(rng.integers(0, 20000))), 1
+        comp.append(c)
+        nnew.append(n)
+        tabs.append(rng.integers(0, pool, size=synth.cdiv(c + n, synth.PAGE)).astype(np.int32))
+    print(f"[test_pack_at_maximum_sizes] R={R} rows={sum(nnew)} max_ctx={max_ctx}", flush=True)
+    step, ref, R, kw = run_both(gpu, comp, nnew, tabs, max_ctx=max_ctx, pool_pages=pool,
+                                dec_grid_waves=2048, dec_min_pages=8, pre_tile_q=32)
+    assert ref["status"] == 0
+    assert_pack_equal(step, ref, R, kw)
+    assert int(step.meta.cpu().numpy()[1]) == R - R // 8

@@ -229,3 +229,25 @@ def test_mixed_step_decode_on_side_stream(gpu):
         del pool
     assert np.array_equal(res[0][0], res[1][0])
     assert np.array_equal(res[0][1], res[1][1])
+
+
+@pytest.mark.gpu
+def test_decode_at_128k_context(gpu):
+    """Decode sequences at 131072 and 65537 keys (8192 and 4097 pages per stream, each
+    stream cut across many wavefronts) beside short ones, and a 3-row prefill chunk on a
+    100000-token prefix: end to end against the oracle."""
+    print("[test_decode_at_128k_context] 131072 / 65537 / 300 / 17 keys + 3-row chunk",
+          flush=True)
+    rng = np.random.default_rng(128)
+    L = [131072, 65537, 300, 17]
+    pool = 8192 + 4097 + 64 + 6300
+    perm = rng.permutation(pool).astype(np.int32)
+    tabs, o = [], 0
+    for x in L + [100003]:
+        k = synth.cdiv(x, PAGE)
+        tabs.append(perm[o:o + k])
+        o += k
+    cfg = synth._assemble("128k", [x - 1 for x in L] + [100000], [1, 1, 1, 1, 3], tabs, pool,
+                          131072)
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=2048, dec_min_pages=8)
+    _check_step(cfg, cfg, dict(kw, device=gpu), 128, "128k")
