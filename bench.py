@@ -293,7 +293,8 @@ def run_config(args, config, *, steps, warmup, with_cpu):
                 "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": traffic,
                 "traffic_source": tsrc,
-                "flops_per_launch": flops, "launch_us": round(kern_ms["prefill"] * 1e3, 2)}
+                "flops_per_launch": flops, "launch_us": round(kern_ms["prefill"] * 1e3, 2),
+                "counters": _profile_mfma_util(config)}
         if has_decode:
             logical, _ = synth.decode_bytes(_selected(cfg, comp_sel, n_sel))
             roof["decode_GBps"] = round(logical / (kern_ms["decode"] * 1e-3) / 1e9, 1)
@@ -512,6 +513,23 @@ def _profile_traffic(config: int, kernels: list[str]):
         if all(k in got for k in kernels):
             return sum(got[k] for k in kernels), f"profiles/{f.name}"
     return None, None
+
+
+def _profile_mfma_util(config: int):
+    """The prefill kernel's MFMA busy fraction of the active cycles, and the clock while it
+    ran, from the committed rocprofv3 counter summary of this config (or None)."""
+    prof = Path(__file__).resolve().parent / "profiles"
+    for f in sorted(prof.glob(f"*_config{config}.txt")):
+        util = clock = None
+        for line in f.read_text().splitlines():
+            if "MfmaUtil" in line and "=" in line:
+                util = float(line.rsplit("=", 1)[1].strip().rstrip("%")) / 100
+            if "clock while the kernel ran" in line:
+                clock = float(line.rsplit("=", 1)[1].split()[0])
+        if util is not None:
+            return {"mfma_busy_of_active_cycles": util, "clock_ghz_under_load": clock,
+                    "source": f"profiles/{f.name}"}
+    return None
 
 
 def _selected(cfg, comp_sel, n_sel):
