@@ -8,6 +8,7 @@
 #include <cstdlib>
 #include <vector>
 
+#include "../../include/fqa_compat.hpp"  // fq::ForwardInput, the reference's batch format
 #include "../../include/fqa_step.hpp"
 
 template <class T>
@@ -23,16 +24,28 @@ int main(int argc, char** argv) {
   rd(f, hdr, 4);
   const int R = hdr[0], T = hdr[1], max_ctx = hdr[2];
   const int64_t pool_pages = hdr[3];
-  fqa::BatchInput in;
-  in.computed.resize(R);
-  in.n_new.resize(R);
-  std::vector<int32_t> off(R + 1);
-  rd(f, in.computed.data(), R);
-  rd(f, in.n_new.data(), R);
+  std::vector<int32_t> computed(R), n_new(R), off(R + 1);
+  rd(f, computed.data(), R);
+  rd(f, n_new.data(), R);
   rd(f, off.data(), R + 1);
   std::vector<int32_t> pages(off[R]);
   rd(f, pages.data(), pages.size());
-  for (int r = 0; r < R; ++r) in.block_tables.emplace_back(pages.begin() + off[r], pages.begin() + off[r + 1]);
+  // the reference's ForwardInput, filled the way Request::EmitChunk fills it
+  fq::ForwardInput in;
+  for (int r = 0; r < R; ++r) {
+    in.AddRequest(std::vector<int>(pages.begin() + off[r], pages.begin() + off[r + 1]));
+    for (int k = 0; k < n_new[r]; ++k) in.AddRow(0, computed[r] + k, r);
+  }
+  // ... and converted to the mirror's per-request batch the way a binding in
+  // ModelRuntime::Forward (model_runtime.cu:304-310) does
+  fqa::BatchInput b;
+  b.computed.assign(in.block_tables.size(), 0);
+  b.n_new.assign(in.block_tables.size(), 0);
+  for (int t = 0; t < in.NumRows(); ++t) {
+    const int r = in.req_index[t];
+    if (b.n_new[r]++ == 0) b.computed[r] = in.positions[t];
+  }
+  b.block_tables.assign(in.block_tables.begin(), in.block_tables.end());
   std::vector<uint16_t> qkv((size_t)T * 6144);
   std::vector<float> wq(128), wk(128);
   const size_t pool_elems = (size_t)pool_pages * 8 * 4096;
@@ -54,7 +67,7 @@ int main(int argc, char** argv) {
     d_wq.Upload(wq.data(), 128, s);
     d_wk.Upload(wk.data(), 128, s);
     fqa::HipCheck(hipMemsetAsync(d_out.D(), 0, (size_t)T * 4096 * 2, s), "memset");
-    ctx.PrepareInputs(in, s);
+    ctx.PrepareInputs(b, s);
     ctx.RunLayer(d_qkv.D(), d_wq.D(), d_wk.D(), d_pool.D(), d_out.D(), s);
     std::vector<int32_t> meta(16);
     std::vector<uint16_t> out((size_t)T * 4096);
