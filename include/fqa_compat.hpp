@@ -383,12 +383,10 @@ class KvStore {
     num_blocks_ = pages;
     const fqa_dims d{32, 8, 128, FQA_PAGE_TOKENS, 6144, 0.f, 0.f};
     const size_t elems = (size_t)fqa_pool_bytes(&d, pages) / 2;
+    for (int l = 0; l < layers_; ++l) kv_.emplace_back(elems);  // may throw: nothing registered yet
     auto& r = detail::Reg();
-    for (int l = 0; l < layers_; ++l) {
-      kv_.emplace_back(elems);
-      std::lock_guard<std::mutex> lock(r.mu);
-      r.pool_pages[kv_.back().D()] = pages;
-    }
+    std::lock_guard<std::mutex> lock(r.mu);
+    for (auto& b : kv_) r.pool_pages[b.D()] = pages;
   }
   int layers_;
   int64_t num_blocks_ = 0;
