@@ -11,12 +11,14 @@
 // index order is (segment, step, lane) and the inverse-CDF pick keeps vocabulary order.
 // The reference finds the top-p threshold by 32 bisection passes over the row, each
 // recomputing every weight; here it is a 3-level radix select on the weights' float bits
-// (bits 30..20, 19..9, 8..0; positive floats order like their bit patterns), with mass
-// histograms in LDS (ds_add_f32): the exact smallest kept weight after 3 passes.  The
-// level-3 histograms are kept per wave, so the same pass also gives each wave's kept
-// mass.  A top-p row is read 4 times in full (max + sum, level 1, level 2, level 3 + kept
-// mass), a temperature-only row once (its kept mass per wave is the rescaled pass-1 sum),
-// against 35 in the reference; the pick then reads 1/16 of one wave's segment twice.
+// (bits 30..20, 19..9, 8..0; positive floats order like their bit patterns), with exact
+// integer mass histograms in LDS: the exact smallest kept weight after 3 levels, and with
+// it each wave's kept mass.  A top-p row is read 3 times in full (max + sum, level 1, level 2): level 2 also
+// copies the weights of the boundary bin into LDS, and level 3 runs on that copy.  Only
+// when the boundary bin holds more than 16384 weights is the row read a 4th time for level
+// 3.  A temperature-only row is read once (its kept mass per wave is the rescaled pass-1
+// sum), against 35 reads in the reference; the pick then reads 1/16 of one wave's segment
+// twice.
 
 #include "fqa_common.h"
 
@@ -26,6 +28,18 @@ namespace {
 constexpr int kSThreads = 1024;
 constexpr int kSWaves = kSThreads / kWave;
 constexpr int kBins = 2048;  // histogram bins per radix level (levels use 11, 11, 9 bits)
+constexpr int kChunk = 2;    // 256-element steps whose loads a wave issues back to back
+// Histogram masses are exact integers: a weight with exponent field E adds its 24-bit
+// significand, and a bin's mass is that sum times 2^(max(E, 1) - 150) (every bin holds one
+// exponent).  ds_add_u64 runs at several times the rate of ds_add_f32 on gfx950, whose
+// float adds were most of a top-p row's time; the sums also no longer depend on the order
+// the atomics land in, so the kept set is the same on every run.
+__device__ __forceinline__ unsigned long long significand(uint32_t bits) {
+  return (bits & 0x7fffffu) | (bits >= 0x800000u ? 0x800000u : 0u);
+}
+__device__ __forceinline__ float bin_mass(unsigned long long sum, int exp_field) {
+  return ldexpf((float)sum, max(exp_field, 1) - 150);
+}
 
 struct SampArgs {
   const float* logits;
@@ -121,15 +135,30 @@ __global__ void __launch_bounds__(kSThreads) sample_kernel(SampArgs a) {
   const int seg = ((N + kSWaves * kStep - 1) / (kSWaves * kStep)) * kStep;
   const int seg0 = min(w * seg, N), seg1 = min(seg0 + seg, N);
   const float it = a.inv_temp[row];
-  // calls f(index, logit) for this lane's elements, in vocabulary order per lane
+  // calls f(index, logit) for this lane's elements, in vocabulary order per lane.  The
+  // segment is walked in chunks of kChunk steps whose loads are all issued before any
+  // element is used, so a wave keeps kChunk KiB in flight instead of waiting out one
+  // load's latency per step.
   auto for_each = [&](auto&& f) {
-    for (int s0 = seg0; s0 < seg1; s0 += kStep) {
-      const int i = s0 + 4 * lane;
-      float x[4];
-      load4<kVec4>(lg, i, seg1, x);
+    for (int c0 = seg0; c0 < seg1; c0 += kChunk * kStep) {
+      float x[kChunk][4];
+      if (kVec4 && c0 + kChunk * kStep <= seg1) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (i + e < seg1) f(i + e, x[e]);
+        for (int u = 0; u < kChunk; ++u) {
+          const float4 v = *reinterpret_cast<const float4*>(lg + c0 + u * kStep + 4 * lane);
+          x[u][0] = v.x; x[u][1] = v.y; x[u][2] = v.z; x[u][3] = v.w;
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) load4<kVec4>(lg, c0 + u * kStep + 4 * lane, seg1, x[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kChunk; ++u) {
+        const int i = c0 + u * kStep + 4 * lane;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (i + e < seg1) f(i + e, x[u][e]);
+      }
     }
   };
 
@@ -211,7 +240,10 @@ __global__ void __launch_bounds__(kSThreads) sample_kernel(SampArgs a) {
 
   // skm[w]: the kept mass of wave w's segment
   __shared__ float skm[kSWaves];
-  __shared__ float hist3[kSWaves][512];
+  __shared__ unsigned long long hcnt[kBins];         // levels 1 and 2
+  __shared__ unsigned long long hcnt3[kSWaves][512];  // level 3, one per wave
+  __shared__ unsigned long long s_kmc[kSWaves];
+  __shared__ int s_ncand;
   uint32_t thr = 0;  // kept: weights whose bits are >= thr (all, without top-p)
   const float tp = a.top_p[row];
   if (tp < 1.f) {
@@ -220,51 +252,97 @@ __global__ void __launch_bounds__(kSThreads) sample_kernel(SampArgs a) {
     // (1 - top_p) * Z / 2, so the top-p boundary lies above them.
     const float need = fmaxf(tp * Z, 1e-37f);  // top_p = 0 still keeps the largest weight
     const float x_min = 0.5f * (1.f - tp) * Z / (float)N;
-    for (int b = t; b < kBins; b += kSThreads) hist[b] = 0.f;
-    __syncthreads();
-    for_each([&](int, float v) {
-      const float wv = weight(v);
-      if (wv >= x_min) atomicAdd(&hist[(__float_as_uint(wv) >> 20) & 2047], wv);
-    });
-    __syncthreads();
-    float above;
-    const int b1 = find_crossing(hist, kBins, 0.f, need, sh, &sres, &sres_f, &above);
-    // pass 3: level 2, bits 19..9 of the weights in bin b1
-    for (int b = t; b < kBins; b += kSThreads) hist[b] = 0.f;
+    for (int b = t; b < kBins; b += kSThreads) hcnt[b] = 0ull;
     __syncthreads();
     for_each([&](int, float v) {
       const uint32_t bits = __float_as_uint(weight(v));
-      if ((int)((bits >> 20) & 2047) == b1) atomicAdd(&hist[(bits >> 9) & 2047], __uint_as_float(bits));
+      if (__uint_as_float(bits) >= x_min) atomicAdd(&hcnt[(bits >> 20) & 2047], significand(bits));
     });
     __syncthreads();
-    const int b2 = find_crossing(hist, kBins, above, need, sh, &sres, &sres_f, &above);
-    // pass 4: level 3 (bits 8..0 of the weights in (b1, b2)) as one histogram per wave,
-    // and per wave the mass of the weights above (b1, b2), which are all kept: the
-    // kept mass per wave then follows from the histograms without another pass
-    const uint32_t hi = ((uint32_t)b1 << 11) | (uint32_t)b2;
-    float* h3 = &hist3[0][0];
-    for (int b = t; b < kSWaves * 512; b += kSThreads) h3[b] = 0.f;
+    for (int b = t; b < kBins; b += kSThreads) hist[b] = bin_mass(hcnt[b], b >> 3);
     __syncthreads();
-    float km_hi = 0.f;
+    float above;
+    const int b1 = find_crossing(hist, kBins, 0.f, need, sh, &sres, &sres_f, &above);
+    const int e1 = b1 >> 3;  // the exponent field of every weight in bin b1
+    // pass 3: level 2, bits 19..9 of the weights in bin b1.  The same pass sums, per
+    // lane, the weights above bin b1 (all kept) and copies the weights in bin b1 into LDS
+    // (low 20 bits and the wave, in the level-3 histograms' memory); when they all fit,
+    // level 3 and the kept masses come from that copy and the row is not read again.
+    uint32_t* cand = reinterpret_cast<uint32_t*>(&hcnt3[0][0]);
+    constexpr int kCandCap = kSWaves * 512 * 2;
+    for (int b = t; b < kBins; b += kSThreads) hcnt[b] = 0ull;
+    if (t == 0) s_ncand = 0;
+    __syncthreads();
+    float km1 = 0.f;
     for_each([&](int, float v) {
       const float wv = weight(v);
       const uint32_t bits = __float_as_uint(wv);
-      if ((bits >> 9) > hi) km_hi += wv;
-      else if ((bits >> 9) == hi) atomicAdd(&hist3[w][bits & 511], wv);
+      const int bb = (int)(bits >> 20);
+      if (bb > b1) {
+        km1 += wv;
+      } else if (bb == b1) {
+        atomicAdd(&hcnt[(bits >> 9) & 2047], significand(bits));
+        const int slot = atomicAdd(&s_ncand, 1);
+        if (slot < kCandCap) cand[slot] = ((uint32_t)w << 20) | (bits & 0xfffffu);
+      }
     });
     __syncthreads();
-    if (t < 512) {
-      float s = 0.f;
-      for (int k = 0; k < kSWaves; ++k) s += hist3[k][t];
-      hist[t] = s;
-    }
+    for (int b = t; b < kBins; b += kSThreads) hist[b] = bin_mass(hcnt[b], e1);
     __syncthreads();
-    const int b3 = find_crossing(hist, 512, above, need, sh, &sres, &sres_f, &above);
-    thr = (hi << 9) | (uint32_t)b3;
-    float km = km_hi;
-    for (int b = b3 + lane; b < 512; b += kWave) km += hist3[w][b];
-    km = wave_sum(km);
-    if (lane == 0) skm[w] = km;
+    const int b2 = find_crossing(hist, kBins, above, need, sh, &sres, &sres_f, &above);
+    const uint32_t hi = ((uint32_t)b1 << 11) | (uint32_t)b2;
+    const int nc = s_ncand;
+    if (nc <= kCandCap) {
+      // level 3 over the copied weights of (b1, b2), then each wave's kept mass: the
+      // weights above bin b1 plus its copied weights at or above the threshold
+      for (int b = t; b < 512; b += kSThreads) hcnt[b] = 0ull;
+      if (t < kSWaves) s_kmc[t] = 0ull;
+      __syncthreads();
+      for (int i = t; i < nc; i += kSThreads) {
+        const uint32_t bits = ((uint32_t)b1 << 20) | (cand[i] & 0xfffffu);
+        if ((bits >> 9) == hi) atomicAdd(&hcnt[bits & 511], significand(bits));
+      }
+      __syncthreads();
+      if (t < 512) hist[t] = bin_mass(hcnt[t], e1);
+      __syncthreads();
+      const int b3 = find_crossing(hist, 512, above, need, sh, &sres, &sres_f, &above);
+      thr = (hi << 9) | (uint32_t)b3;
+      for (int i = t; i < nc; i += kSThreads) {
+        const uint32_t bits = ((uint32_t)b1 << 20) | (cand[i] & 0xfffffu);
+        if (bits >= thr) atomicAdd(&s_kmc[cand[i] >> 20], significand(bits));
+      }
+      __syncthreads();
+      const float km = wave_sum(km1);
+      if (lane == 0) skm[w] = km + bin_mass(s_kmc[w], e1);
+    } else {
+      // pass 4: level 3 (bits 8..0 of the weights in (b1, b2)) as one histogram per
+      // wave, and per wave the mass of the weights above (b1, b2), which are all kept:
+      // the kept mass per wave then follows from the histograms without another pass
+      unsigned long long* h3 = &hcnt3[0][0];
+      for (int b = t; b < kSWaves * 512; b += kSThreads) h3[b] = 0ull;
+      __syncthreads();
+      float km_hi = 0.f;
+      for_each([&](int, float v) {
+        const float wv = weight(v);
+        const uint32_t bits = __float_as_uint(wv);
+        if ((bits >> 9) > hi) km_hi += wv;
+        else if ((bits >> 9) == hi) atomicAdd(&hcnt3[w][bits & 511], significand(bits));
+      });
+      __syncthreads();
+      if (t < 512) {
+        unsigned long long c = 0;
+        for (int k = 0; k < kSWaves; ++k) c += hcnt3[k][t];
+        hist[t] = bin_mass(c, e1);
+      }
+      __syncthreads();
+      const int b3 = find_crossing(hist, 512, above, need, sh, &sres, &sres_f, &above);
+      thr = (hi << 9) | (uint32_t)b3;
+      unsigned long long c = 0;
+      for (int b = b3 + lane; b < 512; b += kWave) c += hcnt3[w][b];
+      float km = km_hi + bin_mass(c, e1);
+      km = wave_sum(km);
+      if (lane == 0) skm[w] = km;
+    }
   } else {
     // every weight is kept: wave w's mass is its pass-1 sum rescaled to the row max
     if (t < kSWaves) skm[t] = sh[t] == -INFINITY ? 0.f : sh2[t] * __expf((sh[t] - m) * it);
