@@ -47,7 +47,7 @@ def parse():
     ap.add_argument("--dec-grid-waves", type=int, default=None,
                     help="decode wavefronts (default: CUs x 8)")
     ap.add_argument("--dec-min-pages", type=int, default=8)
-    ap.add_argument("--pre-tile-q", type=int, default=32, choices=[32, 64])
+    ap.add_argument("--pre-tile-q", type=int, default=64, choices=[32, 64])
     ap.add_argument("--layers", type=int, default=None, help="config 5 only (default 36)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only copy 1 GiB device to device 3 times (the reference dispatch "

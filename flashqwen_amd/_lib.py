@@ -18,6 +18,7 @@ FQA_ENOSPACE = -4
 FQA_PAGE_TOKENS = 16
 FQA_MAX_REQS = 2048
 FQA_DECODE_NOALLOC_MAX_WAVES = 4096
+FQA_PRE_TILE_Q = 64  # prefill rows per work item the step helpers plan with (fqa.h)
 
 META_ROWS, META_N_DECODE, META_N_PREFILL, META_MAX_QLEN = 0, 1, 2, 3
 META_DEC_WAVES, META_PRE_ITEMS, META_DEC_WAVE_PAGES, META_STATUS = 4, 5, 6, 7

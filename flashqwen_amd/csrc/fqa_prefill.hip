@@ -7,11 +7,13 @@
 // fp32 accumulation; output bf16, 0 when l == 0.
 //
 // MI355X design:
-//  * One 256-thread workgroup per (32 query rows, kv head); wave w owns query head w of
-//    the kv head.  The 4 heads share every K/V tile, staged into LDS once (the
-//    reference runs one block per query head and re-reads K/V 4x, attn_cute.cu:157).
-//    Three workgroups share a CU (168 VGPRs, 48 KiB LDS each), so on every SIMD one
-//    wave's MFMAs overlap the others' softmax and waits.
+//  * One 256-thread workgroup per (query tile, kv head); wave w owns query head w of the
+//    kv head.  The 4 heads share every K/V tile, staged into LDS once (the reference runs
+//    one block per query head and re-reads K/V 4x, attn_cute.cu:157).
+//  * Two tile heights.  64 rows (the default): each wave runs two 32-row blocks, so every
+//    K and V^T fragment it reads from LDS feeds two MFMAs and each staged half serves
+//    twice the FLOPs; 256 registers, two workgroups per CU.  32 rows: 168 VGPRs, three
+//    workgroups per CU, the next half's S^T MFMAs interleaved with this half's softmax.
 //  * Transposed FA-2 on v_mfma_f32_32x32x16_bf16:
 //        S^T[32 keys x 32 rows] = K[32 x 128] . Q^T[128 x 32]   (8 MFMAs per 32 keys)
 //        O^T[128 x 32 rows]    += V^T[128 x 16 keys] . P^T      (4 MFMAs per 16 keys)
@@ -28,9 +30,11 @@
 //    rescaled lazily (only when the row max grows by more than 2^8).  Measured, the
 //    per-half staging (the 4 global->LDS instructions per wave, ~10% of the kernel) and
 //    the softmax (~9%) are the largest costs after the MFMAs themselves.
-//  * Software pipeline over 32-key halves: half t's exp/convert/sum is interleaved with
-//    the S^T MFMAs of half t+1 and the LDS reads of half t's V fragments, then half t's
-//    PV MFMAs issue back to back.
+//  * 32-row tiles: half t's exp/convert/sum is interleaved with the S^T MFMAs of half t+1
+//    and the LDS reads of half t's V fragments, then half t's PV MFMAs issue back to back.
+//    64-row tiles have no registers for a second S^T tile: per half the exps, the PV MFMAs
+//    and half t+1's S^T MFMAs run in turn (fragments read one MFMA pair ahead), and the
+//    other workgroup's wave on the SIMD fills the gaps.
 //  * K/V staging is direct global->LDS (global_load_lds_dwordx4): a ring of three 16 KiB
 //    buffers, one 32-key half (two 8 KiB page runs) each, filled two halves ahead.
 //    Each wave moves one 4 KiB region (K or V^T of one page) per half; every lane picks
@@ -39,7 +43,9 @@
 //    carries staged data.  The loads
 //    are issued from inline assembly, so the compiler neither tracks them nor inserts
 //    its own conservative waits: every wait on them is an explicit vmcnt count followed
-//    by a barrier, and the loop issues no other vector-memory loads.
+//    by a barrier.  Vector-memory loads return in order, so other loads in the loop (the
+//    64-row tile's register reloads, off the common path) can only make a count wait
+//    longer, never too little.
 //  * Work items come from the pack sorted by key count, longest first.
 
 #include "fqa_common.h"
@@ -118,12 +124,13 @@ __device__ __forceinline__ void wait_vm() {
 // moving LDS accesses across it.  Callers wait for what they need first.
 __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-// kRG row groups of 32 rows per workgroup (4 kRG waves): wave w is query head w % 4 of the
-// kv head for rows 32 (w / 4) ..  of the item; the K/V staging of a half is split over
-// all the waves, so a 64-row item (kRG = 2) stages each half once for twice the work.
-template <int kRG>
-__global__ void __launch_bounds__(256 * kRG, kRG == 1 ? 3 : 1) prefill_kernel(PreArgs a) {
-  constexpr int kLoads = 4 / kRG;  // global->LDS loads per wave per half
+// kRW row blocks of 32 rows per wave: wave w is query head w of the kv head for all 32 kRW
+// rows of the item, and every K and V^T fragment it reads from LDS feeds kRW MFMAs.  One
+// row block (168 VGPRs) runs 3 workgroups per CU; two (256) run 2 and halve the LDS
+// fragment reads and staging instructions per FLOP.
+template <int kRW>
+__global__ void __launch_bounds__(256, kRW == 1 ? 3 : 2) prefill_kernel(PreArgs a) {
+  constexpr int kLoads = 4;  // global->LDS loads per wave per half
   __shared__ __attribute__((aligned(1024))) char lds[kRing * kHalfBytes];
   auto ring = [&](int t) { return lds + (t % kRing) * kHalfBytes; };
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
@@ -134,7 +141,7 @@ __global__ void __launch_bounds__(256 * kRG, kRG == 1 ? 3 : 1) prefill_kernel(Pr
   const int n_items = a.meta[FQA_META_PRE_ITEMS];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int hw = w & 3, rg = w >> 2;  // query head within the kv head, row group
+  const int hw = w;  // query head within the kv head
   const int4 it = *reinterpret_cast<const int4*>(a.items + 4 * (long long)item);
   asm volatile("" ::"s"(it.x), "s"(it.w), "s"(n_items));  // both loads before the check
   if (item >= n_items) return;
@@ -150,33 +157,44 @@ __global__ void __launch_bounds__(256 * kRG, kRG == 1 ? 3 : 1) prefill_kernel(Pr
   const int n_pages = (nkeys + kPage - 1) / kPage;
 
   const int col = lane & 31, hf = lane >> 5;
-  const int i_row = q0 + 32 * rg + col;  // row within the request
-  const bool row_ok = i_row < q1;
   // A request's new rows sit at positions computed .. computed+qlen-1 (the pack writes
   // positions[] that way, scheduler.h:66-72), and n_keys = computed + q1.
   const int computed = nkeys - q1;
-  const int qpos = row_ok ? computed + i_row : -1;
-  const int min_pos = computed + q0 + 32 * rg;  // first row: smallest position of the wave
+  int i_row[kRW], qpos[kRW];
+  bool row_ok[kRW];
+#pragma unroll
+  for (int rb = 0; rb < kRW; ++rb) {
+    i_row[rb] = q0 + 32 * rb + col;  // row within the request
+    row_ok[rb] = i_row[rb] < q1;
+    qpos[rb] = row_ok[rb] ? computed + i_row[rb] : -1;
+  }
+  const int min_pos = computed + q0;  // smallest position of the wave
   const int h = kvh * kG + hw;
 
-  bf16x8 qf[8];
-  {
-    const uint16_t* q = a.qkv + (long long)(qs + (row_ok ? i_row : q0)) * a.stride + h * kD + hf * 8;
+  bf16x8 qf[kRW][8];
+#pragma unroll
+  for (int rb = 0; rb < kRW; ++rb) {
+    const uint16_t* q = a.qkv + (long long)(qs + (row_ok[rb] ? i_row[rb] : q0)) * a.stride + h * kD + hf * 8;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-      qf[ks] = *reinterpret_cast<const bf16x8*>(q + ks * 16);
-      if (!row_ok)
+      qf[rb][ks] = *reinterpret_cast<const bf16x8*>(q + ks * 16);
+      if (!row_ok[rb])
 #pragma unroll
-        for (int i = 0; i < 8; ++i) qf[ks][i] = (__bf16)0.0f;
+        for (int i = 0; i < 8; ++i) qf[rb][ks][i] = (__bf16)0.0f;
     }
   }
 
-  float16_t o[4];
+  float16_t o[kRW][4];
+  float m_run[kRW], l_run[kRW];
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
+  for (int rb = 0; rb < kRW; ++rb) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
-  float m_run = -1e30f, l_run = 0.f;
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[rb][db][i] = 0.f;
+    m_run[rb] = -1e30f;
+    l_run[rb] = 0.f;
+  }
 
   // ---- staging ----
   // Wave w moves page slot w/2 of each half: its K region (w even) or its V^T region
@@ -188,12 +206,11 @@ __global__ void __launch_bounds__(256 * kRG, kRG == 1 ? 3 : 1) prefill_kernel(Pr
   // scalar-cache line holds the ids of 8 halves).  Ids kept in VGPRs instead would be
   // global loads, and the compiler would then wait for every outstanding global->LDS
   // load before touching those registers.
-  // With kRG row groups the wave moves kiBs qd = rg * kLoads .. of its region.
   const int st_ps = (w >> 1) & 1, st_v = w & 1;
   uint32_t st_off[kLoads];  // byte offset inside the 8 KiB run of this lane's chunk, per load
 #pragma unroll
   for (int j = 0; j < kLoads; ++j) {
-    const int qd = rg * kLoads + j;
+    const int qd = j;
     if (st_v) {
       const int d = 32 * qd + (lane >> 1);
       st_off[j] = kVOff * 2 + d * 32 + (((lane & 1) ^ ((d >> 3) & 1)) << 4);
@@ -244,7 +261,7 @@ __global__ void __launch_bounds__(256 * kRG, kRG == 1 ? 3 : 1) prefill_kernel(Pr
     const Dma dm = stage_prep(hx, ids);
 #pragma unroll
     for (int j = 0; j < kLoads; ++j)
-      dma16(dm.run, st_off[j], dm.dst + (rg * kLoads + j) * 1024);
+      dma16(dm.run, st_off[j], dm.dst + j * 1024);
   };
   // Zero what must not count in ring buffer R: V^T tokens past a page's valid count, and
   // all of K for a page that is missing or outside the pool.  Runs after the barrier
@@ -277,17 +294,28 @@ __global__ void __launch_bounds__(256 * kRG, kRG == 1 ? 3 : 1) prefill_kernel(Pr
   auto kfrag = [&](const char* base, int ks) {
     return *reinterpret_cast<const bf16x8*>(base + lds_k(col >> 4, kf_tok, ks * 2 + hf));
   };
+  struct STile { float16_t s[kRW]; };
   auto s_tile = [&](const char* base) {
-    float16_t s;
+    STile st;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = 0.f;
+    for (int rb = 0; rb < kRW; ++rb)
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
-      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfrag(base, ks), qf[ks], s, 0, 0, 0);
-    return s;
+      for (int i = 0; i < 16; ++i) st.s[rb][i] = 0.f;
+    // K fragments read one step ahead of their MFMAs (two in registers)
+    bf16x8 kf[2];
+    kf[0] = kfrag(base, 0);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      if (ks + 1 < 8) kf[(ks + 1) & 1] = kfrag(base, ks + 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int rb = 0; rb < kRW; ++rb)
+        st.s[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks & 1], qf[rb][ks], st.s[rb], 0, 0, 0);
+    }
+    return st;
   };
 
-  float16_t s_cur;
+  STile s_cur;
   Ids ids_next;  // page ids of the next half to issue
   // One pipeline step: half t lives in ring buffer t % kRing.  kNext: a half follows.
   auto half_step = [&](int t, auto next_tag) {
@@ -308,103 +336,141 @@ __global__ void __launch_bounds__(256 * kRG, kRG == 1 ? 3 : 1) prefill_kernel(Pr
     const int key0 = t * kHalfKeys;
     if (key0 + kHalfKeys - 1 > min_pos) {  // the causal diagonal (or n_keys) crosses these keys
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int key = key0 + (v >> 3) * 16 + hf * 8 + ((v >> 2) & 1) * 4 + (v & 3);
-        if (key > qpos) s_cur[v] = -INFINITY;
-      }
-    }
-    float mx;
-    {  // max3 tree, depth 3
-      const float m0 = fmaxf(fmaxf(s_cur[0], s_cur[1]), s_cur[2]);
-      const float m1 = fmaxf(fmaxf(s_cur[3], s_cur[4]), s_cur[5]);
-      const float m2 = fmaxf(fmaxf(s_cur[6], s_cur[7]), s_cur[8]);
-      const float m3 = fmaxf(fmaxf(s_cur[9], s_cur[10]), s_cur[11]);
-      const float m4 = fmaxf(fmaxf(s_cur[12], s_cur[13]), s_cur[14]);
-      mx = fmaxf(fmaxf(fmaxf(m0, m1), m2), fmaxf(fmaxf(m3, m4), s_cur[15]));
-    }
-    mx = max_xor32(mx);
-    // Lazy rescale: the reference max only moves when the row max grows by more than
-    // 2^kRescale, so P = exp2(s*scale - m) stays <= 2^kRescale and O, l are rescaled
-    // on few halves instead of every one.
-    const float m_new = fmaxf(m_run, mx * a.scale_log2);
-    const bool grow = m_new > m_run + kRescale;
-    if (__builtin_amdgcn_ballot_w64(grow)) {  // wave-uniform: skipped on most halves
-      const float corr = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-      l_run *= corr;
+      for (int rb = 0; rb < kRW; ++rb)
 #pragma unroll
-      for (int db = 0; db < 4; ++db) o[db] *= corr;
-      m_run = grow ? m_new : m_run;
+        for (int v = 0; v < 16; ++v) {
+          const int key = key0 + (v >> 3) * 16 + hf * 8 + ((v >> 2) & 1) * 4 + (v & 3);
+          if (key > qpos[rb]) s_cur.s[rb][v] = -INFINITY;
+        }
+    }
+    bool grow[kRW], any_grow = false;
+    float m_new[kRW];
+#pragma unroll
+    for (int rb = 0; rb < kRW; ++rb) {
+      const float16_t& sc = s_cur.s[rb];
+      const float m0 = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
+      const float m1 = fmaxf(fmaxf(sc[3], sc[4]), sc[5]);
+      const float m2 = fmaxf(fmaxf(sc[6], sc[7]), sc[8]);
+      const float m3 = fmaxf(fmaxf(sc[9], sc[10]), sc[11]);
+      const float m4 = fmaxf(fmaxf(sc[12], sc[13]), sc[14]);
+      float mx = fmaxf(fmaxf(fmaxf(m0, m1), m2), fmaxf(fmaxf(m3, m4), sc[15]));
+      mx = max_xor32(mx);
+      // Lazy rescale: the reference max only moves when the row max grows by more than
+      // 2^kRescale, so P = exp2(s*scale - m) stays <= 2^kRescale and O, l are rescaled
+      // on few halves instead of every one.
+      m_new[rb] = fmaxf(m_run[rb], mx * a.scale_log2);
+      grow[rb] = m_new[rb] > m_run[rb] + kRescale;
+      any_grow |= grow[rb];
+    }
+    if (__builtin_amdgcn_ballot_w64(any_grow)) {  // wave-uniform: skipped on most halves
+#pragma unroll
+      for (int rb = 0; rb < kRW; ++rb) {
+        const float corr = grow[rb] ? __builtin_amdgcn_exp2f(m_run[rb] - m_new[rb]) : 1.0f;
+        l_run[rb] *= corr;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[rb][db] *= corr;
+        m_run[rb] = grow[rb] ? m_new[rb] : m_run[rb];
+      }
     }
 
-    // phase 1: P^T = exp2(S^T*scale - m) as bf16 and l += row sums of the same bf16 P,
-    // interleaved with the S^T MFMAs of half t+1 and the V^T fragment reads of half t
+    // P^T = exp2(S^T*scale - m) as bf16, and l += row sums of the same bf16 P
     const char* base = ring(t);
-    bf16x8 vf[2][4];
-    bf16x8 pt[2];
-    float16_t s_nxt;
-    auto softmax_exp = [&]() {
+    bf16x8 pt[kRW][2];
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+    auto row_sums = [&]() {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        // raw v_exp_f32: results below 2^-126 flush to 0, which a softmax weight can be
-        const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[v], a.scale_log2, -m_run));
-        pt[v >> 3][v & 7] = (__bf16)p;
-      }
-      typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-      const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+      for (int rb = 0; rb < kRW; ++rb)
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc)
+        for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bf16x2_t pr = {pt[kc][2 * e], pt[kc][2 * e + 1]};
-          l_run = __builtin_amdgcn_fdot2_f32_bf16(pr, one, l_run, false);
-        }
+          for (int e = 0; e < 4; ++e) {
+            const bf16x2_t pr = {pt[rb][kc][2 * e], pt[rb][kc][2 * e + 1]};
+            l_run[rb] = __builtin_amdgcn_fdot2_f32_bf16(pr, one, l_run[rb], false);
+          }
     };
-    auto read_v = [&]() {
+    auto exp_group = [&](int rb, int v0) {
+#pragma unroll
+      for (int v = v0; v < v0 + 4; ++v) {
+        // raw v_exp_f32: results below 2^-126 flush to 0, which a softmax weight can be
+        const float p = __builtin_amdgcn_exp2f(fmaf(s_cur.s[rb][v], a.scale_log2, -m_run[rb]));
+        pt[rb][v >> 3][v & 7] = (__bf16)p;
+      }
+    };
+    if constexpr (kRW == 1) {
+      // phase 1: the exps of half t interleaved with the S^T MFMAs of half t+1 and the V^T
+      // fragment reads of half t; phase 2: half t's PV MFMAs back to back
+      bf16x8 vf[2][4];
+      STile s_nxt;
+      if constexpr (kNext) {
+        // per ks of half t+1: its S^T MFMA, and on odd ks 4 exps of half t; V^T fragment
+        // reads of half t spread over the first 4 steps
+        const char* nb = ring(t + 1);
+#pragma unroll
+        for (int rb = 0; rb < kRW; ++rb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) s_nxt.s[rb][i] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+          const bf16x8 kf = kfrag(nb, ks);
+#pragma unroll
+          for (int rb = 0; rb < kRW; ++rb)
+            s_nxt.s[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[rb][ks], s_nxt.s[rb], 0, 0, 0);
+          if (ks & 1) exp_group(0, 4 * (ks >> 1));
+          if (ks < 4) {
+            const int g = ks;
+#pragma unroll
+            for (int db = (g & 1) * 2; db < (g & 1) * 2 + 2; ++db)
+              vf[g >> 1][db] = *reinterpret_cast<const bf16x8*>(base + lds_v(g >> 1, db * 32 + col, hf));
+          }
+        }
+        row_sums();
+      } else {
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+            vf[kc][db] = *reinterpret_cast<const bf16x8*>(base + lds_v(kc, db * 32 + col, hf));
+#pragma unroll
+        for (int rb = 0; rb < kRW; ++rb)
+#pragma unroll
+          for (int v0 = 0; v0 < 16; v0 += 4) exp_group(rb, v0);
+        row_sums();
+      }
+      // phase 2: O^T += V^T P^T over the two pages (16 keys each) of half t
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
         for (int db = 0; db < 4; ++db)
-          vf[kc][db] = *reinterpret_cast<const bf16x8*>(base + lds_v(kc, db * 32 + col, hf));
-    };
-    if constexpr (kNext) {
-      // four groups, each: 2 S^T MFMAs of half t+1, 4 exps, 2 V^T fragment reads
-      const char* nb = ring(t + 1);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s_nxt[i] = 0.f;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-#pragma unroll
-        for (int ks = 2 * g; ks < 2 * g + 2; ++ks)
-          s_nxt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfrag(nb, ks), qf[ks], s_nxt, 0, 0, 0);
-#pragma unroll
-        for (int v = 4 * g; v < 4 * g + 4; ++v) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(s_cur[v], a.scale_log2, -m_run));
-          pt[v >> 3][v & 7] = (__bf16)p;
-        }
-#pragma unroll
-        for (int db = (g & 1) * 2; db < (g & 1) * 2 + 2; ++db)
-          vf[g >> 1][db] = *reinterpret_cast<const bf16x8*>(base + lds_v(g >> 1, db * 32 + col, hf));
-      }
-      typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-      const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
-#pragma unroll
-      for (int kc = 0; kc < 2; ++kc)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bf16x2_t pr = {pt[kc][2 * e], pt[kc][2 * e + 1]};
-          l_run = __builtin_amdgcn_fdot2_f32_bf16(pr, one, l_run, false);
-        }
+          for (int rb = 0; rb < kRW; ++rb)
+            o[rb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[kc][db], pt[rb][kc], o[rb][db], 0, 0, 0);
+      if constexpr (kNext) s_cur = s_nxt;
     } else {
-      read_v();
-      softmax_exp();
+      // Two row blocks: no room for half t+1's S^T beside half t's (256 registers), so the
+      // phases run in turn: the exps of half t, its PV MFMAs, then half t+1's S^T MFMAs;
+      // the other wave on the SIMD overlaps them.
+#pragma unroll
+      for (int rb = 0; rb < kRW; ++rb)
+#pragma unroll
+        for (int v0 = 0; v0 < 16; v0 += 4) exp_group(rb, v0);
+      row_sums();
+      // V^T fragments read one step ahead of their MFMAs (two in registers)
+      bf16x8 vfr[2];
+      vfr[0] = *reinterpret_cast<const bf16x8*>(base + lds_v(0, col, hf));
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        const int kc = g >> 2, db = g & 3;
+        if (g + 1 < 8)
+          vfr[(g + 1) & 1] = *reinterpret_cast<const bf16x8*>(
+              base + lds_v((g + 1) >> 2, ((g + 1) & 3) * 32 + col, hf));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int rb = 0; rb < kRW; ++rb)
+          o[rb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vfr[g & 1], pt[rb][kc], o[rb][db], 0, 0, 0);
+      }
+      if constexpr (kNext) s_cur = s_tile(ring(t + 1));
     }
-    // phase 2: O^T += V^T P^T over the two pages (16 keys each) of half t
-#pragma unroll
-    for (int kc = 0; kc < 2; ++kc)
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[kc][db], pt[kc], o[db], 0, 0, 0);
-    if constexpr (kNext) s_cur = s_nxt;
   };
 
   // prologue: halves 0..2 in flight, half 0 published and fixed, S^T of half 0
@@ -421,20 +487,23 @@ __global__ void __launch_bounds__(256 * kRG, kRG == 1 ? 3 : 1) prefill_kernel(Pr
   for (int t = 0; t + 1 < n_half; ++t) half_step(t, std::true_type{});
   half_step(n_half - 1, std::false_type{});
 
-  if (!row_ok) return;
-  const auto lr = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run),
-                                                   false, false);
-  const float l = __uint_as_float(lr[0]) + __uint_as_float(lr[1]);
-  const float inv = l > 0.f ? 1.0f / l : 0.f;
-  uint16_t* dst = a.out + (long long)(qs + i_row) * (kHq * kD) + h * kD + hf * 4;
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
+  for (int rb = 0; rb < kRW; ++rb) {
+    if (!row_ok[rb]) continue;
+    const auto lr = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run[rb]),
+                                                     __float_as_uint(l_run[rb]), false, false);
+    const float l = __uint_as_float(lr[0]) + __uint_as_float(lr[1]);
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    uint16_t* dst = a.out + (long long)(qs + i_row[rb]) * (kHq * kD) + h * kD + hf * 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint2 pk = make_uint2(pack_bf16x2(o[db][i * 4] * inv, o[db][i * 4 + 1] * inv),
-                                  pack_bf16x2(o[db][i * 4 + 2] * inv, o[db][i * 4 + 3] * inv));
-      *reinterpret_cast<uint2*>(dst + db * 32 + i * 8) = pk;
-    }
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint2 pk = make_uint2(pack_bf16x2(o[rb][db][i * 4] * inv, o[rb][db][i * 4 + 1] * inv),
+                                    pack_bf16x2(o[rb][db][i * 4 + 2] * inv, o[rb][db][i * 4 + 3] * inv));
+        *reinterpret_cast<uint2*>(dst + db * 32 + i * 8) = pk;
+      }
+  }
 }
 
 bool dims_ok(const fqa_dims* d) {
@@ -465,7 +534,7 @@ extern "C" int fqa_prefill(const fqa_dims* dims, const uint16_t* qkv, const uint
     hipLaunchKernelGGL(prefill_kernel<1>, dim3(pre_item_cap * kHkv), dim3(256), 0,
                        (hipStream_t)stream, a);
   else
-    hipLaunchKernelGGL(prefill_kernel<2>, dim3(pre_item_cap * kHkv), dim3(512), 0,
+    hipLaunchKernelGGL(prefill_kernel<2>, dim3(pre_item_cap * kHkv), dim3(256), 0,
                        (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
 }

@@ -63,7 +63,7 @@ class AttnStep:
 
     def __init__(self, *, max_rows: int, max_reqs: int, max_ctx: int, pool_pages: int,
                  device="cuda", dec_grid_waves: int | None = None, dec_min_pages: int = 8,
-                 pre_tile_q: int = 32, max_bt_pages: int | None = None):
+                 pre_tile_q: int = _lib.FQA_PRE_TILE_Q, max_bt_pages: int | None = None):
         self.lib = _lib.load()
         if max_reqs > _lib.FQA_MAX_REQS:
             raise ValueError(f"max_reqs {max_reqs} > {_lib.FQA_MAX_REQS}")

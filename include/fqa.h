@@ -58,6 +58,10 @@ extern "C" {
 #define FQA_ELAUNCH (-3)      /* hipGetLastError() after a launch */
 #define FQA_ENOSPACE (-4)     /* fqa_pool_pages: the pool cannot hold one max_ctx sequence */
 
+/* Query rows per prefill work item that the step helpers (fqa_step.hpp, fqa_compat.hpp,
+ * flashqwen_amd.step) plan with. */
+#define FQA_PRE_TILE_Q 64
+
 #define FQA_PAGE_TOKENS 16
 #define FQA_MAX_REQS 2048 /* max requests in one step (reference: `slots`, args.h:13) */
 
@@ -288,7 +292,9 @@ int fqa_decode_noalloc(const fqa_dims* dims, const uint16_t* qkv, const uint16_t
  * prefix included).  Output rows out[cu_seqlens[r] + i].  Row i of request r is at
  * position computed[r] + i, as fqa_pack writes positions[] (scheduler.h:66-72); the kernel
  * derives it from the work item rather than loading positions[].  pre_tile_q must be the
- * pack's: 32 (fastest) or 64; other values return FQA_EUNSUPPORTED. */
+ * pack's: 64 (each wave runs two 32-row blocks of one query head, so every K/V fragment
+ * it reads feeds two MFMAs; FQA_PRE_TILE_Q, the fastest) or 32; other values return
+ * FQA_EUNSUPPORTED. */
 int fqa_prefill(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
                 int64_t pool_pages, const int32_t* block_tables, int32_t max_blocks,
                 const int32_t* cu_seqlens, const int32_t* positions,

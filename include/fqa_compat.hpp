@@ -161,10 +161,10 @@ class StepContext {
     int waves = fqa_dec_default_waves(device);
     if (waves <= 0) waves = 2048;
     dec_cap_ = fqa_dec_wave_bound(slots, waves);
-    pre_cap_ = fqa_pre_item_bound(slots, max_rows, 32);
+    pre_cap_ = fqa_pre_item_bound(slots, max_rows, FQA_PRE_TILE_Q);
     // the pool's page count is unknown here: pages are range-checked by each kernel
     // against the KvStore layer it reads
-    cfg_ = {max_rows, max_blocks, 0x7fffffff, waves, 8, dec_cap_, 32, pre_cap_};
+    cfg_ = {max_rows, max_blocks, 0x7fffffff, waves, 8, dec_cap_, FQA_PRE_TILE_Q, pre_cap_};
     ids = fqa::DeviceBuffer<int>(max_rows);
     pos = fqa::DeviceBuffer<int>(max_rows);
     req = fqa::DeviceBuffer<int>(max_rows);
@@ -445,7 +445,7 @@ inline void LaunchAttnPrefillCute(const bf16* q, int q_stride, const bf16* cache
   const fqa_dims d = detail::Dims(n_heads, n_kv, head_dim, block_size, q_stride, 1e-6f, scale);
   fqa::Check(fqa_prefill(&d, reinterpret_cast<const uint16_t*>(q),
                          reinterpret_cast<const uint16_t*>(cache_kv), detail::PoolPagesOf(cache_kv),
-                         bt, max_blocks, qstart, pos, ctx.PreItems(), ctx.Meta(), 32,
+                         bt, max_blocks, qstart, pos, ctx.PreItems(), ctx.Meta(), FQA_PRE_TILE_Q,
                          ctx.PreItemCap(), reinterpret_cast<uint16_t*>(out), s),
              "fqa_prefill");
 }

@@ -77,8 +77,8 @@ class StepContext {
     if (dec_grid_waves <= 0) dec_grid_waves = fqa_dec_default_waves(device);
     if (dec_grid_waves <= 0) dec_grid_waves = 2048;
     dec_cap_ = fqa_dec_wave_bound(slots, dec_grid_waves);
-    pre_cap_ = fqa_pre_item_bound(slots, max_rows, 32);
-    cfg_ = {max_rows, max_blocks_, pool_pages, dec_grid_waves, dec_min_pages, dec_cap_, 32,
+    pre_cap_ = fqa_pre_item_bound(slots, max_rows, FQA_PRE_TILE_Q);
+    cfg_ = {max_rows, max_blocks_, pool_pages, dec_grid_waves, dec_min_pages, dec_cap_, FQA_PRE_TILE_Q,
             pre_cap_};
     computed_ = DeviceBuffer<int32_t>(slots);
     n_new_ = DeviceBuffer<int32_t>(slots);
@@ -164,7 +164,7 @@ class StepContext {
           "fqa_qknorm_rope_append");
     if (side) Fork(stream, side);
     Check(fqa_prefill(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_, cu_.D(),
-                      pos_.D(), items_.D(), meta_.D(), 32, pre_cap_, out, stream),
+                      pos_.D(), items_.D(), meta_.D(), FQA_PRE_TILE_Q, pre_cap_, out, stream),
           "fqa_prefill");
     Check(fqa_decode(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_, dwaves_.D(),
                      dseqs_.D(), meta_.D(), dec_cap_, slots_, ws_.D(), out, side ? side : stream),
@@ -205,7 +205,7 @@ class StepContext {
                    hipStream_t stream) const {
     if (!has_prefill_) return;
     Check(fqa_prefill(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_, cu_.D(),
-                      pos_.D(), items_.D(), meta_.D(), 32, pre_cap_, out, stream),
+                      pos_.D(), items_.D(), meta_.D(), FQA_PRE_TILE_Q, pre_cap_, out, stream),
           "fqa_prefill");
   }
   // The attention block of one layer (model_runtime.cu:263-278).  With `side` and a

@@ -14,7 +14,7 @@ ATT_MEAN_ABS = 2e-3
 
 
 def pack_kwargs(cfg: synth.StepConfig, max_rows=None, dec_grid_waves=2048, dec_min_pages=8,
-                pre_tile_q=32, max_reqs=None):
+                pre_tile_q=64, max_reqs=None):
     from oracle import oracle as orc  # noqa: F401  (tests only)
 
     R = cfg.n_reqs if max_reqs is None else max_reqs
