@@ -251,3 +251,32 @@ def test_decode_at_128k_context(gpu):
                           131072)
     kw = sc.pack_kwargs(cfg, dec_grid_waves=2048, dec_min_pages=8)
     _check_step(cfg, cfg, dict(kw, device=gpu), 128, "128k")
+
+
+@pytest.mark.gpu
+def test_prefill_tiles_bit_identical(gpu):
+    """Ragged prefill rows around the tile edges (2, 31, 32, 33, 63, 64, 65, 97, 128, 129 and
+    300 rows, fresh and on cached prefixes that end inside a page): the 64-row items (two
+    32-row blocks per wave) give bit-for-bit the output of the 32-row items, and both are
+    within tolerance of the oracle."""
+    import torch
+
+    print("[test_prefill_tiles_bit_identical] 11 prompts, tiles 32 and 64", flush=True)
+    rng = np.random.default_rng(64)
+    n_new = [2, 31, 32, 33, 63, 64, 65, 97, 128, 129, 300]
+    computed = [0, 0, 5, 16, 0, 1000, 31, 0, 2047, 3, 90]
+    counts = [synth.cdiv(c + n, PAGE) for c, n in zip(computed, n_new)]
+    pool_pages = sum(counts) + 40
+    cfg = synth._assemble("tile-edges", computed, n_new, synth._place(rng, pool_pages, counts),
+                          pool_pages, 4096)
+    outs = {}
+    for tile in (32, 64):
+        kw = sc.pack_kwargs(cfg, dec_grid_waves=64, dec_min_pages=2, pre_tile_q=tile)
+        _check_step(cfg, cfg, dict(kw, device=gpu), 640, f"tile-edges tile {tile}")
+        pool = make_pool(cfg.pool_pages, 1640, gpu)
+        qkv_h = synth.rand_bf16(np.random.default_rng(7), (cfg.rows, QKV_STRIDE))
+        wq, wk = synth.norm_weights()
+        _, _, out = gpu_chain(cfg, qkv_h, pool, wq, wk, gpu, kw)
+        outs[tile] = out.view(torch.int16).cpu().numpy()[: cfg.rows]
+        del pool
+    assert np.array_equal(outs[32], outs[64])
