@@ -253,9 +253,15 @@ def run_config(args, config, *, steps, warmup, with_cpu):
         return None
 
     # ---- timed region: K whole steps -----------------------------------------------------
-    for _ in range(warmup):
+    # The GPU clock ramps over the first tens of milliseconds of sustained work, so steps
+    # much shorter than that (configs 1-4) get more warmup: at least `warmup` steps and
+    # ~50 ms in all.  The line reports the number of warmup steps run.
+    warm_ms = time_graph(graph, warmup) if warmup > 0 else 0.0
+    extra = max(0, math.ceil(50.0 / max(warm_ms, 1e-3)) - warmup) if warmup > 0 else 0
+    for _ in range(extra):
         graph.replay()
     torch.cuda.synchronize()
+    warmup += extra
     t0 = time.perf_counter()
     ms_events = time_graph(graph, steps)
     wall = time.perf_counter() - t0
