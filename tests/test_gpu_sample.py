@@ -138,3 +138,23 @@ def test_top_p_boundary_bin_copied_or_reread(gpu):
     assert exact >= B - 3
     for _ in range(2):
         assert np.array_equal(_run(lg, it, tp, u), got)
+
+
+@pytest.mark.gpu
+def test_top_p_ties_and_extremes(gpu):
+    """Logits on a coarse grid (many exactly equal weights, so whole runs of ties sit at
+    the threshold and the boundary bin overflows the LDS copy on some rows), top_p near 1
+    and near 0, and a vocabulary just above twice the copy's capacity."""
+    print("[test_top_p_ties_and_extremes] 48 rows", flush=True)
+    rng = np.random.default_rng(33)
+    for vocab in (VOCAB, 2 * 16384 + 1):
+        B = 24
+        lg = (np.round(rng.standard_normal((B, vocab)) * 4) / 4).astype(np.float32)
+        lg[:8] = np.round(lg[:8])  # integer logits: very large tie runs
+        it = rng.choice([0.5, 1.0, 3.0], size=B).astype(np.float32)
+        tp = np.array([0.999999, 1e-6, 0.5, 0.9, 0.75, 0.3] * 4, np.float32)
+        u = rng.random(B).astype(np.float32)
+        got = _run(lg, it, tp, u)
+        exact = _check_sampled(lg, it, tp, u, got)
+        print(f"vocab {vocab}: {exact}/{B} picks equal the fp64 oracle's")
+        assert exact >= B - 2
