@@ -34,6 +34,8 @@
 
 #include "fqa_common.h"
 
+#include <type_traits>
+
 namespace fqa {
 namespace {
 
@@ -67,14 +69,23 @@ struct PageFrag {
   short4_t v[8];
 };
 
+// One page run into registers.  kNT: non-temporal loads, for pages no other sequence of
+// the step reads (they stream through without displacing shared prefix pages from the
+// caches; with nothing to reuse they also read faster).  The choice is a template
+// parameter: two copies of the loads that differ only in the hint would be merged.
+template <bool kNT>
 __device__ __forceinline__ void load_page(PageFrag& f, const uint16_t* run, int lane) {
   const int m = lane & 15, g = lane >> 4;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
-    f.k[ks] = *reinterpret_cast<const bf16x8*>(run + m * kD + ks * 32 + g * 8);
+  for (int ks = 0; ks < 4; ++ks) {
+    const bf16x8* p = reinterpret_cast<const bf16x8*>(run + m * kD + ks * 32 + g * 8);
+    f.k[ks] = kNT ? __builtin_nontemporal_load(p) : *p;
+  }
 #pragma unroll
-  for (int b = 0; b < 8; ++b)
-    f.v[b] = *reinterpret_cast<const short4_t*>(run + kVOff + (b * 16 + m) * kPage + g * 4);
+  for (int b = 0; b < 8; ++b) {
+    const short4_t* p = reinterpret_cast<const short4_t*>(run + kVOff + (b * 16 + m) * kPage + g * 4);
+    f.v[b] = kNT ? __builtin_nontemporal_load(p) : *p;
+  }
 }
 
 struct DecState {
@@ -128,7 +139,7 @@ __device__ __forceinline__ void process_page(PageFrag& f, const bf16x8 (&qf)[4],
 }
 
 // Stream pages [pb, pe) of (sequence `seq`, kv head kvh) into `st`.
-template <int kBufs>
+template <int kBufs, bool kNT>
 __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* btr, int kvh,
                                              int pb, int pe, int L, const bf16x8 (&qf)[4],
                                              int lane, DecState& st, int first_page) {
@@ -144,7 +155,7 @@ __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* bt
   auto load = [&](PageFrag& f, bool& ok, int p) {
     const int page = (p == pb && first_page >= 0) ? first_page : btc[p];
     ok = (uint32_t)page < pool32;
-    load_page(f, a.pool + run_offset(ok ? page : 0, kvh), lane);
+    load_page<kNT>(f, a.pool + run_offset(ok ? page : 0, kvh), lane);
   };
   // kBufs page buffers in registers: page p is processed while p+1..p+kBufs-1 are in
   // flight.  The buffers rotate through a kBufs-way unrolled loop so every index is static.  (The
@@ -214,7 +225,9 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
       sq = uni4(*reinterpret_cast<const int4*>(a.seqs + 4 * (long long)di));
       sq.w = -1;  // first page id of a later stream: read from the block table
     }
-    const int r = sq.x, row = sq.y, L = sq.z;
+    // sequences that share their first page read through the caches (FQA_DEC_SHARED)
+    const int r = sq.x, row = sq.y, L = sq.z & FQA_DEC_KEYS_MASK;
+    const bool shared = (sq.z & FQA_DEC_SHARED) != 0;
     const int pages = (L + kPage - 1) / kPage;
     const int cnt = min(pages - page, left);
 
@@ -235,8 +248,12 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
     for (int b = 0; b < 8; ++b) st.acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
     st.m = -1e30f;
     st.l = 0.f;
-    stream_pages<kBufs>(a, a.bt + (long long)r * a.max_blocks, kvh, page, page + cnt, L, qf, lane, st,
-                 sq.w);
+    if (shared)
+      stream_pages<kBufs, false>(a, a.bt + (long long)r * a.max_blocks, kvh, page, page + cnt, L,
+                                 qf, lane, st, sq.w);
+    else
+      stream_pages<kBufs, true>(a, a.bt + (long long)r * a.max_blocks, kvh, page, page + cnt, L,
+                                qf, lane, st, sq.w);
     const float l_run = sum_rows4(st.l);
 
     if (n < kG) {
@@ -290,32 +307,42 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_read_floor_k
   uint32_t sink = 0;
   while (left > 0) {
     const int4 sq = *reinterpret_cast<const int4*>(a.seqs + 4 * (long long)di);
-    const int r = __builtin_amdgcn_readfirstlane(sq.x), L = __builtin_amdgcn_readfirstlane(sq.z);
+    const int r = __builtin_amdgcn_readfirstlane(sq.x);
+    const int zf = __builtin_amdgcn_readfirstlane(sq.z);
+    const int L = zf & FQA_DEC_KEYS_MASK;
+    const bool shared = (zf & FQA_DEC_SHARED) != 0;  // the same load hints as the decode
     const int pages = (L + kPage - 1) / kPage;
     const int cnt = min(pages - page, left);
     const __attribute__((address_space(4))) int32_t* btc =
         (const __attribute__((address_space(4))) int32_t*)(a.bt + (long long)r * a.max_blocks);
-    for (int p = page; p < page + cnt; p += 4) {
-      PageFrag f[4];
+    auto walk = [&](auto nt_tag) {
+      constexpr bool kNT = decltype(nt_tag)::value;
+      for (int p = page; p < page + cnt; p += 4) {
+        PageFrag f[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int id = btc[min(p + i, page + cnt - 1)];
-        load_page(f[i], a.pool + run_offset((uint32_t)id < pool32 ? id : 0, kvh), lane);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const uint4 k = __builtin_bit_cast(uint4, f[i].k[ks]);
-          sink ^= k.x ^ k.y ^ k.z ^ k.w;
+        for (int i = 0; i < 4; ++i) {
+          const int id = btc[min(p + i, page + cnt - 1)];
+          load_page<kNT>(f[i], a.pool + run_offset((uint32_t)id < pool32 ? id : 0, kvh), lane);
         }
 #pragma unroll
-        for (int b = 0; b < 8; ++b) {
-          const uint2 v = __builtin_bit_cast(uint2, f[i].v[b]);
-          sink ^= v.x ^ v.y;
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {
+            const uint4 k = __builtin_bit_cast(uint4, f[i].k[ks]);
+            sink ^= k.x ^ k.y ^ k.z ^ k.w;
+          }
+#pragma unroll
+          for (int b = 0; b < 8; ++b) {
+            const uint2 v = __builtin_bit_cast(uint2, f[i].v[b]);
+            sink ^= v.x ^ v.y;
+          }
         }
       }
-    }
+    };
+    if (shared)
+      walk(std::false_type{});
+    else
+      walk(std::true_type{});
     left -= cnt;
     page = 0;
     if (++kvh == kHkv) {
@@ -342,7 +369,7 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_combine_kern
   if (di >= n_dec) return;
   const long long G = a.meta[FQA_META_DEC_WAVES];
   const long long W = 8LL * a.meta[FQA_META_DEC_PAGES];
-  const int pages = (sq.z + kPage - 1) / kPage;
+  const int pages = ((sq.z & FQA_DEC_KEYS_MASK) + kPage - 1) / kPage;
   const long long S0 = sq.w + (long long)kvh * pages, S1 = S0 + pages;
   const long long wf = ((S0 + 1) * G - 1) / W, wl = (S1 * G - 1) / W;
   if (wf == wl) return;  // finished by one wavefront

@@ -10,7 +10,8 @@
 // Design: requests per step are few (<= FQA_MAX_REQS) while rows and block-table
 // entries are many, so every workgroup of the pack recomputes the per-request scans
 // in LDS (a few KB of L2 reads) and then writes its grid-stride share of the rows and
-// the padded block tables.  One launch, no grid-wide synchronisation, no atomics.
+// the padded block tables.  One launch, no grid-wide synchronisation, no global atomics
+// (the shared-prefix check hashes page ids with LDS atomics).
 // Workgroup 0 alone writes the per-request arrays, `meta`, and checks page ids, so
 // each output word has exactly one writer.
 #include <climits>
@@ -22,6 +23,7 @@ namespace {
 
 constexpr int kPackThreads = 1024;
 constexpr int kPackWaves = kPackThreads / 64;
+constexpr int kHashSlots = 2 * FQA_MAX_REQS;  // open addressing, never more than half full
 
 // Workgroup barrier for LDS exchanges: waits for this wave's LDS (and scalar) accesses
 // only.  __syncthreads would also wait for every outstanding global load; without that,
@@ -146,6 +148,9 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   __shared__ int s_dstart[FQA_MAX_REQS + 1];  // by decode index: 8 * page prefix
   __shared__ int s_dpages[FQA_MAX_REQS];      // by decode index: pages
   __shared__ int s_drid[FQA_MAX_REQS];        // by decode index: request
+  __shared__ int s_dflag[FQA_MAX_REQS];       // by decode index: first page id, then the flag
+  __shared__ int s_hkey[kHashSlots];          // first page ids of decode sequences
+  __shared__ int s_hcnt[kHashSlots];          // ... and how many sequences start there
   __shared__ int s_preit[FQA_MAX_REQS + 1];
   __shared__ Stats s_stats[kPackWaves];  // (Stats now has 6 fields)
   __shared__ Counts s_counts[kPackWaves];
@@ -290,6 +295,41 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       s_drid[s_decidx[r]] = r;
     }
   if (tid == 0) s_dstart[nd] = (int)W;
+  // ---- decode sequences whose first page starts another decode sequence too (a shared
+  // prefix): FQA_DEC_SHARED in their n_keys fields.  Page ids are hashed into LDS. -------
+  for (int i = tid; i < kHashSlots; i += kPackThreads) {
+    s_hkey[i] = -1;
+    s_hcnt[i] = 0;
+  }
+  auto slot_of = [](int id) { return (int)(((uint32_t)id * 2654435761u) >> 20) & (kHashSlots - 1); };
+  lds_sync();
+  for (int d = tid; d < nd; d += kPackThreads) {
+    const int id = a.b.bt_pages[s_btoff[s_drid[d]]];  // a decode sequence has >= 1 page
+    s_dflag[d] = id;
+    if (id < 0) continue;  // not a page (flagged by the range check): never shared
+    int h = slot_of(id);
+    for (int probe = 0; probe < kHashSlots; ++probe, h = (h + 1) & (kHashSlots - 1)) {
+      const int prev = atomicCAS(&s_hkey[h], -1, id);
+      if (prev == -1 || prev == id) {
+        atomicAdd(&s_hcnt[h], 1);
+        break;
+      }
+    }
+  }
+  lds_sync();
+  for (int d = tid; d < nd; d += kPackThreads) {
+    const int id = s_dflag[d];
+    int shared = 0;
+    if (id >= 0) {
+      int h = slot_of(id);
+      for (int probe = 0; probe < kHashSlots; ++probe, h = (h + 1) & (kHashSlots - 1))
+        if (s_hkey[h] == id) {
+          shared = s_hcnt[h] > 1;
+          break;
+        }
+    }
+    s_dflag[d] = shared ? FQA_DEC_SHARED : 0;
+  }
   lds_sync();
 
   // ---- rows (positions, request index, slot mapping) and decode wave shares (where
@@ -316,7 +356,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   auto store_wave = [&](int w, int di, int kvh, int page, int n, int r, int id) {
     int4* dst = reinterpret_cast<int4*>(a.o.dec_waves + 8 * (long long)w);
     dst[0] = make_int4(di, kvh, page, n);
-    dst[1] = make_int4(r, s_qstart[r], s_comp[r] + 1, id);
+    dst[1] = make_int4(r, s_qstart[r], (s_comp[r] + 1) | s_dflag[di], id);
   };
   {
     int r0 = 0, p0 = 0, page0 = 0, di1 = 0, kvh1 = 0, pg1 = 0, n1 = 0, r1 = 0, id1 = 0;
@@ -344,7 +384,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   for (int r = gtid; r < R; r += gsz)
     if (s_n[r] == 1)
       *reinterpret_cast<int4*>(a.o.dec_seqs + 4 * (long long)s_decidx[r]) =
-          make_int4(r, s_qstart[r], s_comp[r] + 1, 8 * s_decit[r]);
+          make_int4(r, s_qstart[r], (s_comp[r] + 1) | s_dflag[s_decidx[r]], 8 * s_decit[r]);
   // ---- prefill items, sorted by key count descending (stable) --------------------
   // Tile t of prefill request r covers rows [t*QT, min((t+1)*QT, n)) and needs
   // c + min((t+1)*QT, n) keys, so per request the number of tiles with more keys than X

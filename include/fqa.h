@@ -63,6 +63,13 @@ extern "C" {
 #define FQA_PRE_TILE_Q 64
 
 #define FQA_PAGE_TOKENS 16
+/* Flag in the n_keys field of dec_seqs and dec_waves (fqa_pack_out): the decode
+ * sequence's first page is also the first page of another decode sequence in the batch
+ * (a shared prefix).  The decode reads such a sequence's pages through the caches and
+ * every other sequence's with non-temporal loads, which do not displace the shared pages.
+ * n_keys = field & FQA_DEC_KEYS_MASK. */
+#define FQA_DEC_SHARED (1 << 30)
+#define FQA_DEC_KEYS_MASK (FQA_DEC_SHARED - 1)
 #define FQA_MAX_REQS 2048 /* max requests in one step (reference: `slots`, args.h:13) */
 
 /* Indices into the int32 `meta` array written by fqa_pack. */
@@ -127,10 +134,10 @@ typedef struct fqa_batch {
  * floor((w+1)*W/G)), one per decode wavefront; dec_waves[w] = {di, kvh, page, n_runs,
  * r, row, n_keys, page id} is where share w starts, how long it is, the first stream's
  * request, row and key count, and its first page (so a wavefront's first loads need no
- * further lookups).  dec_seqs[di] = {r, row = qstart[r],
- * n_keys = computed[r]+1, 8*P[di]}.  Prefill plan: one item per pre_tile_q query rows
- * of each prefill request, pre_items[i] = {r, q0, q1, n_keys = computed + q1}, ordered
- * by n_keys descending (stable). */
+ * further lookups).  dec_seqs[di] = {r, row = qstart[r], n_keys = computed[r]+1,
+ * 8*P[di]}.  The n_keys fields of both carry FQA_DEC_SHARED.  Prefill plan: one item
+ * per pre_tile_q query rows of each prefill request, pre_items[i] = {r, q0, q1,
+ * n_keys = computed + q1}, ordered by n_keys descending (stable). */
 typedef struct fqa_pack_out {
   int32_t* cu_seqlens;     /* [R+1]  qstart = cu_seqlens[r]                   */
   int32_t* qlen;           /* [R]                                             */

@@ -233,6 +233,18 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
       dec_waves[8 * w + 6] = computed[r] + 1;
       dec_waves[8 * w + 7] = bt_pages[bt_off[r] + page];
     }
+    /* A decode sequence whose first page is also another decode sequence's first page
+     * (a shared prefix) carries the shared flag (bit 30, FQA_DEC_SHARED in fqa.h) in both
+     * n_keys fields; a negative id is never shared.  This build's load-hint policy; the
+     * reference has no plan to restate here. */
+    for (int a = 0; a < nd; ++a) {
+      const int32_t id = bt_pages[bt_off[decode_rids[a]]];
+      int shared = 0;
+      for (int b = 0; id >= 0 && b < nd && !shared; ++b)
+        shared = b != a && bt_pages[bt_off[decode_rids[b]]] == id;
+      if (shared) dec_seqs[4 * a + 2] |= 1 << 30;
+    }
+    for (int w = 0; w < G; ++w) dec_waves[8 * w + 6] |= dec_seqs[4 * dec_waves[8 * w] + 2] & (1 << 30);
   }
   {
     int32_t* tmp = (int32_t*)malloc(sizeof(int32_t) * 4 * (npi > 0 ? npi : 1));

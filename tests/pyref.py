@@ -115,6 +115,15 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
         meta = [0] * 16
         meta[8], meta[7] = R, 6
         return {"meta": meta}
+    # decode sequences whose first page starts another decode sequence too: bit 30
+    # (FQA_DEC_SHARED) in both n_keys fields
+    from collections import Counter
+    firsts = Counter(tables[r][0] for r in dec if tables[r][0] >= 0)
+    shared = [tables[r][0] >= 0 and firsts[tables[r][0]] > 1 for r in dec]
+    for di, s in enumerate(seqs):
+        s[2] |= (1 << 30) if shared[di] else 0
+    for wv in waves:
+        wv[6] |= (1 << 30) if shared[wv[0]] else 0
     res["dec_seqs"] = seqs
     res["dec_waves"] = waves
     res["pre_items"] = items

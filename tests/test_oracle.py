@@ -516,3 +516,25 @@ def test_greedy_tie_key_matches_the_thread_tree():
     got = orc.sample(rows, np.zeros(len(rows), np.float32), np.ones(len(rows), np.float32),
                      np.zeros(len(rows), np.float32))[0]
     assert [int(g) for g in got] == [pyref.argmax_kernel(r) for r in rows]
+
+
+def test_pack_shared_first_page_flag():
+    """FQA_DEC_SHARED (bit 30 of n_keys in dec_seqs and dec_waves): set on the decode
+    sequences whose first page also starts another decode sequence.  Requests 0, 2 and 4
+    are decodes whose first page is 7; request 1 decodes alone; request 3's first page is
+    -1 (never shared); request 5 starts at page 7 too but is a prefill, which neither
+    carries nor causes the flag."""
+    comp = [20, 33, 16, 17, 40, 16]
+    nnew = [1, 1, 1, 1, 1, 5]
+    tabs = [[7, 3], [8, 9, 10], [7, 5], [-1, 6], [7, 3, 12], [7, 14]]
+    kw = _kw(6, max_rows=16, max_blocks=4, dec_grid_waves=7, dec_min_pages=1, dec_wave_cap=7,
+             pre_tile_q=32, pre_item_cap=8, pool_pages=64)
+    got, _ = _compare_pack(comp, nnew, tabs, kw)
+    flag = 1 << 30
+    nd = int(got["meta"][1])
+    seqs = got["dec_seqs"][:nd]
+    assert [int(r) for r in seqs[:, 0]] == [0, 1, 2, 3, 4]
+    assert [bool(z & flag) for z in seqs[:, 2]] == [True, False, True, False, True]
+    assert [int(z & (flag - 1)) for z in seqs[:, 2]] == [21, 34, 17, 18, 41]
+    for wv in got["dec_waves"][:int(got["meta"][4])]:
+        assert (wv[6] & flag) == (seqs[wv[0], 2] & flag)
