@@ -310,9 +310,10 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
 
 // The HBM read floor of a decode plan: the same wavefront grid walks the same shares of
 // the same (page, kv head) runs with the same per-lane loads as decode_split_kernel, but
-// does no arithmetic beyond folding the loaded words into one value per lane.  Four
-// pages are always in flight per wave (past the end of a stream the last page is read
-// again).  The time of this kernel is what reading the decode's bytes in its access
+// does no arithmetic beyond folding the loaded words into one value per lane.  The page
+// loop is stream_pages' rotation of four buffers with conditional refills (a variant that
+// always kept four pages in flight, re-reading the last page past a stream's end, read
+// 3-7% slower on configs 2, 4 and 5).  The time of this kernel is what reading the decode's bytes in its access
 // pattern costs on the device; decode_split_kernel's time over it is the price of the
 // attention math and the bookkeeping.  `a.ws_m` receives one word per lane (the sink).
 __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_read_floor_kernel(DecArgs a) {
@@ -339,25 +340,33 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_read_floor_k
         (const __attribute__((address_space(4))) int32_t*)(a.bt + (long long)r * a.max_blocks);
     auto walk = [&](auto nt_tag) {
       constexpr bool kNT = decltype(nt_tag)::value;
-      for (int p = page; p < page + cnt; p += 4) {
-        PageFrag f[4];
+      const int pe = page + cnt;
+      PageFrag f[4];
+      auto ld = [&](PageFrag& x, int p) {
+        const int id = btc[p];
+        load_page<kNT>(x, a.pool + run_offset((uint32_t)id < pool32 ? id : 0, kvh), lane);
+      };
+      auto fold = [&](const PageFrag& x) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int id = btc[min(p + i, page + cnt - 1)];
-          load_page<kNT>(f[i], a.pool + run_offset((uint32_t)id < pool32 ? id : 0, kvh), lane);
+        for (int ks = 0; ks < 4; ++ks) {
+          const uint4 k = __builtin_bit_cast(uint4, x.k[ks]);
+          sink ^= k.x ^ k.y ^ k.z ^ k.w;
         }
 #pragma unroll
+        for (int b = 0; b < 8; ++b) {
+          const uint2 v = __builtin_bit_cast(uint2, x.v[b]);
+          sink ^= v.x ^ v.y;
+        }
+      };
+#pragma unroll
+      for (int i = 0; i < 3; ++i)
+        if (page + i < pe) ld(f[i], page + i);
+      for (int p = page; p < pe; p += 4) {
+#pragma unroll
         for (int i = 0; i < 4; ++i) {
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks) {
-            const uint4 k = __builtin_bit_cast(uint4, f[i].k[ks]);
-            sink ^= k.x ^ k.y ^ k.z ^ k.w;
-          }
-#pragma unroll
-          for (int b = 0; b < 8; ++b) {
-            const uint2 v = __builtin_bit_cast(uint2, f[i].v[b]);
-            sink ^= v.x ^ v.y;
-          }
+          if (i > 0 && p + i >= pe) break;
+          if (p + i + 3 < pe) ld(f[(i + 3) % 4], p + i + 3);
+          fold(f[i]);
         }
       }
     };

@@ -280,3 +280,58 @@ def test_prefill_tiles_bit_identical(gpu):
         outs[tile] = out.view(torch.int16).cpu().numpy()[: cfg.rows]
         del pool
     assert np.array_equal(outs[32], outs[64])
+
+
+def _floor_checksum(pool_u16, pool_pages, bt, max_blocks, dec_seqs, n_decode):
+    """XOR of every 32-bit word of every (page, kv head) run a decode plan covers, each run
+    once per decode sequence that reads it; pages outside the pool count as page 0."""
+    runs = pool_u16.view(np.uint32).reshape(-1, PAGE * HEAD_DIM)  # one row per run (K+V)
+    run_x = np.bitwise_xor.reduce(runs, axis=1)
+    acc = np.uint32(0)
+    for r, _row, z, _ in dec_seqs[:n_decode]:
+        L = int(z) & ((1 << 30) - 1)
+        ids = bt[r * max_blocks: r * max_blocks + (L + PAGE - 1) // PAGE].astype(np.int64)
+        ids = np.where((ids >= 0) & (ids < pool_pages), ids, 0)
+        idx = (ids[:, None] * 8 + np.arange(8)[None, :]).reshape(-1)
+        acc ^= np.bitwise_xor.reduce(run_x[idx])
+    return int(acc)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cfgno,waves", [(1, 16), (2, 2048), (2, 3000)])
+def test_decode_read_floor_reads_every_run_once(gpu, cfgno, waves):
+    """fqa_decode_read_floor (the bench's HBM floor for the decode) must read exactly the
+    pages fqa_decode reads: the XOR of all lanes' folded words equals the XOR of all words
+    of every (page, kv head) run of the plan, each once per decode sequence (bit-exact;
+    a page skipped, read twice or read at a wrong address changes it).  Config 1 adds two
+    block-table entries outside the pool, which both kernels read as page 0."""
+    import torch
+
+    print(f"[test_decode_read_floor_reads_every_run_once] config{cfgno} waves={waves}",
+          flush=True)
+    cfg = synth.CONFIGS[cfgno]()
+    if cfgno == 1:
+        tabs = [t.copy() for t in cfg.tables()]
+        tabs[3][5] = cfg.pool_pages + 7
+        tabs[1][2] = -3
+        cfg = synth._assemble("bad-pages", list(cfg.computed), list(cfg.n_new), tabs,
+                              cfg.pool_pages, cfg.max_ctx)
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=waves, dec_min_pages=2)
+    kwp = {k: v for k, v in kw.items() if k != "device"}
+    rng = np.random.default_rng(7)
+    qkv_h = synth.rand_bf16(rng, (cfg.rows, QKV_STRIDE))
+    wq, wk = synth.norm_weights()
+    pool = make_pool(cfg.pool_pages, 77, gpu)
+    step, _qkv, _out = gpu_chain(cfg, qkv_h, pool, wq, wk, gpu, kwp)
+    step.workspace.zero_()
+    step.decode_read_floor(pool[0])
+    torch.cuda.synchronize()
+    meta = step.meta.cpu().numpy()
+    n_decode, n_waves = int(meta[1]), int(meta[4])
+    assert n_decode == cfg.n_reqs and n_waves > 0
+    sink = step.workspace.view(torch.int32).cpu().numpy().view(np.uint32)
+    got = int(np.bitwise_xor.reduce(sink[: n_waves * 64]))
+    want = _floor_checksum(_host_u16(pool).reshape(-1), cfg.pool_pages,
+                           step.block_tables.cpu().numpy().reshape(-1), kwp["max_blocks"],
+                           step.dec_seqs.cpu().numpy().reshape(-1, 4), n_decode)
+    assert got == want, (hex(got), hex(want))
