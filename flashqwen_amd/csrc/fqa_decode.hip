@@ -19,17 +19,19 @@
 //  * Both products run on MFMA in transposed form so that no operand is ever
 //    shuffled between lanes:
 //        S^T[16 keys x 16 cols] = K[16 x 128] . Q^T[128 x 16]  (4 x mfma 16x16x32 bf16)
-//        O^T[128 x 16 cols]    += V^T[128 x 16 keys] . P^T    (8 x mfma 16x16x16 bf16)
+//        O^T[128 x 16 cols]    += V^T[128 x 16 keys] . P^T    (2 x 8 x mfma 16x16x16 bf16)
 //    Columns 0..3 are the 4 query heads (the rest carry zeros); the S^T accumulator
 //    layout (lane = column, 4 consecutive keys per lane) is exactly the B-operand
 //    layout P^T needs, and V^T's page layout gives each lane 4 consecutive keys of one
 //    dim as one 8-byte load.  The kernel is HBM-bound; MFMA keeps the ALU out of the
 //    way (about 5% of the CU's matrix rate at full HBM bandwidth).
-//  * P is rounded to bf16 for the PV product (the reference's decode keeps P in fp32;
-//    the difference is below the bf16 output rounding the tolerance allows).
-//  * Pages rotate through four register buffers: while page p is processed the loads of
-//    p+1..p+3 are in flight, 24 KiB per wave (HBM latency x bandwidth needs ~64 KiB in
-//    flight per CU; at 2 waves per SIMD this gives ~190 KiB).
+//  * P keeps fp32 precision in the PV product, as in the reference: it is split into two
+//    bf16 terms (hi + lo) and both go through the MFMA.
+//  * Pages rotate through four register buffers, refilled one page ahead of use.  The
+//    refills are conditional (a segment's last pages), so the compiler waits for every
+//    outstanding load before a page's math: about one 8 KiB page per wave is in flight,
+//    ~64 KiB per CU at 2 waves per SIMD, which is what HBM latency x bandwidth needs.
+//    Deeper pipelines (every refill issued) measured slower on the long-sequence batch.
 #include <mutex>
 
 #include "fqa_common.h"
@@ -150,13 +152,22 @@ __device__ __forceinline__ void process_page(PageFrag& f, const bf16x8 (&qf)[4],
   }
   st.l = st.l * corr + psum;
   st.m = m_new;
-  short4_t pt;
+  // P stays fp32 as in the reference (attn_cute.cu:199): it enters the bf16 MFMA as two
+  // bf16 terms, hi = bf16(p) and lo = bf16(p - hi) (p - hi is exact in fp32), so V^T P
+  // carries ~16 significand bits of p.  The 8 extra MFMAs per page hide under the page
+  // loads (configs 2, 4 and 5 within 0.5%).
+  short4_t ph, pl;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) pt[j] = (short)f32_to_bf16_bits(pj[j]);
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t hi = f32_to_bf16_bits(pj[j]);
+    ph[j] = (short)hi;
+    pl[j] = (short)f32_to_bf16_bits(pj[j] - __uint_as_float(hi << 16));
+  }
 #pragma unroll
   for (int b = 0; b < 8; ++b) {
     st.acc[b] *= corr;
-    st.acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(f.v[b], pt, st.acc[b], 0, 0, 0);
+    st.acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(f.v[b], ph, st.acc[b], 0, 0, 0);
+    st.acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(f.v[b], pl, st.acc[b], 0, 0, 0);
   }
 }
 

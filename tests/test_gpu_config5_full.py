@@ -78,6 +78,7 @@ def test_config5_36_layers_full_pool(gpu):
         mx, mean = sc.att_errors(o_got, o_ref)
         print(f"  layer {l}: max-abs {mx:.3e} mean-abs {mean:.3e}", flush=True)
         assert mx <= sc.ATT_MAX_ABS and mean <= sc.ATT_MEAN_ABS, (l, mx, mean)
+        sc.assert_decode_rows_close(o_got, o_ref, f"layer {l}")  # every row decodes
         del pool_l
     del pool, flat, qkv, out
     torch.cuda.empty_cache()

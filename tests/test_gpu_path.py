@@ -135,6 +135,11 @@ def _check_step(cfg, sub, kw, seed, label, schedule=False, kernel_only=True):
     mx, mean = sc.att_errors(o_got, o_ref)
     print(f"{label}: kernel-only max-abs {mx:.3e} mean-abs {mean:.3e}")
     assert mx <= sc.ATT_MAX_ABS and mean <= sc.ATT_MEAN_ABS
+    drows = pk["cu_seqlens"][pk["decode_rids"][: int(pk["meta"][1])]]
+    if drows.size:
+        dmx, dmean = sc.att_errors(o_got[drows], o_ref[drows])
+        print(f"{label}: decode rows kernel-only max-abs {dmx:.3e} mean-abs {dmean:.3e}")
+        sc.assert_decode_rows_close(o_got[drows], o_ref[drows], label)
 
 
 @pytest.mark.gpu
