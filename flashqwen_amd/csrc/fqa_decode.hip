@@ -27,11 +27,12 @@
 //    way (about 5% of the CU's matrix rate at full HBM bandwidth).
 //  * P keeps fp32 precision in the PV product, as in the reference: it is split into two
 //    bf16 terms (hi + lo) and both go through the MFMA.
-//  * Pages rotate through four register buffers, refilled one page ahead of use.  The
-//    refills are conditional (a segment's last pages), so the compiler waits for every
-//    outstanding load before a page's math: about one 8 KiB page per wave is in flight,
-//    ~64 KiB per CU at 2 waves per SIMD, which is what HBM latency x bandwidth needs.
-//    Deeper pipelines (every refill issued) measured slower on the long-sequence batch.
+//  * One wavefront per SIMD (grid = CUs x 4, one workgroup per CU, which an LDS
+//    reservation keeps to itself).  Each wave computes page p while page p+1 loads: one
+//    to two 8 KiB pages in flight per wave, 4-8 MiB over the device.  On this part HBM
+//    reads go faster with fewer requests in flight: a plain streaming read peaks at one
+//    wave per SIMD, and this layout beat two waves per SIMD with one page each by 1% on
+//    the 36-layer batch, 5% on the 64-sequence batch and 3% on the mixed step.
 #include <mutex>
 
 #include "fqa_common.h"
@@ -42,10 +43,13 @@ namespace fqa {
 namespace {
 
 constexpr int kDecWavesPerBlock = 4;
-// Page buffers per wave.  2 buffers (135 VGPRs, 3 waves per SIMD possible) measured the
-// same as 4 on configs 2 and 5 at 2048 waves, slower at 3072 waves, and slower in mixed
-// steps, where the decode's waves then share CUs with the prefill's.
-constexpr int kDecBufs = 4;
+// Page buffers per wave: page p is computed while page p+1 loads (180 VGPRs).
+constexpr int kDecBufs = 2;
+// LDS reserved by each split-kernel workgroup and never touched: with it one decode
+// workgroup (one wave per SIMD) holds a CU alone.  Neither a second decode workgroup nor
+// a prefill workgroup (48 KiB) fits beside it; a prefill wave sharing a SIMD with a decode
+// wave slowed a mixed step by 30%.
+constexpr int kDecExclusiveLds = 120 * 1024;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecArgs {
@@ -74,41 +78,31 @@ struct PageFrag {
   short4_t v[8];
 };
 
-// One page run into registers.  kNT: non-temporal loads, for pages no other sequence of
-// the step reads (they stream through without displacing shared prefix pages from the
-// caches; with nothing to reuse they also read faster).  The choice is a template
-// parameter: two copies of the loads that differ only in the hint would be merged.
-// The non-temporal copy reads through a buffer resource over the 8 KiB run: every load
-// is then a 32-bit lane offset against one scalar base, not a 64-bit address add per
-// load (about 50 fewer VALU adds per page loop; config 5 decode 745 -> 720 us).  The
-// same buffer form for the temporal copy measured slower on configs 4 and 5.
+// One page run into registers, through a buffer resource over the 8 KiB run: each load is
+// a 32-bit lane offset against one scalar base, not a 64-bit address add per load.  kNT:
+// non-temporal loads, for pages no other sequence of the step reads (they stream through
+// without displacing shared prefix pages from the caches, and read faster with nothing to
+// reuse).  The hint is a template parameter: two copies of the loads that differ only in
+// it would be merged.  !live: a zero-length resource, so the loads return zeros without
+// touching memory (a refill past the end of a segment).
 template <bool kNT>
-__device__ __forceinline__ void load_page(PageFrag& f, const uint16_t* run, int lane) {
+__device__ __forceinline__ void load_page(PageFrag& f, const uint16_t* run, int lane, bool live) {
   const int m = lane & 15, g = lane >> 4;
-  if constexpr (kNT) {
-    // word 3 0x00020000: the raw-buffer format gfx9 devices expect; num_records bounds the
-    // run, so no load can leave it
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)run, (short)0, kRunElems * 2, 0x00020000);
-    constexpr int kAuxNT = 2;  // cache-policy operand: the nt bit
+  // word 3 0x00020000: the raw-buffer format gfx9 devices expect; num_records bounds the
+  // run, so no load can leave it
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)run, (short)0, live ? kRunElems * 2 : 0, 0x00020000);
+  constexpr int kAux = kNT ? 2 : 0;  // cache-policy operand: 2 is the nt bit
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, (m * kD + ks * 32 + g * 8) * 2, 0, kAuxNT);
-      f.k[ks] = __builtin_bit_cast(bf16x8, v);
-    }
+  for (int ks = 0; ks < 4; ++ks) {
+    const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, (m * kD + ks * 32 + g * 8) * 2, 0, kAux);
+    f.k[ks] = __builtin_bit_cast(bf16x8, v);
+  }
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      const i32x2 v = __builtin_amdgcn_raw_buffer_load_b64(
-          rs, (kVOff + (b * 16 + m) * kPage + g * 4) * 2, 0, kAuxNT);
-      f.v[b] = __builtin_bit_cast(short4_t, v);
-    }
-  } else {
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      f.k[ks] = *reinterpret_cast<const bf16x8*>(run + m * kD + ks * 32 + g * 8);
-#pragma unroll
-    for (int b = 0; b < 8; ++b)
-      f.v[b] = *reinterpret_cast<const short4_t*>(run + kVOff + (b * 16 + m) * kPage + g * 4);
+  for (int b = 0; b < 8; ++b) {
+    const i32x2 v = __builtin_amdgcn_raw_buffer_load_b64(
+        rs, (kVOff + (b * 16 + m) * kPage + g * 4) * 2, 0, kAux);
+    f.v[b] = __builtin_bit_cast(short4_t, v);
   }
 }
 
@@ -186,16 +180,17 @@ __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* bt
   // may take from a page buffer still in flight (a full vmcnt drain)
   const uint32_t pool32 = (uint32_t)min(a.pool_pages, (long long)0x7fffffff);
   auto load = [&](PageFrag& f, bool& ok, int p) {
-    const int page = (p == pb && first_page >= 0) ? first_page : btc[p];
+    const bool live = p < pe;
+    const int page = (p == pb && first_page >= 0) ? first_page : btc[min(p, pe - 1)];
     ok = (uint32_t)page < pool32;
-    load_page<kNT>(f, a.pool + run_offset(ok ? page : 0, kvh), lane);
+    load_page<kNT>(f, a.pool + run_offset(ok ? page : 0, kvh), lane, live);
   };
   // kBufs page buffers in registers: page p is processed while p+1..p+kBufs-1 are in
-  // flight.  The buffers rotate through a kBufs-way unrolled loop so every index is static.  (The
-  // refills are conditional, so the compiler drains the loads at each one and about one
-  // page per wave is in flight in practice; unconditional refills that keep three in
-  // flight were measured 2% slower on config 5 and equal on config 2: with 8 waves per
-  // CU the DRAM queues are already full.)
+  // flight.  The buffers rotate through a kBufs-way unrolled loop so every index is
+  // static.  Every refill is issued, past the segment's end as zero-length loads: the
+  // compiler then counts the loads exactly and waits only for the page it computes next
+  // (with conditional refills it waited for all of them, the refill just issued
+  // included, and a wave never computed while its own loads were in flight).
   // A page outside the pool (the pack flags the batch) reads as zeros: its keys score 0
   // and add nothing to the numerator.  The online softmax merge is order-free, so such
   // keys are only counted here and merged into `st` once, after the loop.
@@ -205,14 +200,12 @@ __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* bt
 #pragma unroll
   for (int i = 0; i < kBufs; ++i) ok[i] = false;
 #pragma unroll
-  for (int i = 0; i + 1 < kBufs; ++i)
-    if (pb + i < pe) load(f[i], ok[i], pb + i);
+  for (int i = 0; i + 1 < kBufs; ++i) load(f[i], ok[i], pb + i);
   for (int p = pb; p < pe; p += kBufs) {
 #pragma unroll
     for (int i = 0; i < kBufs; ++i) {
       if (i > 0 && p + i >= pe) break;
-      if (p + i + kBufs - 1 < pe)
-        load(f[(i + kBufs - 1) % kBufs], ok[(i + kBufs - 1) % kBufs], p + i + kBufs - 1);
+      load(f[(i + kBufs - 1) % kBufs], ok[(i + kBufs - 1) % kBufs], p + i + kBufs - 1);
       if (ok[i]) process_page(f[i], qf, p + i, L, g, a.scale_log2, st);
       else n_zero += min(kPage, L - (p + i) * kPage);
     }
@@ -235,6 +228,8 @@ __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* bt
 // slot 2w (the share's first stream) or 2w+1 (its last).
 template <int kBufs>
 __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel(DecArgs a) {
+  __shared__ char lds_excl[kDecExclusiveLds];  // allocated, never accessed
+  asm volatile("" ::"s"((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds_excl));
   // Everything a wave's loop indexes with is wave-uniform; readfirstlane says so, so that
   // block-table reads become scalar loads (see stream_pages).
   const int w = blockIdx.x * kDecWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -322,12 +317,14 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
 // The HBM read floor of a decode plan: the same wavefront grid walks the same shares of
 // the same (page, kv head) runs with the same per-lane loads as decode_split_kernel, but
 // does no arithmetic beyond folding the loaded words into one value per lane.  The page
-// loop is stream_pages' rotation of four buffers with conditional refills (a variant that
-// always kept four pages in flight, re-reading the last page past a stream's end, read
-// 3-7% slower on configs 2, 4 and 5).  The time of this kernel is what reading the decode's bytes in its access
+// loop is stream_pages' own (kDecBufs rotating buffers, every refill issued), and it
+// reserves the same LDS, so its workgroups sit on the CUs as the decode's do.  The time
+// of this kernel is what reading the decode's bytes in its access
 // pattern costs on the device; decode_split_kernel's time over it is the price of the
 // attention math and the bookkeeping.  `a.ws_m` receives one word per lane (the sink).
 __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_read_floor_kernel(DecArgs a) {
+  __shared__ char lds_excl[kDecExclusiveLds];  // placement as decode_split_kernel
+  asm volatile("" ::"s"((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds_excl));
   const int w = blockIdx.x * kDecWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int4 desc =
@@ -352,10 +349,11 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_read_floor_k
     auto walk = [&](auto nt_tag) {
       constexpr bool kNT = decltype(nt_tag)::value;
       const int pe = page + cnt;
-      PageFrag f[4];
+      constexpr int kB = kDecBufs;
+      PageFrag f[kB];
       auto ld = [&](PageFrag& x, int p) {
-        const int id = btc[p];
-        load_page<kNT>(x, a.pool + run_offset((uint32_t)id < pool32 ? id : 0, kvh), lane);
+        const int id = btc[min(p, pe - 1)];
+        load_page<kNT>(x, a.pool + run_offset((uint32_t)id < pool32 ? id : 0, kvh), lane, p < pe);
       };
       auto fold = [&](const PageFrag& x) {
 #pragma unroll
@@ -370,14 +368,13 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_read_floor_k
         }
       };
 #pragma unroll
-      for (int i = 0; i < 3; ++i)
-        if (page + i < pe) ld(f[i], page + i);
-      for (int p = page; p < pe; p += 4) {
+      for (int i = 0; i + 1 < kB; ++i) ld(f[i], page + i);
+      for (int p = page; p < pe; p += kB) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < kB; ++i) {
           if (i > 0 && p + i >= pe) break;
-          if (p + i + 3 < pe) ld(f[(i + 3) % 4], p + i + 3);
-          fold(f[i]);
+          ld(f[(i + kB - 1) % kB], p + i + kB - 1);
+          fold(f[i]);  // a zero-length load folds in zeros
         }
       }
     };

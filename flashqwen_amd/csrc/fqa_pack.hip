@@ -683,7 +683,7 @@ int32_t fqa_dec_default_waves(int32_t device) {
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
       cus <= 0)
     return 0;
-  return cus * 8;  // 2 decode wavefronts per SIMD (the kernel's register budget), 4 SIMDs
+  return cus * 4;  // one decode wavefront per SIMD, 4 SIMDs per CU
 }
 
 int32_t fqa_pre_item_bound(int32_t n_reqs, int32_t max_rows, int32_t pre_tile_q) {

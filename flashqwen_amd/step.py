@@ -73,8 +73,8 @@ class AttnStep:
         self.pool_pages = pool_pages
         self.max_blocks = -(-max_ctx // PAGE)
         self.pre_tile_q = pre_tile_q
-        if dec_grid_waves is None:  # fill the device: CUs x resident decode waves per CU
-            dec_grid_waves = int(self.lib.fqa_dec_default_waves(self.device.index or 0)) or 2048
+        if dec_grid_waves is None:  # fill the device: one decode wave per SIMD
+            dec_grid_waves = int(self.lib.fqa_dec_default_waves(self.device.index or 0)) or 1024
         self.dec_grid_waves = dec_grid_waves
         self.dec_wave_cap = int(self.lib.fqa_dec_wave_bound(max_reqs, dec_grid_waves))
         self.pre_cap = int(self.lib.fqa_pre_item_bound(max_reqs, max_rows, pre_tile_q))

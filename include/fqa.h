@@ -194,7 +194,7 @@ int fqa_pool_pages_device(const fqa_dims* dims, float fraction, int32_t layers,
 /* Upper bounds for plan capacities and launch grids, from host-known sizes. */
 int32_t fqa_dec_wave_bound(int32_t n_reqs, int32_t dec_grid_waves);
 
-/* A decode grid that fills the device: CUs x resident decode wavefronts per CU. */
+/* A decode grid that fills the device: CUs x 4, one decode wavefront per SIMD. */
 int32_t fqa_dec_default_waves(int32_t device);
 int32_t fqa_pre_item_bound(int32_t n_reqs, int32_t max_rows, int32_t pre_tile_q);
 

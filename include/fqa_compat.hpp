@@ -159,7 +159,7 @@ class StepContext {
       detail::Fail("StepContext sizes");
     max_blocks = (max_ctx + FQA_PAGE_TOKENS - 1) / FQA_PAGE_TOKENS;
     int waves = fqa_dec_default_waves(device);
-    if (waves <= 0) waves = 2048;
+    if (waves <= 0) waves = 1024;
     dec_cap_ = fqa_dec_wave_bound(slots, waves);
     pre_cap_ = fqa_pre_item_bound(slots, max_rows, FQA_PRE_TILE_Q);
     // the pool's page count is unknown here: pages are range-checked by each kernel

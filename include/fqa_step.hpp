@@ -75,7 +75,7 @@ class StepContext {
     max_blocks_ = (max_ctx + FQA_PAGE_TOKENS - 1) / FQA_PAGE_TOKENS;
     dims_ = {32, 8, 128, FQA_PAGE_TOKENS, 6144, 1e-6f, 1.0f / std::sqrt(128.0f)};
     if (dec_grid_waves <= 0) dec_grid_waves = fqa_dec_default_waves(device);
-    if (dec_grid_waves <= 0) dec_grid_waves = 2048;
+    if (dec_grid_waves <= 0) dec_grid_waves = 1024;
     dec_cap_ = fqa_dec_wave_bound(slots, dec_grid_waves);
     pre_cap_ = fqa_pre_item_bound(slots, max_rows, FQA_PRE_TILE_Q);
     cfg_ = {max_rows, max_blocks_, pool_pages, dec_grid_waves, dec_min_pages, dec_cap_, FQA_PRE_TILE_Q,

@@ -14,7 +14,7 @@ ATT_MAX_ABS = 2e-2
 ATT_MEAN_ABS = 2e-3
 
 
-def pack_kwargs(cfg: synth.StepConfig, max_rows=None, dec_grid_waves=2048, dec_min_pages=8,
+def pack_kwargs(cfg: synth.StepConfig, max_rows=None, dec_grid_waves=1024, dec_min_pages=8,
                 pre_tile_q=64, max_reqs=None):
     from oracle import oracle as orc  # noqa: F401  (tests only)
 

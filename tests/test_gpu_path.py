@@ -179,7 +179,7 @@ def test_decode_long_and_shared_prefix(gpu):
     tables.  Pool sized to the pages the batch uses (70000 pages, 4.6 GB)."""
     print("[test_decode_long_and_shared_prefix] config5, 1 layer", flush=True)
     cfg = synth.config5(layers=1, pool_pages=70000)
-    kw = sc.pack_kwargs(cfg, dec_grid_waves=2048, dec_min_pages=8)
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=1024, dec_min_pages=8)
     _check_step(cfg, cfg, dict(kw, device=gpu), 105, "config5", kernel_only=False)
 
 
@@ -254,7 +254,7 @@ def test_decode_at_128k_context(gpu):
         o += k
     cfg = synth._assemble("128k", [x - 1 for x in L] + [100000], [1, 1, 1, 1, 3], tabs, pool,
                           131072)
-    kw = sc.pack_kwargs(cfg, dec_grid_waves=2048, dec_min_pages=8)
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=1024, dec_min_pages=8)
     _check_step(cfg, cfg, dict(kw, device=gpu), 128, "128k")
 
 
@@ -303,7 +303,7 @@ def _floor_checksum(pool_u16, pool_pages, bt, max_blocks, dec_seqs, n_decode):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("cfgno,waves", [(1, 16), (2, 2048), (2, 3000)])
+@pytest.mark.parametrize("cfgno,waves", [(1, 16), (2, 1024), (2, 2048), (2, 3000)])
 def test_decode_read_floor_reads_every_run_once(gpu, cfgno, waves):
     """fqa_decode_read_floor (the bench's HBM floor for the decode) must read exactly the
     pages fqa_decode reads: the XOR of all lanes' folded words equals the XOR of all words
