@@ -340,3 +340,56 @@ def test_decode_read_floor_reads_every_run_once(gpu, cfgno, waves):
                            step.block_tables.cpu().numpy().reshape(-1), kwp["max_blocks"],
                            step.dec_seqs.cpu().numpy().reshape(-1, 4), n_decode)
     assert got == want, (hex(got), hex(want))
+
+
+def _random_step(seed: int):
+    """A random mixed step: 3-40 requests, each a decode (context 1-3000) or a prefill chunk
+    (2-200 rows on a 0-1000-token prefix, at most 4 of them), some sharing their first
+    pages with an earlier request's (full pages only, never appended to), page ids shuffled
+    over a pool with free pages between them."""
+    rng = np.random.default_rng(seed)
+    R = int(rng.integers(3, 41))
+    comp, new, tabs = [], [], []
+    n_pre = 0
+    for _ in range(R):
+        if n_pre < 4 and rng.random() < 0.25:
+            c = int(rng.integers(0, 1001)) if rng.random() < 0.6 else 0
+            n = int(rng.integers(2, 201))
+            n_pre += 1
+        else:
+            c = int(rng.integers(0, 3000))
+            n = 1
+        comp.append(c)
+        new.append(n)
+    need = [synth.cdiv(c + n, PAGE) for c, n in zip(comp, new)]
+    pool = int(sum(need) * 1.5) + 64
+    perm = rng.permutation(pool).astype(np.int32)
+    o = 0
+    for r in range(R):
+        t = perm[o:o + need[r]].copy()
+        o += need[r]
+        full = comp[r] // PAGE  # pages this request reads but never writes
+        if r > 0 and full > 0 and rng.random() < 0.3:
+            src = int(rng.integers(0, r))
+            k = min(full, comp[src] // PAGE)
+            if k > 0:
+                t[:k] = tabs[src][:k]
+        tabs.append(t)
+    return synth._assemble(f"random{seed}", comp, new, tabs, pool, 4096)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(6))
+def test_random_steps(gpu, seed):
+    """Random mixed steps (decode contexts, prefill prefixes and chunk lengths, shared
+    prefix pages, decode grid 16-2048 waves, minimum pages per wave, prefill tile) end to
+    end and kernel-only against the oracle; decode rows within one bf16 step."""
+    cfg = _random_step(seed)
+    rng = np.random.default_rng(1000 + seed)
+    waves = int(rng.choice([16, 256, 1024, 2048]))
+    min_pages = int(rng.choice([1, 2, 8]))
+    tile = int(rng.choice([32, 64]))
+    print(f"[test_random_steps] seed={seed} reqs={cfg.n_reqs} rows={cfg.rows} "
+          f"waves={waves} min_pages={min_pages} tile={tile}", flush=True)
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=waves, dec_min_pages=min_pages, pre_tile_q=tile)
+    _check_step(cfg, cfg, dict(kw, device=gpu), 500 + seed, f"random{seed}")
