@@ -179,6 +179,7 @@ __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* bt
   // compare runs on the VALU and needs a temporary register pair, which the allocator
   // may take from a page buffer still in flight (a full vmcnt drain)
   const uint32_t pool32 = (uint32_t)min(a.pool_pages, (long long)0x7fffffff);
+  // (pe > pb: a segment holds at least one page, so min(p, pe - 1) indexes the segment)
   auto load = [&](PageFrag& f, bool& ok, int p) {
     const bool live = p < pe;
     const int page = (p == pb && first_page >= 0) ? first_page : btc[min(p, pe - 1)];
