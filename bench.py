@@ -94,10 +94,12 @@ def main():
         bench_gemm(args)
         return
 
+    device = None if args.profile_kernels else device_info()
     line = run_config(args, args.config, steps=args.steps, warmup=args.warmup,
                       with_cpu=not args.no_cpu)
     if line is None:  # --profile-kernels
         return
+    line["device"] = device
     if args.config == 5 and not args.no_prefill_lines:
         # the metric's second half: prefill MFMA utilisation on the two prefill configs,
         # measured in the same process after config 5's pool is released
@@ -121,6 +123,31 @@ def main():
             torch.cuda.empty_cache()
         line["prefill"] = pre
     print(json.dumps(line))
+
+
+def device_info():
+    """The device's CU count and a measured device-to-device copy rate, beside the datasheet
+    peak the rooflines use: 1 GiB copied 10 times after 3 warm-up copies, HIP events on the
+    current stream, bytes counted as read + written."""
+    import torch
+
+    props = torch.cuda.get_device_properties(0)
+    n = 2**28  # fp32 elements: 1 GiB
+    x = torch.ones(n, device="cuda", dtype=torch.float32)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        y.copy_(x)
+    e1.record()
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3 / 10
+    del x, y
+    torch.cuda.empty_cache()
+    return {"name": props.name, "cus": props.multi_processor_count,
+            "copy_GBps": round(2 * n * 4 / sec / 1e9, 1), "copy_bytes": n * 4}
 
 
 def run_config(args, config, *, steps, warmup, with_cpu):
