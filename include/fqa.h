@@ -270,7 +270,10 @@ int fqa_store_kv(const fqa_dims* dims, const uint16_t* qkv, const int32_t* posit
  * log-sum-exp combine merges.  Output rows out[row] ([n_q_heads][head_dim] bf16, row
  * stride n_q_heads*head_dim).  `workspace` must hold
  * fqa_decode_workspace_bytes(dims, dec_wave_cap) bytes; n_reqs_bound bounds the
- * decode requests (combine grid). */
+ * decode requests (combine grid).  The split kernel runs 4 wavefronts per workgroup and
+ * reserves 120 KiB of LDS per workgroup, so each workgroup holds its CU alone while it
+ * runs: work queued on other streams meanwhile gets the CUs the decode does not hold.
+ * fqa_dec_default_waves sizes the plan to one workgroup per CU. */
 int fqa_decode(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
                int64_t pool_pages, const int32_t* block_tables, int32_t max_blocks,
                const int32_t* dec_waves, const int32_t* dec_seqs, const int32_t* meta,
