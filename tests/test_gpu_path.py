@@ -393,3 +393,33 @@ def test_random_steps(gpu, seed):
           f"waves={waves} min_pages={min_pages} tile={tile}", flush=True)
     kw = sc.pack_kwargs(cfg, dec_grid_waves=waves, dec_min_pages=min_pages, pre_tile_q=tile)
     _check_step(cfg, cfg, dict(kw, device=gpu), 500 + seed, f"random{seed}")
+
+
+@pytest.mark.gpu
+def test_decode_at_maximum_requests(gpu):
+    """FQA_MAX_REQS (2048) decode sequences of 1-200 keys on the default 1024-wave grid: each
+    wave walks many short streams (its segment loop reloads q and restarts the page
+    rotation per stream), the combine runs on its largest grid, and some sequences share
+    their first pages.  End to end and kernel-only against the oracle."""
+    from flashqwen_amd import _lib
+
+    rng = np.random.default_rng(4096)
+    R = _lib.FQA_MAX_REQS
+    L = rng.integers(1, 201, size=R)
+    need = [synth.cdiv(int(x), PAGE) for x in L]
+    pool = sum(need) + 1000
+    perm = rng.permutation(pool).astype(np.int32)
+    tabs, o = [], 0
+    for r in range(R):
+        t = perm[o:o + need[r]].copy()
+        o += need[r]
+        full = (int(L[r]) - 1) // PAGE
+        if r > 0 and full > 0 and rng.random() < 0.2:
+            src = int(rng.integers(0, r))
+            k = min(full, (int(L[src]) - 1) // PAGE)
+            t[:k] = tabs[src][:k]
+        tabs.append(t)
+    cfg = synth._assemble("max-reqs", L - 1, np.ones(R, np.int32), tabs, pool, 4096)
+    print(f"[test_decode_at_maximum_requests] R={R} keys={int(L.sum())}", flush=True)
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=1024, dec_min_pages=1)
+    _check_step(cfg, cfg, dict(kw, device=gpu), 2048, "max-reqs")
