@@ -45,7 +45,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--dec-grid-waves", type=int, default=None,
-                    help="decode wavefronts (default: CUs x 8)")
+                    help="decode wavefronts (default: CUs x 4, one per SIMD)")
     ap.add_argument("--dec-min-pages", type=int, default=8)
     ap.add_argument("--pre-tile-q", type=int, default=64, choices=[32, 64])
     ap.add_argument("--layers", type=int, default=None, help="config 5 only (default 36)")
