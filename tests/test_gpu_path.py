@@ -423,3 +423,50 @@ def test_decode_at_maximum_requests(gpu):
     print(f"[test_decode_at_maximum_requests] R={R} keys={int(L.sum())}", flush=True)
     kw = sc.pack_kwargs(cfg, dec_grid_waves=1024, dec_min_pages=1)
     _check_step(cfg, cfg, dict(kw, device=gpu), 2048, "max-reqs")
+
+
+@pytest.mark.gpu
+def test_invariant_under_page_relabelling_and_grid(gpu):
+    """Two invariances of the path on a random mixed step (decodes, prefill chunks, shared
+    prefix pages): relabelling every page id, with the pool's pages moved to match, leaves
+    the attention output and the appended K/V bit-identical (the kernels do the same loads
+    in the same order, only at other addresses); and the decode grid (where stream-K cuts
+    the streams) changes decode rows by fp32 merge order only: within one bf16 step."""
+    import torch
+
+    cfg = _random_step(45)  # 38 requests, 4 prefill chunks, shared prefix pages
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=1024, dec_min_pages=1)
+    kwp = {k: v for k, v in kw.items() if k != "device"}
+    rng = np.random.default_rng(9)
+    qkv_h = synth.rand_bf16(rng, (cfg.rows, QKV_STRIDE))
+    wq, wk = synth.norm_weights()
+    print(f"[test_invariant_under_page_relabelling_and_grid] reqs={cfg.n_reqs} rows={cfg.rows}",
+          flush=True)
+    pool = make_pool(cfg.pool_pages, 77, gpu)
+    base = pool.clone()
+    step, _q, out = gpu_chain(cfg, qkv_h, pool, wq, wk, gpu, kwp)
+    out_a, pool_a = _host_u16(out)[: cfg.rows], pool
+
+    # relabel: page p -> perm[p], and move the pool's pages with it
+    perm = np.random.default_rng(10).permutation(cfg.pool_pages).astype(np.int32)
+    cfg_b = synth._assemble("relabelled", cfg.computed, cfg.n_new,
+                            [perm[t] for t in cfg.tables()], cfg.pool_pages, cfg.max_ctx)
+    inv = np.empty_like(perm)
+    inv[perm] = np.arange(cfg.pool_pages, dtype=np.int32)
+    pool_b = base[:, torch.from_numpy(inv.astype(np.int64)).to(gpu)].contiguous()
+    step_b, _q, out_b = gpu_chain(cfg_b, qkv_h, pool_b, wq, wk, gpu, kwp)
+    assert np.array_equal(_host_u16(out_b)[: cfg.rows], out_a)
+    moved_back = pool_b[:, torch.from_numpy(perm.astype(np.int64)).to(gpu)]
+    assert torch.equal(moved_back.view(torch.int16), pool_a.view(torch.int16))
+
+    # other decode grids: decode rows within one bf16 step of the 1024-wave result
+    drows = step.cu_seqlens.cpu().numpy()[step.decode_rids.cpu().numpy()[
+        : int(step.meta.cpu().numpy()[1])]]
+    for waves in (7, 256, 3000):
+        kw_g = sc.pack_kwargs(cfg, dec_grid_waves=waves, dec_min_pages=1)
+        kwp_g = {k: v for k, v in kw_g.items() if k != "device"}
+        _s, _q, out_g = gpu_chain(cfg, qkv_h, base.clone(), wq, wk, gpu, kwp_g)
+        got = _host_u16(out_g)[: cfg.rows]
+        sc.assert_decode_rows_close(got[drows], out_a[drows], f"grid {waves}")
+        prow = np.setdiff1d(np.arange(cfg.rows), drows)
+        assert np.array_equal(got[prow], out_a[prow])  # prefill rows do not depend on it
