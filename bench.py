@@ -112,13 +112,14 @@ def main():
         pre = {}
         for c in (3, 4):
             sub = run_config(args, c, steps=max(args.steps, 20), warmup=args.warmup,
-                             with_cpu=False)
+                             with_cpu=not args.no_cpu)
             pre[f"config{c}"] = {"workload": sub["config"]["workload"],
                                  "ms_per_step": sub["ms_per_step"],
                                  "tokens_per_s": sub["value"],
                                  "rows_per_step": sub["config"]["rows_per_step"],
                                  "roofline": sub["roofline"],
-                                 "kernels_us": sub["kernels_us"]}
+                                 "kernels_us": sub["kernels_us"],
+                                 "cpu_baseline": sub["cpu_baseline"]}
             gc.collect()
             torch.cuda.empty_cache()
         line["prefill"] = pre
@@ -585,58 +586,107 @@ def _describe(n):
 
 
 def cpu_baseline(cfg, comp_sel, n_sel, T, seconds):
-    """The OpenMP fp32 oracle on the same step: pack + norm/rope/append + decode + prefill,
-    on one layer, repeated for about `seconds`; tokens/s = rows / time per step (x layers)."""
+    """The OpenMP fp32 oracle on the same step: (selection for a scheduled config) + pack +
+    norm/rope/append + decode + prefill, one layer, repeated for about `seconds` (at least 3
+    repetitions); tokens/s = rows / (time per step x layers).  Only the oracle's C calls
+    are timed: the q/k/v rows the append normalises in place are restored from a pristine
+    copy between repetitions outside the timer, and the pool is copied once, before the
+    first repetition (the append rewrites the same slots with the same values each time)."""
     from flashqwen_amd import synth
     from oracle import oracle as orc
     from tests import stepcase as sc
 
     sub = cfg
-    if cfg.num_tokens is not None:
+    scheduled = cfg.num_tokens is not None
+    if scheduled:
         sel_req, _ = orc.schedule(cfg.num_tokens, cfg.computed, cfg.token_budget,
                                   cfg.prefill_chunk)
         tabs = cfg.tables()
         sub = synth._assemble(cfg.name, comp_sel, n_sel, [tabs[i] for i in sel_req],
                               cfg.pool_pages, cfg.max_ctx)
+    # the pages the step reads, renumbered into a compact pool (shared pages stay shared):
+    # the oracle's time does not depend on where in the pool a page sits
     sample = "full step, one layer"
+    keep = list(range(len(sub.computed)))
     if cfg.name == "config5":
-        # a sample of 8 long and 24 shared-prefix sequences, re-paged into a compact pool
+        # a sample of 8 long and 24 shared-prefix sequences
         keep = list(range(8)) + list(range(32, 56))
-        sub, sample = _compact(cfg, keep), "8 of 32 long + 24 of 96 shared-prefix seqs, 1 layer"
+        sample = "8 of 32 long + 24 of 96 shared-prefix seqs, 1 layer"
+    sub = _compact(sub, keep)
     rng = np.random.default_rng(5)
     kw = sc.pack_kwargs(sub)
-    qkv = synth.rand_bf16(rng, (sub.rows, synth.QKV_STRIDE))
-    pool = synth.rand_bf16(rng, sc.pool_elems(sub.pool_pages))
+    qkv0 = synth.rand_bf16(rng, (sub.rows, synth.QKV_STRIDE))
+    # the pool: a 4M-value N(0,1) bf16 block tiled over the pages (the oracle's time does not
+    # depend on the values; drawing ~1e9 normals would take minutes)
+    block = synth.rand_bf16(rng, 1 << 22)
+    pool = np.resize(block, sc.pool_elems(sub.pool_pages))
     wq, wk = synth.norm_weights()
-    times = []
+    cos, sin = orc.rope_tables(sub.max_ctx)
+    parts = {k: [] for k in (["schedule"] if scheduled else []) +
+             ["pack", "qknorm_rope_append", "decode", "prefill"]}
+    totals = []
     t_end = time.perf_counter() + seconds
     while True:
+        q = qkv0.copy()  # untimed restore
+        out = np.zeros((max(sub.rows, 1), synth.N_Q * synth.HEAD_DIM), np.uint16)
+        tot = 0.0
+        if scheduled:
+            t0 = time.perf_counter()
+            orc.schedule(cfg.num_tokens, cfg.computed, cfg.token_budget, cfg.prefill_chunk)
+            dt = time.perf_counter() - t0
+            parts["schedule"].append(dt)
+            tot += dt
         t0 = time.perf_counter()
-        sc.oracle_chain(sub, qkv, pool, wq, wk, kw)
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() > t_end or len(times) >= 50:
+        pk = orc.pack(sub.computed, sub.n_new, sub.bt_off, sub.bt_pages, **kw)
+        dt = time.perf_counter() - t0
+        parts["pack"].append(dt)
+        tot += dt
+        Tn = int(pk["meta"][0])
+        t0 = time.perf_counter()
+        orc.qknorm_rope_append(q, wq, wk, cos, sin, pk["positions"], pk["slot_mapping"], Tn,
+                               pool, sub.pool_pages)
+        dt = time.perf_counter() - t0
+        parts["qknorm_rope_append"].append(dt)
+        tot += dt
+        t0 = time.perf_counter()
+        orc.decode(q, pool, sub.pool_pages, pk["block_tables"], kw["max_blocks"],
+                   pk["cu_seqlens"], pk["positions"], pk["decode_rids"], int(pk["meta"][1]), out)
+        dt = time.perf_counter() - t0
+        parts["decode"].append(dt)
+        tot += dt
+        t0 = time.perf_counter()
+        orc.prefill(q, pool, sub.pool_pages, pk["block_tables"], kw["max_blocks"],
+                    pk["cu_seqlens"], pk["positions"], pk["prefill_rids"], int(pk["meta"][2]),
+                    out)
+        dt = time.perf_counter() - t0
+        parts["prefill"].append(dt)
+        tot += dt
+        totals.append(tot)
+        if (time.perf_counter() > t_end and len(totals) >= 3) or len(totals) >= 50:
             break
-    per = float(np.median(times))
+    per = float(np.median(totals))
     rows = sub.rows
-    if cfg.name == "config5":
-        value = rows / (per * cfg.layers)
+    value = rows / (per * cfg.layers)
+    if cfg.layers > 1:
         sample += f"; x{cfg.layers} layers extrapolated"
-    else:
-        value = rows / (per * cfg.layers)
     return {"value": round(value, 2), "unit": "tokens/s", "cores": orc.num_threads(),
-            "kind": "port", "sample": f"{sample}; {len(times)} reps, median {per * 1e3:.1f} ms",
+            "kind": "port",
+            "sample": f"{sample}; {len(totals)} reps, median {per * 1e3:.1f} ms of oracle C "
+                      "calls only (input restores and copies outside the timer)",
+            "parts_ms": {k: round(float(np.median(v)) * 1e3, 3) for k, v in parts.items()},
             "nproc": os.cpu_count()}
 
 
 def _compact(cfg, keep):
-    """Subset of config 5's sequences with their pages renumbered into a small pool (shared
-    prefix pages stay shared)."""
+    """The requests `keep` of a step with their pages (the new tokens' pages included)
+    renumbered into a small pool; pages shared between requests stay shared."""
     from flashqwen_amd import synth
 
-    tabs = [cfg.tables()[i] for i in keep]
+    all_tabs = cfg.tables()
+    tabs = [all_tabs[i] for i in keep]
     uniq = {p: i for i, p in enumerate(dict.fromkeys(np.concatenate(tabs).tolist()))}
     new = [np.array([uniq[p] for p in tb], np.int32) for tb in tabs]
-    return synth._assemble(cfg.name, cfg.computed[keep], cfg.n_new[keep], new, len(uniq),
+    return synth._assemble(cfg.name, cfg.computed[keep], cfg.n_new[keep], new, max(len(uniq), 1),
                            cfg.max_ctx, layers=cfg.layers)
 
 

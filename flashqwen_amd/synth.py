@@ -181,8 +181,9 @@ CONFIGS = {1: config1, 2: config2, 3: config3, 4: config4, 5: config5}
 def rand_bf16(rng: np.random.Generator, shape) -> np.ndarray:
     """N(0,1) samples rounded to bf16 (RNE); returned as uint16 bit patterns."""
     x = rng.standard_normal(shape, dtype=np.float32)
-    u = x.view(np.uint32).astype(np.uint64)
-    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    u = x.view(np.uint32)
+    # finite float32 bit patterns stay below 2^32 - 2^16, so the sum cannot wrap
+    u = (u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)
     return u.astype(np.uint16)
 
 
