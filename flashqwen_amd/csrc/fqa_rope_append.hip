@@ -12,14 +12,14 @@
 // halves of every rotate-half pair sit in one lane and RoPE needs no data exchange; the
 // sum of squares is a 16-lane butterfly.  q is written back in place, k into its page.
 // V goes into the V^T [dim][16 tokens] rows of the page.  When 16 consecutive rows fill
-// one page (every full page of a prefill), the page's first row writes the whole page:
-// per kv head each lane reads one 4-byte word (2 dims) of each of the 16 rows, transposes
-// in registers (v_perm) and stores its two 32-byte V^T rows, so the 4 KiB go out as
-// contiguous 16-byte stores; the other 15 rows skip V.  Rows of a partly filled page
-// (decode rows, the ends of a chunk) write their column with 2-byte stores, split over
-// the W waves; those must meet in one L2 before the line goes to HBM: workgroup b runs
-// on XCD b % 8 and rows are dealt to XCDs in contiguous ranges, so a page's rows (except
-// where a range ends) go through the same XCD's L2.
+// one page (every full page of a prefill), the page's 16 rows share its V^T: row tok
+// reads 2 dims x 8 tokens per lane of kv head tok/2's half tok%2 (64 dims of 16 rows),
+// transposes in registers (v_perm) and stores 16-byte pieces of V^T rows, so each row
+// moves 1 KiB of V and the page goes out as contiguous 16-byte stores.  Rows of a partly
+// filled page (decode rows, the ends of a chunk) write their column with 2-byte stores,
+// split over the W waves; those must meet in one L2 before the line goes to HBM:
+// workgroup b runs on XCD b % 8 and rows are dealt to XCDs in contiguous ranges, so a
+// page's rows (except where a range ends) go through the same XCD's L2.
 // Memory-bound: per row 12 KiB read, 8 KiB (q) + 4 KiB (k, v) written.
 //
 // fqa_qkv_proj_append runs the same kernel on the QKV projection's split-K partials
@@ -195,28 +195,25 @@ __global__ void __launch_bounds__(256) qknorm_rope_append_kernel(AppendArgs a) {
            a.positions[lead] >= 0 && a.positions[lead + kPage - 1] < a.rope_max_pos;
   }
   if (full) {
-    if (tok != 0) return;  // the page's first row writes it
-    // kv heads sw*NKV ..: lane -> dims 2*lane, 2*lane+1 of all 16 tokens
+    // The page's 16 rows share its V^T: row tok moves kv head tok/2, dims 64*(tok%2) ..
+    // +63, for all 16 tokens (one wave of the row: the first).  Lane l holds dims
+    // d = 64*(tok%2) + 2*(l%32), d+1 of tokens 8*(l/32) .. +7, transposes them in
+    // registers (v_perm) and stores two 16-byte pieces of V^T rows d and d+1.
+    if (sw != 0) return;
+    const int kvh = tok >> 1, d = 64 * (tok & 1) + 2 * (lane & 31), t0 = 8 * (lane >> 5);
+    uint32_t x[8];
 #pragma unroll
-    for (int hv = 0; hv < NKV; ++hv) {
-      const int kvh = sw * NKV + hv;
-      if (kvh >= kHkv) break;
-      uint32_t x[kPage];
+    for (int t = 0; t < 8; ++t)
+      x[t] = load2<kPart>(a, (long long)lead + t0 + t, (kHq + kHkv + kvh) * kD + d);
+    uint32_t y0[4], y1[4];  // dim d / d+1, tokens t0+2k, t0+2k+1
 #pragma unroll
-      for (int t = 0; t < kPage; ++t)
-        x[t] = load2<kPart>(a, (long long)row + t, (kHq + kHkv + kvh) * kD + 2 * lane);
-      uint32_t y0[8], y1[8];  // dim 2*lane / 2*lane+1, tokens 2k, 2k+1
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        y0[k] = __builtin_amdgcn_perm(x[2 * k + 1], x[2 * k], 0x05040100u);
-        y1[k] = __builtin_amdgcn_perm(x[2 * k + 1], x[2 * k], 0x07060302u);
-      }
-      uint4* vt = reinterpret_cast<uint4*>(a.pool + run_offset(page, kvh) + kVOff + 2 * lane * kPage);
-      vt[0] = make_uint4(y0[0], y0[1], y0[2], y0[3]);
-      vt[1] = make_uint4(y0[4], y0[5], y0[6], y0[7]);
-      vt[2] = make_uint4(y1[0], y1[1], y1[2], y1[3]);
-      vt[3] = make_uint4(y1[4], y1[5], y1[6], y1[7]);
+    for (int k = 0; k < 4; ++k) {
+      y0[k] = __builtin_amdgcn_perm(x[2 * k + 1], x[2 * k], 0x05040100u);
+      y1[k] = __builtin_amdgcn_perm(x[2 * k + 1], x[2 * k], 0x07060302u);
     }
+    uint16_t* vt = a.pool + run_offset(page, kvh) + kVOff + d * kPage + t0;
+    *reinterpret_cast<uint4*>(vt) = make_uint4(y0[0], y0[1], y0[2], y0[3]);
+    *reinterpret_cast<uint4*>(vt + kPage) = make_uint4(y1[0], y1[1], y1[2], y1[3]);
     return;
   }
   // Partly filled page: v heads sw*NKV .. : lane -> (kv head, DPL consecutive dims)
@@ -267,9 +264,9 @@ int append_launch(const fqa_dims* dims, uint16_t* qkv, const float* q_norm_w,
   if (!qkv || !positions || (norm && (!q_norm_w || !k_norm_w || !cos_tab || !sin_tab)) ||
       (store && (!slot_mapping || !pool)))
     return FQA_EINVAL;
-  // Heads per lane group: 1 (10 waves per row) for decode-sized steps, 10 (one wave per
-  // row) for prefill-sized ones; measured crossover between.
-  const int hpg = rows_bound <= 512 ? 1 : (rows_bound <= 2048 ? 2 : 10);
+  // Heads per lane group: 1 (10 waves per row) for decode-sized steps, 2 (5 waves per row)
+  // above 512 rows (measured at 8192 rows: 2 took 31.9 us, 5 32.3, 10 35.2, 1 39.2).
+  const int hpg = rows_bound <= 512 ? 1 : 2;
   const long long waves = (long long)rows_bound * (10 / hpg);
   const int blocks = (int)((waves + kWavesPerBlock - 1) / kWavesPerBlock);
   const int blocks_per_xcd = (blocks + 7) / 8;
