@@ -70,43 +70,34 @@ struct Stats {
   int v[6];  // code (min), rows (sum), dpages (sum), dmax (max), qmax (max), overflow (max)
 };
 
-__device__ Stats block_reduce_stats(Stats v, Stats* sh) {
-  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
-  Stats r;
-  r.v[0] = wave_extreme<false>(v.v[0], INT_MAX);
-  r.v[1] = __builtin_amdgcn_readlane(wave_incl_scan(v.v[1]), 63);
-  r.v[2] = __builtin_amdgcn_readlane(wave_incl_scan(v.v[2]), 63);
-  r.v[3] = wave_extreme<true>(v.v[3], 0);
-  r.v[4] = wave_extreme<true>(v.v[4], 1);
-  r.v[5] = wave_extreme<true>(v.v[5], 0);
-  if (lane == 0) sh[w] = r;
-  lds_sync();
-  const bool have = lane < kPackWaves;
-  const Stats o = sh[have ? lane : 0];
-  r.v[0] = wave_extreme<false>(have ? o.v[0] : INT_MAX, INT_MAX);
-  r.v[1] = __builtin_amdgcn_readlane(wave_incl_scan(have ? o.v[1] : 0), 63);
-  r.v[2] = __builtin_amdgcn_readlane(wave_incl_scan(have ? o.v[2] : 0), 63);
-  r.v[3] = wave_extreme<true>(have ? o.v[3] : 0, 0);
-  r.v[4] = wave_extreme<true>(have ? o.v[4] : 1, 1);
-  r.v[5] = wave_extreme<true>(have ? o.v[5] : 0, 0);
-  lds_sync();
-  return r;
-}
-
 struct Counts {
   int v[5];
 };
 
-// Exclusive scans of 5 values over the workgroup; *total gets the 5 sums.
-__device__ Counts block_excl_scan5(const Counts& in, Counts* sh, Counts* total) {
+// Exclusive scans of 5 values over the workgroup (*total gets the 5 sums) and, when
+// `stats` (wave-uniform), the reduction of every thread's Stats into *st, in one LDS
+// exchange: the wave-level DPP scans and reductions of all 11 values first, then one
+// barrier, the second level, and a closing barrier.
+__device__ Counts block_scan5_stats(const Counts& in, Counts* total, Stats* st, bool stats,
+                                    Counts* shc, Stats* shs) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
   Counts incl;
 #pragma unroll
   for (int k = 0; k < 5; ++k) incl.v[k] = wave_incl_scan(in.v[k]);
-  if (lane == kWave - 1) sh[w] = incl;
+  Stats r;
+  if (stats) {
+    r.v[0] = wave_extreme<false>(st->v[0], INT_MAX);
+    r.v[1] = __builtin_amdgcn_readlane(wave_incl_scan(st->v[1]), 63);
+    r.v[2] = __builtin_amdgcn_readlane(wave_incl_scan(st->v[2]), 63);
+    r.v[3] = wave_extreme<true>(st->v[3], 0);
+    r.v[4] = wave_extreme<true>(st->v[4], 1);
+    r.v[5] = wave_extreme<true>(st->v[5], 0);
+    if (lane == 0) shs[w] = r;
+  }
+  if (lane == kWave - 1) shc[w] = incl;
   lds_sync();
   const bool have = lane < kPackWaves;
-  const Counts o = sh[have ? lane : 0];
+  const Counts o = shc[have ? lane : 0];
   Counts out;
 #pragma unroll
   for (int k = 0; k < 5; ++k) {
@@ -114,6 +105,16 @@ __device__ Counts block_excl_scan5(const Counts& in, Counts* sh, Counts* total) 
     total->v[k] = __builtin_amdgcn_readlane(sc, kPackWaves - 1);
     const int below = __builtin_amdgcn_readlane(sc, w == 0 ? 0 : w - 1);
     out.v[k] = (w == 0 ? 0 : below) + incl.v[k] - in.v[k];
+  }
+  if (stats) {
+    const Stats so = shs[have ? lane : 0];
+    r.v[0] = wave_extreme<false>(have ? so.v[0] : INT_MAX, INT_MAX);
+    r.v[1] = __builtin_amdgcn_readlane(wave_incl_scan(have ? so.v[1] : 0), 63);
+    r.v[2] = __builtin_amdgcn_readlane(wave_incl_scan(have ? so.v[2] : 0), 63);
+    r.v[3] = wave_extreme<true>(have ? so.v[3] : 0, 0);
+    r.v[4] = wave_extreme<true>(have ? so.v[4] : 1, 1);
+    r.v[5] = wave_extreme<true>(have ? so.v[5] : 0, 0);
+    *st = r;
   }
   lds_sync();
   return out;
@@ -144,15 +145,15 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   __shared__ int s_btoff[FQA_MAX_REQS + 1];
   __shared__ int s_decidx[FQA_MAX_REQS + 1];
   __shared__ int s_preidx[FQA_MAX_REQS + 1];
-  __shared__ int s_decit[FQA_MAX_REQS + 1];  // exclusive prefix of decode pages
   __shared__ int s_dstart[FQA_MAX_REQS + 1];  // by decode index: 8 * page prefix
   __shared__ int s_dpages[FQA_MAX_REQS];      // by decode index: pages
   __shared__ int s_drid[FQA_MAX_REQS];        // by decode index: request
   __shared__ int s_dflag[FQA_MAX_REQS];       // by decode index: first page id, then the flag
+  __shared__ int s_prer[FQA_MAX_REQS];        // by prefill index: request
+  __shared__ int s_pit[FQA_MAX_REQS + 1];     // by prefill index: first item
   __shared__ int s_hkey[kHashSlots];          // first page ids of decode sequences
   __shared__ int s_hcnt[kHashSlots];          // ... and how many sequences start there
-  __shared__ int s_preit[FQA_MAX_REQS + 1];
-  __shared__ Stats s_stats[kPackWaves];  // (Stats now has 6 fields)
+  __shared__ Stats s_stats[kPackWaves];
   __shared__ Counts s_counts[kPackWaves];
   __shared__ int sh32[kPackWaves];
 
@@ -162,37 +163,94 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   if (R < 0) R = 0;
   const int QT = a.c.pre_tile_q;
   const int maxb = a.c.max_blocks;
+  // the shared-prefix hash starts empty (published by the scan's barriers)
+  for (int i = tid; i < kHashSlots; i += kPackThreads) {
+    s_hkey[i] = -1;
+    s_hcnt[i] = 0;
+  }
 
-  // ---- pass 1: load, structural checks, totals ---------------------------------
+  // ---- per request: load, structural checks, totals, and the five exclusive scans
+  // (rows, decode / prefill indices, decode pages, prefill items), one pass per 1024
+  // requests; the totals are reduced with the last pass's scans -------------------------
   Stats st = {{INT_MAX, 0, 0, 0, 1, 0}};
-  for (int r = tid; r < R; r += kPackThreads) {
-    const int c = a.b.computed[r], n = a.b.n_new[r];
-    const int o0 = a.b.bt_off[r], o1 = a.b.bt_off[r + 1];
-    s_comp[r] = c;
-    s_n[r] = n;
-    s_btoff[r] = o0;
-    int cc = 0;
-    if (c < 0 || n < 0) cc = FQA_PACK_NEGATIVE;
-    else {
-      const int nb = o1 - o0;
-      if (nb < cdiv((long long)c + n, kPage)) cc = FQA_PACK_SHORT_TABLE;
-      else if (nb > maxb) cc = FQA_PACK_WIDE_TABLE;
-      st.v[1] = min(st.v[1] + min(n, kPartCap), kPartCap + 1);
+  Counts carry = {{0, 0, 0, 0, 0}};
+  const int bt_end = a.b.bt_off[R];  // issued with the first loads, not after the scans
+  for (int base = 0; base < R; base += kPackThreads) {
+    const int r = base + tid;
+    Counts v = {{0, 0, 0, 0, 0}};
+    // Loads at a clamped index, not under the lane condition: a conditional load is
+    // waited for where its value merges with the default.
+    const int rc = r < R ? r : R - 1;
+    int c = a.b.computed[rc], n = a.b.n_new[rc], o0 = a.b.bt_off[rc];
+    const int o1 = a.b.bt_off[rc + 1];
+    // a decode sequence's first page id, for the shared-prefix check below (in flight
+    // across the scan's barriers; other lanes re-read their own table offset)
+    const int first = *(n == 1 && o0 >= 0 && o1 > o0 ? a.b.bt_pages + o0 : a.b.bt_off + rc);
+    if (r >= R) c = n = o0 = 0;
+    if (r < R) {
+      int cc = 0;
+      if (c < 0 || n < 0) cc = FQA_PACK_NEGATIVE;
+      else {
+        const int nb = o1 - o0;
+        if (nb < cdiv((long long)c + n, kPage)) cc = FQA_PACK_SHORT_TABLE;
+        else if (nb > maxb) cc = FQA_PACK_WIDE_TABLE;
+        st.v[1] = min(st.v[1] + min(n, kPartCap), kPartCap + 1);
+        if (n == 1) {
+          const int pg = c / kPage + 1;
+          st.v[2] = min(st.v[2] + min(pg, kPartCap), kPartCap + 1);
+          st.v[3] = max(pg, st.v[3]);
+        } else {
+          st.v[4] = max(n, st.v[4]);
+        }
+      }
+      if (cc) st.v[0] = min(st.v[0], cc);
+      v.v[0] = n;
+      v.v[1] = n == 1;
+      v.v[2] = n != 1;
+      v.v[3] = n == 1 ? c / kPage + 1 : 0;  // pages of a decode stream
+      v.v[4] = n != 1 ? (n + QT - 1) / QT : 0;
+    }
+    const bool last = base + kPackThreads >= R;
+    if (last) st.v[5] = st.v[2] > kPartCap;
+    Counts tot;
+    const Counts e = block_scan5_stats(v, &tot, &st, last, s_counts, s_stats);
+    if (r < R) {
+      s_comp[r] = c;
+      s_n[r] = n;
+      s_btoff[r] = o0;
+      const int qs = carry.v[0] + e.v[0], di = carry.v[1] + e.v[1];
+      const int pi = carry.v[2] + e.v[2];
+      s_qstart[r] = qs;
+      s_decidx[r] = di;
+      s_preidx[r] = pi;
       if (n == 1) {
-        const int pg = c / kPage + 1;
-        st.v[2] = min(st.v[2] + min(pg, kPartCap), kPartCap + 1);
-        st.v[3] = max(pg, st.v[3]);
+        s_dstart[di] = 8 * (carry.v[3] + e.v[3]);
+        s_dpages[di] = c / kPage + 1;
+        s_drid[di] = r;
+        s_dflag[di] = first;
       } else {
-        st.v[4] = max(n, st.v[4]);
+        s_prer[pi] = r;
+        s_pit[pi] = carry.v[4] + e.v[4];
       }
     }
-    if (cc) st.v[0] = min(st.v[0], cc);
+#pragma unroll
+    for (int k = 0; k < 5; ++k) carry.v[k] += tot.v[k];
   }
-  st.v[5] = st.v[2] > kPartCap;
-  if (tid == 0) s_btoff[R] = a.b.bt_off[R];
-  st = block_reduce_stats(st, s_stats);
+  const int nd = carry.v[1], np = carry.v[2], npi = carry.v[4];
+  // decode plan: W page runs (8 kv heads x pages) cut into G equal shares
+  const int dpages = st.v[2];
+  const long long W = 8LL * dpages;
+  if (tid == 0) {
+    s_btoff[R] = bt_end;
+    s_qstart[R] = carry.v[0];
+    s_decidx[R] = nd;
+    s_preidx[R] = np;
+    s_dstart[nd] = (int)W;
+    s_pit[np] = npi;
+  }
+  lds_sync();
   int code = st.v[0];
-  const int rows = st.v[1], dpages = st.v[2], qmax = st.v[4];
+  const int rows = st.v[1], qmax = st.v[4];
   if (rows > a.c.max_rows && code > FQA_PACK_ROWS) code = FQA_PACK_ROWS;
   if (code == INT_MAX && st.v[5]) code = FQA_PACK_ITEMS;  // decode pages beyond the plan's range
   if (code != INT_MAX) {
@@ -203,20 +261,65 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   const int T = rows;
   const int gtid = blockIdx.x * kPackThreads + tid;
   const int gsz = gridDim.x * kPackThreads;
-
-  // ---- padded block tables: they need only the table offsets, so their loads and
-  // stores go out before the scans (whose barriers leave global accesses in flight) ----
-  {
-    const int total = R * maxb;  // < 2^31: R <= 2048, max_blocks <= 2^19
-    for (int e = gtid; e < total; e += gsz) {
-      const int r = e / maxb, g = e - r * maxb;
-      int nb = s_btoff[r + 1] - s_btoff[r];
-      a.o.block_tables[e] = g < nb ? a.b.bt_pages[s_btoff[r] + g] : -1;
-    }
+  int G = 0;
+  if (W > 0) {
+    const int minp = a.c.dec_min_pages > 0 ? a.c.dec_min_pages : 1;
+    G = (int)min((long long)a.c.dec_grid_waves, (W + minp - 1) / minp);
   }
-  // ---- workgroup 0: the first chunk of the page-id range check is loaded now and
-  // checked at the end (16-byte loads, kPgVec per thread; the scalar head and tail are
-  // the at most 3 ids on either side of 16-byte alignment) ----------------------------
+  if (G > a.c.dec_wave_cap || npi > a.c.pre_item_cap || dpages > INT_MAX / 8) {
+    if (blockIdx.x == 0 && tid < FQA_META_LEN)
+      a.o.meta[tid] = tid == FQA_META_STATUS ? FQA_PACK_ITEMS : (tid == FQA_META_REQS ? R : 0);
+    return;
+  }
+
+  // ---- the first iteration's page-id loads of rows, decode waves and block tables go
+  // out together; the LDS-only work below (shared-prefix hash, item ranks) runs while
+  // they are in flight, and their stores follow -------------------------------------------
+  auto row_of = [&](int t, int& r, int& p) {
+    r = upper_index(s_qstart, R, t);
+    p = s_comp[r] + (t - s_qstart[r]);
+  };
+  auto wave_of = [&](int w, int& di, int& kvh, int& page, int& n, int& r) {
+    const long long g0 = (long long)w * W / G, g1 = (long long)(w + 1) * W / G;
+    di = upper_index(s_dstart, nd, (int)g0);
+    const int rem = (int)g0 - s_dstart[di], pg = s_dpages[di];
+    kvh = rem / pg;
+    page = rem % pg;
+    n = (int)(g1 - g0);
+    r = s_drid[di];
+  };
+  auto bt_of = [&](int e, int& r, int& g) {
+    r = e / maxb;
+    g = e - r * maxb;
+  };
+  auto store_row = [&](int t, int r, int p, int page) {
+    a.o.positions[t] = p;
+    a.o.row_req[t] = r;
+    a.o.slot_mapping[t] = page * kPage + p % kPage;
+  };
+  auto store_wave = [&](int w, int di, int kvh, int page, int n, int r, int id) {
+    int4* dst = reinterpret_cast<int4*>(a.o.dec_waves + 8 * (long long)w);
+    dst[0] = make_int4(di, kvh, page, n);
+    dst[1] = make_int4(r, s_qstart[r], (s_comp[r] + 1) | s_dflag[di], id);
+  };
+  const int bt_total = R * maxb;  // < 2^31: R <= 2048, max_blocks <= 2^19
+  int r0 = 0, p0 = 0, page0 = 0, di1 = 0, kvh1 = 0, pg1 = 0, n1 = 0, r1 = 0, id1 = 0, bt0 = -1;
+  if (gtid < T) {
+    row_of(gtid, r0, p0);
+    page0 = a.b.bt_pages[s_btoff[r0] + p0 / kPage];
+  }
+  if (gtid < G) {
+    wave_of(gtid, di1, kvh1, pg1, n1, r1);
+    id1 = a.b.bt_pages[s_btoff[r1] + pg1];
+  }
+  if (gtid < bt_total) {
+    int r, g;
+    bt_of(gtid, r, g);
+    if (g < s_btoff[r + 1] - s_btoff[r]) bt0 = a.b.bt_pages[s_btoff[r] + g];
+  }
+  // workgroup 0: the first chunk of the page-id range check (16-byte loads, kPgVec per
+  // thread; the scalar head and tail are the at most 3 ids on either side of 16-byte
+  // alignment), checked at the end
   constexpr int kPgVec = 12;
   const int32_t* pg = a.b.bt_pages + s_btoff[0];
   const int npages = s_btoff[R] - s_btoff[0];
@@ -237,90 +340,28 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     pg_tail_id = pg[max(min(pg_lead + 4 * pg_nvec + tid, npages - 1), 0)];
   }
 
-  // decode plan: W page runs (8 kv heads x pages) cut into G equal shares
-  const long long W = 8LL * dpages;
-  int G = 0;
-  if (W > 0) {
-    const int minp = a.c.dec_min_pages > 0 ? a.c.dec_min_pages : 1;
-    G = (int)min((long long)a.c.dec_grid_waves, (W + minp - 1) / minp);
-  }
-
-  // ---- pass 2: exclusive scans over requests ------------------------------------
-  {
-    Counts carry = {{0, 0, 0, 0, 0}};
-    for (int base = 0; base < R; base += kPackThreads) {
-      const int r = base + tid;
-      Counts v = {{0, 0, 0, 0, 0}};
-      if (r < R) {
-        const int n = s_n[r];
-        v.v[0] = n;
-        v.v[1] = n == 1;
-        v.v[2] = n != 1;
-        v.v[3] = n == 1 ? s_comp[r] / kPage + 1 : 0;  // pages of a decode stream
-        v.v[4] = n != 1 ? (n + QT - 1) / QT : 0;
+  // ---- decode sequences whose first page starts another decode sequence too (a shared
+  // prefix): FQA_DEC_SHARED in their n_keys fields.  Page ids are hashed into LDS. -------
+  auto slot_of = [](int id) { return (int)(((uint32_t)id * 2654435761u) >> 20) & (kHashSlots - 1); };
+  if (nd > 1) {
+    for (int d = tid; d < nd; d += kPackThreads) {
+      const int id = s_dflag[d];
+      if (id < 0) continue;  // not a page (flagged by the range check): never shared
+      int h = slot_of(id);
+      for (int probe = 0; probe < kHashSlots; ++probe, h = (h + 1) & (kHashSlots - 1)) {
+        const int prev = atomicCAS(&s_hkey[h], -1, id);
+        if (prev == -1 || prev == id) {
+          atomicAdd(&s_hcnt[h], 1);
+          break;
+        }
       }
-      Counts tot;
-      const Counts e = block_excl_scan5(v, s_counts, &tot);
-      if (r < R) {
-        s_qstart[r] = carry.v[0] + e.v[0];
-        s_decidx[r] = carry.v[1] + e.v[1];
-        s_preidx[r] = carry.v[2] + e.v[2];
-        s_decit[r] = carry.v[3] + e.v[3];
-        s_preit[r] = carry.v[4] + e.v[4];
-      }
-#pragma unroll
-      for (int k = 0; k < 5; ++k) carry.v[k] += tot.v[k];
-    }
-    if (tid == 0) {
-      s_qstart[R] = carry.v[0];
-      s_decidx[R] = carry.v[1];
-      s_preidx[R] = carry.v[2];
-      s_decit[R] = carry.v[3];
-      s_preit[R] = carry.v[4];
     }
     lds_sync();
   }
-  const int nd = s_decidx[R], np = s_preidx[R];
-  const int npi = s_preit[R];
-  if (G > a.c.dec_wave_cap || npi > a.c.pre_item_cap || dpages > INT_MAX / 8) {
-    if (blockIdx.x == 0 && tid < FQA_META_LEN)
-      a.o.meta[tid] = tid == FQA_META_STATUS ? FQA_PACK_ITEMS : (tid == FQA_META_REQS ? R : 0);
-    return;
-  }
-  // decode streams by decode index: start of (di, kv head 0) and pages
-  for (int r = tid; r < R; r += kPackThreads)
-    if (s_n[r] == 1) {
-      s_dstart[s_decidx[r]] = 8 * s_decit[r];
-      s_dpages[s_decidx[r]] = s_comp[r] / kPage + 1;
-      s_drid[s_decidx[r]] = r;
-    }
-  if (tid == 0) s_dstart[nd] = (int)W;
-  // ---- decode sequences whose first page starts another decode sequence too (a shared
-  // prefix): FQA_DEC_SHARED in their n_keys fields.  Page ids are hashed into LDS. -------
-  for (int i = tid; i < kHashSlots; i += kPackThreads) {
-    s_hkey[i] = -1;
-    s_hcnt[i] = 0;
-  }
-  auto slot_of = [](int id) { return (int)(((uint32_t)id * 2654435761u) >> 20) & (kHashSlots - 1); };
-  lds_sync();
-  for (int d = tid; d < nd; d += kPackThreads) {
-    const int id = a.b.bt_pages[s_btoff[s_drid[d]]];  // a decode sequence has >= 1 page
-    s_dflag[d] = id;
-    if (id < 0) continue;  // not a page (flagged by the range check): never shared
-    int h = slot_of(id);
-    for (int probe = 0; probe < kHashSlots; ++probe, h = (h + 1) & (kHashSlots - 1)) {
-      const int prev = atomicCAS(&s_hkey[h], -1, id);
-      if (prev == -1 || prev == id) {
-        atomicAdd(&s_hcnt[h], 1);
-        break;
-      }
-    }
-  }
-  lds_sync();
   for (int d = tid; d < nd; d += kPackThreads) {
     const int id = s_dflag[d];
     int shared = 0;
-    if (id >= 0) {
+    if (id >= 0 && nd > 1) {
       int h = slot_of(id);
       for (int probe = 0; probe < kHashSlots; ++probe, h = (h + 1) & (kHashSlots - 1))
         if (s_hkey[h] == id) {
@@ -330,47 +371,52 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     }
     s_dflag[d] = shared ? FQA_DEC_SHARED : 0;
   }
-  lds_sync();
 
-  // ---- rows (positions, request index, slot mapping) and decode wave shares (where
-  // share w = [w*W/G, (w+1)*W/G) starts): the page-id loads of both loops' first
-  // iteration are issued before any of their stores ------------------------------------
-  auto row_of = [&](int t, int& r, int& p) {
-    r = upper_index(s_qstart, R, t);
-    p = s_comp[r] + (t - s_qstart[r]);
-  };
-  auto wave_of = [&](int w, int& di, int& kvh, int& page, int& n, int& r) {
-    const long long g0 = (long long)w * W / G, g1 = (long long)(w + 1) * W / G;
-    di = upper_index(s_dstart, nd, (int)g0);
-    const int rem = (int)g0 - s_dstart[di], pg = s_dpages[di];
-    kvh = rem / pg;
-    page = rem % pg;
-    n = (int)(g1 - g0);
-    r = s_drid[di];
-  };
-  auto store_row = [&](int t, int r, int p, int page) {
-    a.o.positions[t] = p;
-    a.o.row_req[t] = r;
-    a.o.slot_mapping[t] = page * kPage + p % kPage;
-  };
-  auto store_wave = [&](int w, int di, int kvh, int page, int n, int r, int id) {
-    int4* dst = reinterpret_cast<int4*>(a.o.dec_waves + 8 * (long long)w);
-    dst[0] = make_int4(di, kvh, page, n);
-    dst[1] = make_int4(r, s_qstart[r], (s_comp[r] + 1) | s_dflag[di], id);
-  };
+  // ---- prefill items, sorted by key count descending (stable) --------------------
+  // Tile t of prefill request r covers rows [t*QT, min((t+1)*QT, n)) and needs
+  // c + min((t+1)*QT, n) keys, so per request the number of tiles with more keys than X
+  // (and with exactly X) has a closed form; an item's rank is a sum over the prefill
+  // requests.  A group of S lanes (S = np rounded up to a power of two, at most 64) per
+  // item, its lanes splitting the prefill requests; QT is a power of two.
   {
-    int r0 = 0, p0 = 0, page0 = 0, di1 = 0, kvh1 = 0, pg1 = 0, n1 = 0, r1 = 0, id1 = 0;
-    if (gtid < T) {
-      row_of(gtid, r0, p0);
-      page0 = a.b.bt_pages[s_btoff[r0] + p0 / kPage];
+    const int lane = tid & (kWave - 1), wv = tid >> 6;
+    const int S = np >= 64 ? 64 : (np <= 1 ? 1 : 1 << (32 - __builtin_clz(np - 1)));
+    const int per_wave = kWave / S, sub = lane / S, sl = lane % S;
+    const int qsh = QT == 32 ? 5 : (QT == 64 ? 6 : 7);
+    const int stride = gridDim.x * kPackWaves * per_wave;
+    for (int i0 = (blockIdx.x * kPackWaves + wv) * per_wave; i0 < npi; i0 += stride) {
+      const int i = i0 + sub;
+      const bool live = i < npi;
+      const int k = live ? upper_index(s_pit, np, i) : 0;  // the prefill owning item i
+      const int r = s_prer[k];
+      const int t = i - s_pit[k];
+      const int n = s_n[r], c = s_comp[r];
+      const int q0 = t * QT, q1 = min(q0 + QT, n);
+      const int X = c + q1;
+      int rank = 0;
+      for (int kk = sl; kk < np && live; kk += S) {
+        const int nt = s_pit[kk + 1] - s_pit[kk];
+        if (nt == 0) continue;  // empty prefill
+        const int rr = s_prer[kk];
+        const int cc = s_comp[rr], nn = s_n[rr], y = X - cc;
+        const int kq = y < 0 ? 0 : y >> qsh;
+        rank += (cc + nn > X) + max(0, nt - 1 - kq);  // tiles with more keys than X
+        // tiles with exactly X keys that come earlier in (request, tile) order
+        const int te = (y > 0 && (y & (QT - 1)) == 0 && (y >> qsh) - 1 < nt - 1) ? (y >> qsh) - 1
+                       : (cc + nn == X ? nt - 1 : -1);
+        if (te >= 0 && (kk < k || (kk == k && te < t))) ++rank;
+      }
+      for (int m = 1; m < S; m <<= 1) rank += __shfl_xor(rank, m, kWave);
+      if (live && sl == 0)
+        *reinterpret_cast<int4*>(a.o.pre_items + 4 * (long long)rank) = make_int4(r, q0, q1, X);
     }
-    if (gtid < G) {
-      wave_of(gtid, di1, kvh1, pg1, n1, r1);
-      id1 = a.b.bt_pages[s_btoff[r1] + pg1];
-    }
-    if (gtid < T) store_row(gtid, r0, p0, page0);
-    if (gtid < G) store_wave(gtid, di1, kvh1, pg1, n1, r1, id1);
   }
+  lds_sync();  // the decode flags are complete
+
+  // ---- stores of the first iteration, then the rest of the grid-stride loops ---------
+  if (gtid < T) store_row(gtid, r0, p0, page0);
+  if (gtid < G) store_wave(gtid, di1, kvh1, pg1, n1, r1, id1);
+  if (gtid < bt_total) a.o.block_tables[gtid] = bt0;
   for (int t = gtid + gsz; t < T; t += gsz) {
     int r, p;
     row_of(t, r, p);
@@ -381,40 +427,16 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     wave_of(w, di, kvh, page, n, r);
     store_wave(w, di, kvh, page, n, r, a.b.bt_pages[s_btoff[r] + page]);
   }
-  for (int r = gtid; r < R; r += gsz)
-    if (s_n[r] == 1)
-      *reinterpret_cast<int4*>(a.o.dec_seqs + 4 * (long long)s_decidx[r]) =
-          make_int4(r, s_qstart[r], (s_comp[r] + 1) | s_dflag[s_decidx[r]], 8 * s_decit[r]);
-  // ---- prefill items, sorted by key count descending (stable) --------------------
-  // Tile t of prefill request r covers rows [t*QT, min((t+1)*QT, n)) and needs
-  // c + min((t+1)*QT, n) keys, so per request the number of tiles with more keys than X
-  // (and with exactly X) has a closed form; an item's rank is a sum over requests.
-  // One wave per item, the lanes splitting the requests; QT is a power of two.
-  {
-    const int lane = tid & (kWave - 1), wv = tid >> 6;
-    const int qsh = QT == 32 ? 5 : (QT == 64 ? 6 : 7);
-    for (int i = blockIdx.x + wv * gridDim.x; i < npi; i += gridDim.x * kPackWaves) {
-      const int r = upper_index(s_preit, R, i);  // the prefill request owning item i
-      const int t = i - s_preit[r];
-      const int n = s_n[r], c = s_comp[r];
-      const int q0 = t * QT, q1 = min(q0 + QT, n);
-      const int X = c + q1;
-      int rank = 0;
-      for (int rr = lane; rr < R; rr += kWave) {
-        const int nt = s_preit[rr + 1] - s_preit[rr];
-        if (nt == 0) continue;  // decode request or empty prefill
-        const int cc = s_comp[rr], nn = s_n[rr], y = X - cc;
-        const int k = y < 0 ? 0 : y >> qsh;
-        rank += (cc + nn > X) + max(0, nt - 1 - k);  // tiles with more keys than X
-        // tiles with exactly X keys that come earlier in (request, tile) order
-        const int te = (y > 0 && (y & (QT - 1)) == 0 && (y >> qsh) - 1 < nt - 1) ? (y >> qsh) - 1
-                       : (cc + nn == X ? nt - 1 : -1);
-        if (te >= 0 && (rr < r || (rr == r && te < t))) ++rank;
-      }
-      rank = __builtin_amdgcn_readlane(wave_incl_scan(rank), kWave - 1);
-      if (lane == 0)
-        *reinterpret_cast<int4*>(a.o.pre_items + 4 * (long long)rank) = make_int4(r, q0, q1, X);
-    }
+  for (int e = gtid + gsz; e < bt_total; e += gsz) {
+    int r, g;
+    bt_of(e, r, g);
+    const int nb = s_btoff[r + 1] - s_btoff[r];
+    a.o.block_tables[e] = g < nb ? a.b.bt_pages[s_btoff[r] + g] : -1;
+  }
+  for (int di = gtid; di < nd; di += gsz) {
+    const int r = s_drid[di];
+    *reinterpret_cast<int4*>(a.o.dec_seqs + 4 * (long long)di) =
+        make_int4(r, s_qstart[r], (s_comp[r] + 1) | s_dflag[di], s_dstart[di]);
   }
 
   if (blockIdx.x != 0) return;
@@ -434,7 +456,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     if (i >= np) a.o.prefill_rids[i] = -1;
   }
   // page-id range check over the concatenated tables: the first chunk was loaded before
-  // the scans
+  // the hash and the item ranks
   int bad = 0;
   {
     const long long np64 = a.c.pool_pages;
@@ -486,19 +508,30 @@ __global__ void __launch_bounds__(kSchedThreads)
 schedule_kernel(const int32_t* __restrict__ num_tokens, const int32_t* __restrict__ computed,
                 int R, int budget, int chunk, int32_t* batch_req, int32_t* batch_n,
                 int32_t* n_batch) {
-  __shared__ int s_rem[FQA_MAX_REQS];
+  __shared__ __attribute__((aligned(16))) int s_rem[FQA_MAX_REQS + 4];
   __shared__ int s_order[FQA_MAX_REQS];
   __shared__ int s_wsum[kSchedThreads / kWave];
   __shared__ int s_wcnt[kSchedThreads / kWave];
   const int tid = threadIdx.x;
   for (int i = tid; i < R; i += kSchedThreads) s_rem[i] = num_tokens[i] - computed[i];
+  if (tid < 4) s_rem[R + tid] = INT_MAX;  // padding: never below a value, and past every i
   lds_sync();
-  // stable sort by remaining ascending: rank = #smaller + #equal-and-earlier
+  // stable sort by remaining ascending: rank = #smaller + #equal-and-earlier.  The
+  // values are read 4 per LDS access, 4 accesses in flight (a one-value loop waited for
+  // every read: ~10 us at 261 requests).
+  const int4* rem4 = reinterpret_cast<const int4*>(s_rem);
+  const int n4 = (R + 3) >> 2;
   for (int i = tid; i < R; i += kSchedThreads) {
-    int v = s_rem[i], rank = 0;
-    for (int j = 0; j < R; ++j) {
-      int u = s_rem[j];
-      rank += (u < v) || (u == v && j < i);
+    const int v = s_rem[i];
+    int rank = 0;
+#pragma unroll 4
+    for (int j4 = 0; j4 < n4; ++j4) {
+      const int4 u = rem4[j4];
+      const int j = 4 * j4;
+      rank += (u.x < v) || (u.x == v && j < i);
+      rank += (u.y < v) || (u.y == v && j + 1 < i);
+      rank += (u.z < v) || (u.z == v && j + 2 < i);
+      rank += (u.w < v) || (u.w == v && j + 3 < i);
     }
     s_order[rank] = i;
   }
@@ -665,7 +698,7 @@ int fqa_pack(const fqa_batch* batch, const fqa_pack_cfg* cfg, const fqa_pack_out
     return FQA_EINVAL;
   long long work = (long long)R * cfg->max_blocks;
   if (cfg->max_rows > work) work = cfg->max_rows;
-  long long grid = (work + 2 * kPackThreads - 1) / (2 * kPackThreads);
+  long long grid = (work + kPackThreads - 1) / kPackThreads;
   grid = grid < 1 ? 1 : (grid > 256 ? 256 : grid);
   PackArgs a{*batch, *cfg, *out};
   hipLaunchKernelGGL(pack_kernel, dim3((unsigned)grid), dim3(kPackThreads), 0,
