@@ -370,7 +370,8 @@ static float dot_d(const float* a, const float* b, int D) {
  * to bf16 in the numerator (prefill, attn_cute.cu:128) but summed unrounded into l
  * (attn_cute.cu:122-127).  Output 0 when no key contributes (l == 0, attn_cute.cu:141). */
 static void attend_row(const float* q, const float* K, const float* V, const unsigned char* ok,
-                       int nk, int D, float scale, int round_p, float* s, uint16_t* out) {
+                       int nk, int D, float scale, int round_p, float* s, uint16_t* out,
+                       float* absv) {
   float m = -INFINITY;
   for (int k = 0; k < nk; ++k) {
     s[k] = ok[k] ? dot_d(q, K + (int64_t)k * D, D) * scale : -INFINITY;
@@ -390,6 +391,17 @@ static void attend_row(const float* q, const float* K, const float* V, const uns
     }
   float inv = l > 0.f ? 1.0f / l : 0.f;
   for (int d = 0; d < D; ++d) out[d] = fqo_f32_to_bf16(acc[d] * inv);
+  if (absv) { /* sum_k p_k |V_kd| / sum_k p_k, for the rounding allowance of P */
+    for (int d = 0; d < D; ++d) absv[d] = 0.f;
+    if (m > -INFINITY)
+      for (int k = 0; k < nk; ++k) {
+        if (!ok[k]) continue;
+        float p = expf(s[k] - m);
+        const float* vr = V + (int64_t)k * D;
+        for (int d = 0; d < D; ++d) absv[d] += p * fabsf(vr[d]);
+      }
+    for (int d = 0; d < D; ++d) absv[d] *= inv;
+  }
 }
 
 /* CuteDecodeSplitKernel + CuteDecodeCombineKernel (attn_cute.cu:165-238) without the
@@ -414,7 +426,7 @@ void fqo_decode(int n_q, int n_kv, int D, int stride, float scale, const uint16_
       int h = kvh * G + g;
       float q[512];
       for (int d = 0; d < D; ++d) q[d] = fqo_bf16_to_f32(qkv[(int64_t)row * stride + h * D + d]);
-      attend_row(q, K, V, ok, nk, D, scale, 0, s, out + ((int64_t)row * n_q + h) * D);
+      attend_row(q, K, V, ok, nk, D, scale, 0, s, out + ((int64_t)row * n_q + h) * D, NULL);
     }
     free(K);
     free(V);
@@ -430,6 +442,18 @@ void fqo_prefill(int n_q, int n_kv, int D, int stride, float scale, const uint16
                  const uint16_t* pool, int64_t pool_pages, const int32_t* block_tables,
                  int max_blocks, const int32_t* cu_seqlens, const int32_t* positions,
                  const int32_t* prefill_rids, int n_prefill, uint16_t* out) {
+  fqo_prefill_absv(n_q, n_kv, D, stride, scale, qkv, pool, pool_pages, block_tables,
+                   max_blocks, cu_seqlens, positions, prefill_rids, n_prefill, out, NULL);
+}
+
+/* fqo_prefill, and (absv non-NULL) per output element sum_k p_k |V_kd| / sum_k p_k with
+ * the row's fp32 weights: the scale of the error that rounding P to bf16 can put into an
+ * output (each p_k moves by at most 2^-9 relative), for per-element test bounds. */
+void fqo_prefill_absv(int n_q, int n_kv, int D, int stride, float scale, const uint16_t* qkv,
+                      const uint16_t* pool, int64_t pool_pages, const int32_t* block_tables,
+                      int max_blocks, const int32_t* cu_seqlens, const int32_t* positions,
+                      const int32_t* prefill_rids, int n_prefill, uint16_t* out,
+                      float* absv) {
   int G = n_q / n_kv;
 #pragma omp parallel for schedule(dynamic, 1)
   for (int w = 0; w < n_prefill * n_kv; ++w) {
@@ -451,7 +475,8 @@ void fqo_prefill(int n_q, int n_kv, int D, int stride, float scale, const uint16
         int h = kvh * G + g;
         float q[512];
         for (int d = 0; d < D; ++d) q[d] = fqo_bf16_to_f32(qkv[(int64_t)row * stride + h * D + d]);
-        attend_row(q, K, V, ok, kv_end, D, scale, 1, s, out + ((int64_t)row * n_q + h) * D);
+        attend_row(q, K, V, ok, kv_end, D, scale, 1, s, out + ((int64_t)row * n_q + h) * D,
+                 absv ? absv + ((int64_t)row * n_q + h) * D : NULL);
       }
     }
     free(K);

@@ -50,6 +50,11 @@ void fqo_prefill(int n_q, int n_kv, int head_dim, int qkv_stride, float scale,
                  const int32_t* block_tables, int max_blocks, const int32_t* cu_seqlens,
                  const int32_t* positions, const int32_t* prefill_rids, int n_prefill,
                  uint16_t* out);
+void fqo_prefill_absv(int n_q, int n_kv, int head_dim, int qkv_stride, float scale,
+                      const uint16_t* qkv, const uint16_t* pool, int64_t pool_pages,
+                      const int32_t* block_tables, int max_blocks, const int32_t* cu_seqlens,
+                      const int32_t* positions, const int32_t* prefill_rids, int n_prefill,
+                      uint16_t* out, float* absv);
 
 /* Float view of one pooled key or value: returns pool element offset of
  * (page, kv head, plane 0=K/1=V, token-in-page, dim). */

@@ -123,6 +123,20 @@ def prefill(qkv, pool, pool_pages, block_tables, max_blocks, cu_seqlens, positio
                        n_prefill, _p(out))
 
 
+def prefill_absv(qkv, pool, pool_pages, block_tables, max_blocks, cu_seqlens, positions,
+                 prefill_rids, n_prefill, out, scale=1.0 / np.sqrt(128.0), n_q=32, n_kv=8,
+                 head_dim=128):
+    """prefill() into `out`, and per output element sum_k p_k |V_kd| / sum_k p_k (float32
+    [rows, n_q * head_dim]; 0 on rows that are not prefill rows): the scale of what rounding
+    P to bf16 can move an output by (each weight moves by at most 2^-9 relative)."""
+    absv = np.zeros(out.shape, np.float32)
+    load().fqo_prefill_absv(n_q, n_kv, head_dim, qkv.shape[1], C.c_float(scale), _p(qkv),
+                            _p(pool), C.c_int64(pool_pages), _p(i32(block_tables)), max_blocks,
+                            _p(i32(cu_seqlens)), _p(i32(positions)), _p(i32(prefill_rids)),
+                            n_prefill, _p(out), _p(absv))
+    return absv
+
+
 def pool_offset(page, kvh, plane, tok, d, n_kv=8, head_dim=128) -> int:
     return int(load().fqo_pool_offset(n_kv, head_dim, page, kvh, plane, tok, d))
 

@@ -130,11 +130,20 @@ def _check_step(cfg, sub, kw, seed, label, schedule=False, kernel_only=True):
     pk = ref["pack"]
     orc.decode(q_got, pool_got.copy(), sub.pool_pages, pk["block_tables"], kwp["max_blocks"],
                pk["cu_seqlens"], pk["positions"], pk["decode_rids"], int(pk["meta"][1]), o_ref)
-    orc.prefill(q_got, pool_got.copy(), sub.pool_pages, pk["block_tables"], kwp["max_blocks"],
-                pk["cu_seqlens"], pk["positions"], pk["prefill_rids"], int(pk["meta"][2]), o_ref)
+    absv = orc.prefill_absv(q_got, pool_got.copy(), sub.pool_pages, pk["block_tables"],
+                            kwp["max_blocks"], pk["cu_seqlens"], pk["positions"],
+                            pk["prefill_rids"], int(pk["meta"][2]), o_ref)
     mx, mean = sc.att_errors(o_got, o_ref)
     print(f"{label}: kernel-only max-abs {mx:.3e} mean-abs {mean:.3e}")
     assert mx <= sc.ATT_MAX_ABS and mean <= sc.ATT_MEAN_ABS
+    prows = np.concatenate([np.arange(pk["cu_seqlens"][r], pk["cu_seqlens"][r + 1])
+                            for r in pk["prefill_rids"][: int(pk["meta"][2])]] or
+                           [np.zeros(0, np.int64)]).astype(np.int64)
+    if prows.size:
+        worst, steps = sc.assert_prefill_rows_close(o_got[prows], o_ref[prows], absv[prows],
+                                                    label)
+        print(f"{label}: prefill rows per element: worst |diff|/allowance {worst:.3f}, "
+              f"worst {steps} bf16 steps where |out| >= 2^-6")
     drows = pk["cu_seqlens"][pk["decode_rids"][: int(pk["meta"][1])]]
     if drows.size:
         dmx, dmean = sc.att_errors(o_got[drows], o_ref[drows])
@@ -167,8 +176,7 @@ def test_step_parity_scheduled(gpu):
     sub = synth._assemble("config4-selected", cfg.computed[sel_req], sel_n,
                           [tabs[i] for i in sel_req], cfg.pool_pages, cfg.max_ctx)
     kw = sc.pack_kwargs(sub, dec_grid_waves=2048, dec_min_pages=8)
-    _check_step(cfg, sub, dict(kw, device=gpu), 104, "config4", schedule=True,
-                kernel_only=False)
+    _check_step(cfg, sub, dict(kw, device=gpu), 104, "config4", schedule=True)
 
 
 @pytest.mark.gpu

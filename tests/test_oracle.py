@@ -238,6 +238,43 @@ def test_attention_against_torch_sdpa(lens, computed):
         assert np.abs(got - ref).mean() <= 2e-3
 
 
+def test_prefill_rounding_allowance_against_fp64():
+    """The per-element allowance the GPU tests give prefill rows rests on two facts checked
+    here against torch fp64: prefill_absv's A equals sum_k p_k |V_kd| / sum_k p_k, and the
+    oracle's output (P rounded to bf16 in the numerator, as attn_cute.cu:128) is within
+    2^-8 A of the exact attention (bf16 rounds a weight by at most 2^-8 relative) plus
+    its final rounding (half a bf16 step, of the larger binade at a boundary)."""
+    lens, computed = [37, 20, 64], [0, 50, 200]
+    cfg, qkv, pool, pk, kw = _attn_case(11, lens, computed)
+    out = np.zeros((cfg.rows, N_Q * HEAD_DIM), np.uint16)
+    absv = orc.prefill_absv(qkv, pool, cfg.pool_pages, pk["block_tables"], kw["max_blocks"],
+                            pk["cu_seqlens"], pk["positions"], pk["prefill_rids"],
+                            int(pk["meta"][2]), out)
+    assert np.array_equal(out, _run_attn(cfg, qkv, pool, pk, kw))  # same outputs as prefill()
+    worst = 0.0
+    for r, (n, c) in enumerate(zip(lens, computed)):
+        K, V = _logical_kv(cfg, pool, r, n + c)
+        q0 = pk["cu_seqlens"][r]
+        Q = f32(qkv[q0:q0 + n, :N_Q * HEAD_DIM]).reshape(n, N_Q, HEAD_DIM).astype(np.float64)
+        Kh = np.repeat(K.transpose(1, 0, 2), 4, 0)  # [H, keys, D], GQA h -> h // 4
+        Vh = np.repeat(V.transpose(1, 0, 2), 4, 0)
+        s = np.einsum("nhd,hkd->hnk", Q, Kh) / np.sqrt(HEAD_DIM)
+        mask = np.arange(n + c)[None, :] <= (c + np.arange(n))[:, None]
+        s = np.where(mask[None], s, -np.inf)
+        p = np.exp(s - s.max(-1, keepdims=True))
+        exact = np.einsum("hnk,hkd->nhd", p, Vh) / p.sum(-1).T[..., None]
+        a_ref = np.einsum("hnk,hkd->nhd", p, np.abs(Vh)) / p.sum(-1).T[..., None]
+        a_got = absv[q0:q0 + n].reshape(n, N_Q, HEAD_DIM)
+        assert np.allclose(a_got, a_ref, rtol=1e-4, atol=1e-6)
+        got = f32(out[q0:q0 + n]).reshape(n, N_Q, HEAD_DIM).astype(np.float64)
+        ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(exact), 1e-30))) - 7)
+        allow = 2.0 ** -8 * a_ref + ulp + 1e-6
+        ratio = np.abs(got - exact) / allow
+        assert ratio.max() <= 1.0, ratio.max()
+        worst = max(worst, float(ratio.max()))
+    assert worst > 0.3  # the allowance is not slack by orders of magnitude
+
+
 def test_attention_closed_forms():
     # single key: decode at context 1 returns V[0] exactly; first row of a fresh prompt too
     cfg, qkv, pool, pk, kw = _attn_case(3, [1, 9], [0, 0])
