@@ -38,7 +38,10 @@ int64_t fqa_pool_bytes(const fqa_dims* dims, int64_t pages) {
 // Fewer pages than one max_ctx sequence needs is FQA_ENOSPACE (the reference throws).
 int fqa_pool_pages(const fqa_dims* dims, uint64_t total_bytes, uint64_t used_bytes,
                    float fraction, int32_t layers, int32_t max_ctx, int64_t* pages) {
-  if (!dims || !pages || layers < 1 || max_ctx < 1 || !(fraction > 0.f) || fraction > 1.f ||
+  // any positive finite fraction, as the reference's constructor takes it (above 1 the
+  // budget exceeds the device; the allocation is what then fails)
+  if (!dims || !pages || layers < 1 || max_ctx < 1 || !(fraction > 0.f) ||
+      !std::isfinite(fraction) || static_cast<float>(total_bytes) * fraction >= 1.8e19f ||
       dims->page_size < 1 || dims->n_kv_heads < 1 || dims->head_dim < 1)
     return FQA_EINVAL;
   *pages = 0;

@@ -182,7 +182,9 @@ int64_t fqa_pool_bytes(const fqa_dims* dims, int64_t pages);
  * layer).  *pages receives the count (capped at 2^31 - 1) in every case; the return is
  * FQA_ENOSPACE when it is below ceil(max_ctx / page_size) (the reference throws), FQA_OK
  * otherwise.  At Qwen3-8B's 36 layers one page costs 2.25 MiB, so a 288 GB device at
- * fraction 0.9 with 20 GB used holds ~101k pages (1.6M tokens). */
+ * fraction 0.9 with 20 GB used holds ~101k pages (1.6M tokens).  Any positive finite
+ * fraction is accepted, above 1 too, as the reference's constructor accepts it; FQA_EINVAL
+ * for a fraction <= 0 or not finite. */
 int fqa_pool_pages(const fqa_dims* dims, uint64_t total_bytes, uint64_t used_bytes,
                    float fraction, int32_t layers, int32_t max_ctx, int64_t* pages);
 
@@ -270,7 +272,8 @@ int fqa_store_kv(const fqa_dims* dims, const uint16_t* qkv, const int32_t* posit
  * log-sum-exp combine merges.  Output rows out[row] ([n_q_heads][head_dim] bf16, row
  * stride n_q_heads*head_dim).  `workspace` must hold
  * fqa_decode_workspace_bytes(dims, dec_wave_cap) bytes; n_reqs_bound bounds the
- * decode requests (combine grid).  The split kernel runs 4 wavefronts per workgroup and
+ * decode requests (combine grid), and dec_seqs must hold at least n_reqs_bound rows (the
+ * combine reads the row of every index below it before checking the decode count).  The split kernel runs 4 wavefronts per workgroup and
  * reserves 120 KiB of LDS per workgroup, so each workgroup holds its CU alone while it
  * runs: work queued on other streams meanwhile gets the CUs the decode does not hold.
  * fqa_dec_default_waves sizes the plan to one workgroup per CU. */
@@ -288,7 +291,8 @@ int fqa_decode(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
  * on the first call on each device (hipGetSymbolAddress); no call allocates or frees.
  * Every call on one device shares that device's array: calls that overlap in time on one
  * device (different streams, or different host threads) race and must be serialised by
- * the caller.  Results are bit-identical to fqa_decode's. */
+ * the caller.  Results are bit-identical to fqa_decode's.  dec_seqs must hold at least
+ * n_reqs_bound rows, as for fqa_decode. */
 #define FQA_DECODE_NOALLOC_MAX_WAVES 4096
 int fqa_decode_noalloc(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
                        int64_t pool_pages, const int32_t* block_tables, int32_t max_blocks,

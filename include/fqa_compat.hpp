@@ -33,6 +33,9 @@
 //  * the decode's split partials live in the context's workspace: pm / pl / pa are
 //    accepted for the signature and not used;
 //  * a rejected call throws std::runtime_error (the reference asserts or exits);
+//  * LaunchHeadNormRope leaves rows whose position has no row in the cos/sin tables
+//    untouched (a RopeTables' row count is looked up through Cos(); a table built
+//    elsewhere is taken to hold the StepContext's max_ctx rows);
 //  * the rows of a request must be contiguous in ForwardInput with consecutive positions,
 //    which is what Request::EmitChunk produces (scheduler.h:66-72) and what the reference's
 //    attention kernels assume (row qstart[r] + i at position pos[qstart[r]] + i).
@@ -104,6 +107,7 @@ struct Registry {
   std::mutex mu;
   std::map<hipStream_t, const Ctx*> by_stream;
   std::map<const void*, int64_t> pool_pages;
+  std::map<const void*, int> rope_rows;  // RopeTables: rows of the table at Cos()
 };
 
 }  // namespace detail
@@ -128,6 +132,14 @@ inline int64_t PoolPagesOf(const void* layer) {
   auto it = r.pool_pages.find(layer);
   if (it == r.pool_pages.end()) Fail("cache_kv is not a layer of a KvStore");
   return it->second;
+}
+// Rows of the cos table at `cos_tab` if a RopeTables built it; otherwise `fallback` (a
+// table built elsewhere is taken to hold max_ctx rows, as the reference assumes).
+inline int RopeRowsOf(const float* cos_tab, int fallback) {
+  auto& r = Reg();
+  std::lock_guard<std::mutex> lock(r.mu);
+  auto it = r.rope_rows.find(cos_tab);
+  return it == r.rope_rows.end() ? fallback : it->second;
 }
 inline fqa_dims Dims(int n_heads, int n_kv, int head_dim, int block_size, int stride, float eps,
                      float scale) {
@@ -304,6 +316,11 @@ class RopeTables {
  public:
   template <class Spec>
   void Build(const Spec& spec, int max_ctx) {
+    {
+      auto& r = detail::Reg();
+      std::lock_guard<std::mutex> lock(r.mu);
+      r.rope_rows.erase(cos_.D());  // a rebuild replaces the table
+    }
     const int half = spec.head_dim / 2;
     std::vector<float> c((size_t)max_ctx * half), s((size_t)max_ctx * half);
     fqa::Check(fqa_rope_tables(max_ctx, spec.head_dim, spec.rope_theta, c.data(), s.data()),
@@ -313,6 +330,17 @@ class RopeTables {
     cos_.Upload(c.data(), c.size(), nullptr);
     sin_.Upload(s.data(), s.size(), nullptr);
     fqa::HipCheck(hipDeviceSynchronize(), "rope upload");
+    auto& r = detail::Reg();
+    std::lock_guard<std::mutex> lock(r.mu);
+    r.rope_rows[cos_.D()] = max_ctx;
+  }
+  RopeTables() = default;
+  RopeTables(const RopeTables&) = delete;
+  RopeTables& operator=(const RopeTables&) = delete;
+  ~RopeTables() {
+    auto& r = detail::Reg();
+    std::lock_guard<std::mutex> lock(r.mu);
+    r.rope_rows.erase(cos_.D());
   }
   const float* Cos() const { return cos_.D(); }
   const float* Sin() const { return sin_.D(); }
@@ -403,8 +431,9 @@ inline void LaunchHeadNormRope(bf16* buf, const float* wq, const float* wk, cons
   if (pos != ctx.pos.D() || M != ctx.n_rows)
     detail::Fail("LaunchHeadNormRope: pos / M are not the stream's StepContext's");
   const fqa_dims d = detail::Dims(n_q, n_kv, head_dim, FQA_PAGE_TOKENS, stride, eps, 0.f);
+  // rows past the table's end are left untouched by the kernel, never read past it
   fqa::Check(fqa_qknorm_rope(&d, reinterpret_cast<uint16_t*>(buf), wq, wk, cos_tab, sin_tab,
-                             ctx.MaxCtx(), pos, ctx.Meta(), M, s),
+                             detail::RopeRowsOf(cos_tab, ctx.MaxCtx()), pos, ctx.Meta(), M, s),
              "fqa_qknorm_rope");
 }
 

@@ -13,14 +13,14 @@ import numpy as np
 import pytest
 
 
-def _case(gpu, M, K, write_k, seed):
+def _case(gpu, M, K, write_k, seed, rows=None):
     import torch
 
     from flashqwen_amd import _lib
     from flashqwen_amd.gemm import gemm, workspace_bytes
     from flashqwen_amd.step import alloc_pool, make_dims, rope_tables
 
-    print(f"[qkv_fused] M={M} K={K} write_k={write_k}", flush=True)
+    print(f"[qkv_fused] M={M} K={K} write_k={write_k} rows={rows}", flush=True)
     lib = _lib.load()
     rng = np.random.default_rng(seed)
     P, max_pos = 64 + M // 8, 4096
@@ -47,12 +47,22 @@ def _case(gpu, M, K, write_k, seed):
         slots[32:] = np.where(np.isin(slots[32:], np.arange((P - 3) * 16, (P - 1) * 16)) &
                               ~np.isin(np.arange(32, M), np.r_[96:112, 248:264]),
                               -1, slots[32:])
+    if rows is not None:
+        # a full page across the row count (rows rows-10 .. rows+5): its rows below the count
+        # are appended as a partly filled page, the rest not at all
+        r0, page = rows - 10, P - 4
+        pos[r0:r0 + 16] = np.arange(700, 716)
+        slots[r0:r0 + 16] = np.arange(page * 16, page * 16 + 16)
+        other = np.ones(M, bool)
+        other[r0:r0 + 16] = False
+        slots[other & (slots // 16 == page)] = -1
     pos[M // 2] = max_pos + 5          # no table row
     slots[M // 3] = P * 16 + 40        # page outside the pool
     pos_t = torch.from_numpy(pos).to(gpu)
     slot_t = torch.from_numpy(slots).to(gpu)
     meta = torch.zeros(16, dtype=torch.int32, device=gpu)
-    meta[_lib.META_ROWS] = M
+    T = M if rows is None else rows
+    meta[_lib.META_ROWS] = T
     dims = make_dims()
 
     qkv_a = torch.full((M, 6144), 3.0, dtype=torch.bfloat16, device=gpu)
@@ -74,9 +84,13 @@ def _case(gpu, M, K, write_k, seed):
         ws.data_ptr() if nb else None, nb, None), "fqa_qkv_proj_append")
     torch.cuda.synchronize()
     ncols = 5120 if write_k else 4096
-    a16 = qkv_a.view(torch.int16)[:, :ncols].cpu().numpy()
-    b16 = qkv_b.view(torch.int16)[:, :ncols].cpu().numpy()
+    a16 = qkv_a.view(torch.int16)[:T, :ncols].cpu().numpy()
+    b16 = qkv_b.view(torch.int16)[:T, :ncols].cpu().numpy()
     assert np.array_equal(a16, b16), int((a16 != b16).sum())
+    # rows at or past the row count: the fused path leaves qkv untouched (the unfused
+    # projection writes every row it is given)
+    rest = qkv_b[T:].float().cpu().numpy()
+    assert np.all(rest == 3.0), int((rest != 3.0).sum())
     pa = pool_a.view(torch.int16).cpu().numpy()
     pb = pool_b.view(torch.int16).cpu().numpy()
     assert np.array_equal(pa, pb), int((pa != pb).sum())
@@ -97,3 +111,14 @@ def test_qkv_fused_equals_unfused(gpu, M, K, write_k):
         assert nb > 0  # the split path (partials read by the append kernel) was exercised
     else:
         assert nb == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,rows", [(1300, 1290), (1000, 990)])
+def test_qkv_fused_rows_below_m(gpu, M, rows):
+    """Unsplit tiles (256 x 256 at 1300 rows, 256 x 128 at 1000) with the pack's row
+    count below M inside the last tile: rows at or past it are neither normalised nor
+    appended, and a page that the count cuts is appended as a partly filled one; the
+    pool equals the unfused path's byte for byte."""
+    nb = _case(gpu, M, 1024, 0, seed=M + 7, rows=rows)
+    assert nb == 0

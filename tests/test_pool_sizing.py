@@ -75,11 +75,20 @@ def test_rejected_arguments():
     out = C.c_int64()
     assert lib.fqa_pool_pages(None, GB, 0, 0.9, 36, 4096, C.byref(out)) == _lib.FQA_EINVAL
     assert lib.fqa_pool_pages(C.byref(d), GB, 0, 0.9, 36, 4096, None) == _lib.FQA_EINVAL
-    for frac in (0.0, -0.5, 1.5, float("nan")):
+    for frac in (0.0, -0.5, float("nan"), float("inf")):
         assert lib.fqa_pool_pages(C.byref(d), GB, 0, frac, 36, 4096, C.byref(out)) == _lib.FQA_EINVAL
     assert lib.fqa_pool_pages(C.byref(d), GB, 0, 0.9, 0, 4096, C.byref(out)) == _lib.FQA_EINVAL
     assert lib.fqa_pool_pages(C.byref(d), GB, 0, 0.9, 36, 0, C.byref(out)) == _lib.FQA_EINVAL
     assert lib.fqa_pool_pages_device(C.byref(d), 0.9, 36, 4096, None) == _lib.FQA_EINVAL
+
+
+def test_fraction_above_one_accepted():
+    """The reference's constructor takes any fraction (kv_store.cu:10-33): above 1 the
+    budget is larger than the device, and the pages follow the same formula."""
+    rc, pages = pages_of(288 * GB, 20 * GB, 1.5)
+    assert rc == _lib.FQA_OK
+    budget = int(np.float32(np.float32(288 * GB) * np.float32(1.5)))
+    assert pages == (budget - 20 * GB) // (36 * 2 * 16 * 1024 * 2)
 
 
 @pytest.mark.gpu

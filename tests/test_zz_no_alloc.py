@@ -56,6 +56,11 @@ def test_noalloc_decode_equals_workspace_decode(gpu):
     big = list(args)
     big[9] = _lib.FQA_DECODE_NOALLOC_MAX_WAVES + 1
     assert lib.fqa_decode_noalloc(*big, None, step.stream) == _lib.FQA_EINVAL
+    # the largest plan the array holds: 4096 wavefronts over config 2 (every stream cut),
+    # bit-equal to the workspace decode
+    print("[test_noalloc_decode_equals_workspace_decode] config2 at the cap", flush=True)
+    _, capargs = _run(synth.config2(), gpu, 5, _lib.FQA_DECODE_NOALLOC_MAX_WAVES)
+    assert capargs[9] == _lib.FQA_DECODE_NOALLOC_MAX_WAVES
     # zero work: nothing launched, nothing looked up
     big[9] = 0
     assert lib.fqa_decode_noalloc(*big, None, step.stream) == _lib.FQA_OK
