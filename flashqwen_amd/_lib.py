@@ -99,6 +99,7 @@ SIGNATURES = {
     "fqa_decode_workspace_bytes": (I64, [C.POINTER(FqaDims), I32]),
     "fqa_schedule": (C.c_int, [P, P, I32, I32, I32, P, P, P, P]),
     "fqa_gather_batch": (C.c_int, [P, P, P, I32, P, P, P, P, P, P, P, I32, P]),
+    "fqa_schedule_gather": (C.c_int, [P, P, I32, I32, I32, P, P, P, P, P, P, P, P, P, I32, P]),
     "fqa_pack": (C.c_int, [C.POINTER(FqaBatch), C.POINTER(FqaPackCfg), C.POINTER(FqaPackOut), P]),
     "fqa_qknorm_rope_append": (
         C.c_int,

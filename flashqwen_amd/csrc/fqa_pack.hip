@@ -504,41 +504,56 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
 // ---- token-budget selection (Scheduler::BuildBatch, scheduler.cc:116-143) ---------
 constexpr int kSchedThreads = 1024;
 
-__global__ void __launch_bounds__(kSchedThreads)
-schedule_kernel(const int32_t* __restrict__ num_tokens, const int32_t* __restrict__ computed,
-                int R, int budget, int chunk, int32_t* batch_req, int32_t* batch_n,
-                int32_t* n_batch) {
-  __shared__ __attribute__((aligned(16))) int s_rem[FQA_MAX_REQS + 4];
-  __shared__ int s_order[FQA_MAX_REQS];
-  __shared__ int s_wsum[kSchedThreads / kWave];
-  __shared__ int s_wcnt[kSchedThreads / kWave];
+// LDS of the selection.
+struct SelectLds {
+  long long key[FQA_MAX_REQS];  // (remaining << 32) | index: distinct, in the sort's order
+  int rem[FQA_MAX_REQS];
+  int rank[FQA_MAX_REQS];
+  int order[FQA_MAX_REQS];
+  int req[FQA_MAX_REQS];  // chosen requests, in batch order
+  int n[FQA_MAX_REQS];    // ... and their rows
+  int wsum[kSchedThreads / kWave];
+  int wcnt[kSchedThreads / kWave];
+};
+
+// The selection of one step by a whole kSchedThreads workgroup, into sl.req / sl.n;
+// returns the number of chosen requests (every thread).  Stable sort of the running
+// requests by remaining ascending: rank(i) = #smaller + #equal-and-earlier, i.e. the
+// number of smaller (remaining, index) keys, the R^2 comparisons spread over every thread
+// of the workgroup (parts of the j range per i, summed with LDS atomics).  Then n_k = min(B, S_k) - min(B, S_{k-1}) with S the
+// inclusive prefix of the per-request caps in sorted order: the greedy loop's budget
+// bookkeeping in closed form.
+__device__ int select_batch(const int32_t* __restrict__ num_tokens,
+                            const int32_t* __restrict__ computed, int R, int budget, int chunk,
+                            SelectLds& sl) {
   const int tid = threadIdx.x;
-  for (int i = tid; i < R; i += kSchedThreads) s_rem[i] = num_tokens[i] - computed[i];
-  if (tid < 4) s_rem[R + tid] = INT_MAX;  // padding: never below a value, and past every i
-  lds_sync();
-  // stable sort by remaining ascending: rank = #smaller + #equal-and-earlier.  The
-  // values are read 4 per LDS access, 4 accesses in flight (a one-value loop waited for
-  // every read: ~10 us at 261 requests).
-  const int4* rem4 = reinterpret_cast<const int4*>(s_rem);
-  const int n4 = (R + 3) >> 2;
   for (int i = tid; i < R; i += kSchedThreads) {
-    const int v = s_rem[i];
-    int rank = 0;
-#pragma unroll 4
-    for (int j4 = 0; j4 < n4; ++j4) {
-      const int4 u = rem4[j4];
-      const int j = 4 * j4;
-      rank += (u.x < v) || (u.x == v && j < i);
-      rank += (u.y < v) || (u.y == v && j + 1 < i);
-      rank += (u.z < v) || (u.z == v && j + 2 < i);
-      rank += (u.w < v) || (u.w == v && j + 3 < i);
-    }
-    s_order[rank] = i;
+    const int rem = num_tokens[i] - computed[i];
+    sl.rem[i] = rem;
+    sl.key[i] = (long long)((unsigned long long)(long long)rem << 32) | (unsigned)i;
+    sl.rank[i] = 0;
   }
   lds_sync();
-  // n_k = min(B, S_k) - min(B, S_{k-1}), S = inclusive prefix of per-request caps:
-  // the greedy loop's budget bookkeeping in closed form.  Only min(B, S) matters, so the
-  // prefix is taken with saturating adds at B + 1 (B <= 2^24 keeps every sum in int).
+  {
+    // rank(i) = #{j : key_j < key_i}: one 64-bit compare per pair, the keys of a wave's
+    // j range read as LDS broadcasts
+    const int parts = R > 0 && R < kSchedThreads ? kSchedThreads / R : 1;
+    const int span = (R + parts - 1) / parts;
+    for (int t = tid; t < R * parts; t += kSchedThreads) {
+      const int i = t % R, p = t / R;
+      const long long v = sl.key[i];
+      const int j1 = min(R, (p + 1) * span);
+      int cnt = 0;
+#pragma unroll 8
+      for (int j = p * span; j < j1; ++j) cnt += sl.key[j] < v;
+      if (cnt) atomicAdd(&sl.rank[i], cnt);
+    }
+  }
+  lds_sync();
+  for (int i = tid; i < R; i += kSchedThreads) sl.order[sl.rank[i]] = i;
+  lds_sync();
+  // Only min(B, S) matters, so the prefix is taken with saturating adds at B + 1
+  // (B <= 2^24 keeps every sum in int).
   const int lane = tid & (kWave - 1), w = tid >> 6;
   const int B = budget > 0 ? budget : 0, cap1 = B + 1;
   auto sat = [cap1](int x, int y) { const int s = x + y; return s < cap1 ? s : cap1; };
@@ -548,8 +563,8 @@ schedule_kernel(const int32_t* __restrict__ num_tokens, const int32_t* __restric
     const int k = base + tid;
     int cap = 0, idx = -1;
     if (k < R) {
-      idx = s_order[k];
-      const int rem = s_rem[idx];
+      idx = sl.order[k];
+      const int rem = sl.rem[idx];
       cap = rem <= 0 ? 0 : (rem > 1 && chunk < rem ? chunk : rem);
       cap = cap < cap1 ? cap : cap1;
     }
@@ -560,12 +575,12 @@ schedule_kernel(const int32_t* __restrict__ num_tokens, const int32_t* __restric
     x = sat(x, __builtin_amdgcn_update_dpp(0, x, kDppRowShr8, 0xf, 0xf, true));
     x = sat(x, __builtin_amdgcn_update_dpp(0, x, kDppRowBcast15, 0xa, 0xf, false));
     x = sat(x, __builtin_amdgcn_update_dpp(0, x, kDppRowBcast31, 0xc, 0xf, false));
-    if (lane == kWave - 1) s_wsum[w] = x;
+    if (lane == kWave - 1) sl.wsum[w] = x;
     lds_sync();
     int pre = carry;  // saturating prefix of the earlier waves
-    for (int i = 0; i < w; ++i) pre = sat(pre, s_wsum[i]);
+    for (int i = 0; i < w; ++i) pre = sat(pre, sl.wsum[i]);
     int tot = carry;
-    for (int i = 0; i < kSchedThreads / kWave; ++i) tot = sat(tot, s_wsum[i]);
+    for (int i = 0; i < kSchedThreads / kWave; ++i) tot = sat(tot, sl.wsum[i]);
     lds_sync();
     // exclusive prefix = the previous lane's saturated inclusive prefix (wave_shr:1)
     const int xe = __builtin_amdgcn_update_dpp(0, x, kDppWaveShr1, 0xf, 0xf, true);
@@ -575,46 +590,90 @@ schedule_kernel(const int32_t* __restrict__ num_tokens, const int32_t* __restric
     const int take = n > 0;
     // compact the chosen requests in sorted order
     const int c = wave_incl_scan(take);
-    if (lane == kWave - 1) s_wcnt[w] = c;
+    if (lane == kWave - 1) sl.wcnt[w] = c;
     lds_sync();
     int cpre = 0, ctot = 0;
     for (int i = 0; i < kSchedThreads / kWave; ++i) {
-      if (i < w) cpre += s_wcnt[i];
-      ctot += s_wcnt[i];
+      if (i < w) cpre += sl.wcnt[i];
+      ctot += sl.wcnt[i];
     }
-    lds_sync();
     if (take) {
       const int pos = ccount + cpre + c - 1;
-      batch_req[pos] = idx;
-      batch_n[pos] = n;
+      sl.req[pos] = idx;
+      sl.n[pos] = n;
     }
+    lds_sync();
     carry = tot;
     ccount += ctot;
   }
-  if (tid == 0) *n_batch = ccount;
+  return ccount;
+}
+
+__global__ void __launch_bounds__(kSchedThreads)
+schedule_kernel(const int32_t* __restrict__ num_tokens, const int32_t* __restrict__ computed,
+                int R, int budget, int chunk, int32_t* batch_req, int32_t* batch_n,
+                int32_t* n_batch) {
+  __shared__ SelectLds sl;
+  const int cnt = select_batch(num_tokens, computed, R, budget, chunk, sl);
+  for (int i = threadIdx.x; i < cnt; i += kSchedThreads) {
+    batch_req[i] = sl.req[i];
+    batch_n[i] = sl.n[i];
+  }
+  if (threadIdx.x == 0) *n_batch = cnt;
 }
 
 // Gather the chosen running requests into a compact fqa_batch.  Each workgroup
 // recomputes the exclusive scan of table lengths, then copies its share of pages.
-__global__ void __launch_bounds__(kPackThreads)
-gather_kernel(const int32_t* __restrict__ batch_req, const int32_t* __restrict__ batch_n,
-              const int32_t* __restrict__ n_batch, int R_bound,
-              const int32_t* __restrict__ run_computed, const int32_t* __restrict__ run_bt_off,
-              const int32_t* __restrict__ run_bt_pages, int32_t* out_computed,
-              int32_t* out_n_new, int32_t* out_bt_off, int32_t* out_bt_pages, int cap) {
+// kSelect: the workgroup first makes the selection itself (select_batch, the same in
+// every workgroup) instead of reading fqa_schedule's, and workgroup 0 writes it out.
+struct GatherArgs {
+  const int32_t* num_tokens;  // kSelect: the running requests' token counts
+  int budget, chunk;
+  int32_t* batch_req;  // kSelect: written; else read
+  int32_t* batch_n;
+  int32_t* n_batch;
+  int R_bound;
+  const int32_t* run_computed;
+  const int32_t* run_bt_off;
+  const int32_t* run_bt_pages;
+  int32_t* out_computed;
+  int32_t* out_n_new;
+  int32_t* out_bt_off;
+  int32_t* out_bt_pages;
+  int cap;
+};
+
+template <bool kSelect>
+__global__ void __launch_bounds__(kPackThreads) gather_kernel(GatherArgs a) {
+  static_assert(kPackThreads == kSchedThreads, "one workgroup size");
   __shared__ int s_off[FQA_MAX_REQS + 1];
   __shared__ int s_src[FQA_MAX_REQS];
   __shared__ int sh32[kPackWaves];
+  __shared__ SelectLds sl;
   const int tid = threadIdx.x;
-  int R = *n_batch;
-  if (R > R_bound) R = R_bound;
+  int R;
+  if constexpr (kSelect) {
+    R = select_batch(a.num_tokens, a.run_computed, a.R_bound, a.budget, a.chunk, sl);
+    if (blockIdx.x == 0) {
+      for (int i = tid; i < R; i += kPackThreads) {
+        a.batch_req[i] = sl.req[i];
+        a.batch_n[i] = sl.n[i];
+      }
+      if (tid == 0) *a.n_batch = R;
+    }
+  } else {
+    R = *a.n_batch;
+    if (R > a.R_bound) R = a.R_bound;
+  }
+  auto req_of = [&](int i) { return kSelect ? sl.req[i] : a.batch_req[i]; };
+  auto n_of = [&](int i) { return kSelect ? sl.n[i] : a.batch_n[i]; };
   int carry = 0;
   for (int base = 0; base < R; base += kPackThreads) {
     int i = base + tid, len = 0;
     if (i < R) {
-      int q = batch_req[i];
-      s_src[i] = run_bt_off[q];
-      len = run_bt_off[q + 1] - run_bt_off[q];
+      int q = req_of(i);
+      s_src[i] = a.run_bt_off[q];
+      len = a.run_bt_off[q + 1] - a.run_bt_off[q];
     }
     int tot;
     int e = block_excl_scan(len, sh32, &tot);
@@ -626,17 +685,22 @@ gather_kernel(const int32_t* __restrict__ batch_req, const int32_t* __restrict__
   const int gtid = blockIdx.x * kPackThreads + tid, gsz = gridDim.x * kPackThreads;
   if (blockIdx.x == 0)
     for (int i = tid; i <= R; i += kPackThreads) {
-      out_bt_off[i] = s_off[i] < cap ? s_off[i] : cap;
+      a.out_bt_off[i] = s_off[i] < a.cap ? s_off[i] : a.cap;
       if (i < R) {
-        out_computed[i] = run_computed[batch_req[i]];
-        out_n_new[i] = batch_n[i];
+        a.out_computed[i] = a.run_computed[req_of(i)];
+        a.out_n_new[i] = n_of(i);
       }
     }
-  const int total = carry < cap ? carry : cap;
+  const int total = carry < a.cap ? carry : a.cap;
   for (int e = gtid; e < total; e += gsz) {
     int i = upper_index(s_off, R, e);
-    out_bt_pages[e] = run_bt_pages[s_src[i] + (e - s_off[i])];
+    a.out_bt_pages[e] = a.run_bt_pages[s_src[i] + (e - s_off[i])];
   }
+}
+
+int gather_grid(int cap) {
+  int grid = (cap + 4 * kPackThreads - 1) / (4 * kPackThreads);
+  return grid < 1 ? 1 : (grid > 512 ? 512 : grid);
 }
 
 }  // namespace
@@ -668,12 +732,33 @@ int fqa_gather_batch(const int32_t* batch_req, const int32_t* batch_n, const int
   if (!batch_req || !batch_n || !n_batch || !run_computed || !run_bt_off || !out_computed ||
       !out_n_new || !out_bt_off || (bt_pages_cap > 0 && (!run_bt_pages || !out_bt_pages)))
     return FQA_EINVAL;
-  int grid = (bt_pages_cap + 4 * kPackThreads - 1) / (4 * kPackThreads);
-  grid = grid < 1 ? 1 : (grid > 512 ? 512 : grid);
-  hipLaunchKernelGGL(gather_kernel, dim3(grid), dim3(kPackThreads), 0, (hipStream_t)stream,
-                     batch_req, batch_n, n_batch, n_running, run_computed, run_bt_off,
-                     run_bt_pages, out_computed, out_n_new, out_bt_off, out_bt_pages,
-                     bt_pages_cap);
+  GatherArgs a{nullptr, 0, 0, const_cast<int32_t*>(batch_req), const_cast<int32_t*>(batch_n),
+               const_cast<int32_t*>(n_batch), n_running, run_computed, run_bt_off, run_bt_pages,
+               out_computed, out_n_new, out_bt_off, out_bt_pages, bt_pages_cap};
+  hipLaunchKernelGGL(gather_kernel<false>, dim3(gather_grid(bt_pages_cap)), dim3(kPackThreads),
+                     0, (hipStream_t)stream, a);
+  return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
+}
+
+int fqa_schedule_gather(const int32_t* num_tokens, const int32_t* run_computed,
+                        int32_t n_running, int32_t token_budget, int32_t prefill_chunk,
+                        const int32_t* run_bt_off, const int32_t* run_bt_pages,
+                        int32_t* batch_req, int32_t* batch_n, int32_t* n_batch,
+                        int32_t* out_computed, int32_t* out_n_new, int32_t* out_bt_off,
+                        int32_t* out_bt_pages, int32_t bt_pages_cap, void* stream) {
+  if (n_running < 0 || n_running > FQA_MAX_REQS || prefill_chunk < 1 ||
+      token_budget > (1 << 24) || bt_pages_cap < 0 || !n_batch || !run_bt_off ||
+      !out_bt_off)
+    return FQA_EINVAL;
+  if (n_running > 0 && (!num_tokens || !run_computed || !batch_req || !batch_n ||
+                        !out_computed || !out_n_new))
+    return FQA_EINVAL;
+  if (bt_pages_cap > 0 && (!run_bt_pages || !out_bt_pages)) return FQA_EINVAL;
+  GatherArgs a{num_tokens, token_budget, prefill_chunk, batch_req, batch_n, n_batch, n_running,
+               run_computed, run_bt_off, run_bt_pages, out_computed, out_n_new, out_bt_off,
+               out_bt_pages, bt_pages_cap};
+  hipLaunchKernelGGL(gather_kernel<true>, dim3(gather_grid(bt_pages_cap)), dim3(kPackThreads),
+                     0, (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
 }
 

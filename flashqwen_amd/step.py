@@ -137,17 +137,28 @@ class AttnStep:
 
     def schedule_and_prepare(self, num_tokens: torch.Tensor, computed: torch.Tensor,
                              bt_off: torch.Tensor, bt_pages: torch.Tensor, token_budget: int,
-                             prefill_chunk: int, rows_bound: int | None = None):
-        """Scheduler::BuildBatch selection + gather + pack, all on the GPU."""
+                             prefill_chunk: int, rows_bound: int | None = None,
+                             fused: bool = True):
+        """Scheduler::BuildBatch selection + gather + pack, all on the GPU: two launches
+        (fqa_schedule_gather, fqa_pack), or with fused=False three (fqa_schedule,
+        fqa_gather_batch, fqa_pack)."""
         n_run = int(num_tokens.shape[0])
-        check(self.lib.fqa_schedule(_ptr(num_tokens), _ptr(computed), n_run, token_budget,
-                                    prefill_chunk, _ptr(self.sel_req), _ptr(self.sel_n),
-                                    _ptr(self.n_sel), self.stream), "fqa_schedule")
-        check(self.lib.fqa_gather_batch(_ptr(self.sel_req), _ptr(self.sel_n), _ptr(self.n_sel),
-                                        n_run, _ptr(computed), _ptr(bt_off), _ptr(bt_pages),
-                                        _ptr(self.b_computed), _ptr(self.b_n_new),
-                                        _ptr(self.b_bt_off), _ptr(self.b_bt_pages),
-                                        self.max_bt_pages, self.stream), "fqa_gather_batch")
+        if fused:
+            check(self.lib.fqa_schedule_gather(
+                _ptr(num_tokens), _ptr(computed), n_run, token_budget, prefill_chunk,
+                _ptr(bt_off), _ptr(bt_pages), _ptr(self.sel_req), _ptr(self.sel_n),
+                _ptr(self.n_sel), _ptr(self.b_computed), _ptr(self.b_n_new), _ptr(self.b_bt_off),
+                _ptr(self.b_bt_pages), self.max_bt_pages, self.stream), "fqa_schedule_gather")
+        else:
+            check(self.lib.fqa_schedule(_ptr(num_tokens), _ptr(computed), n_run, token_budget,
+                                        prefill_chunk, _ptr(self.sel_req), _ptr(self.sel_n),
+                                        _ptr(self.n_sel), self.stream), "fqa_schedule")
+            check(self.lib.fqa_gather_batch(_ptr(self.sel_req), _ptr(self.sel_n),
+                                            _ptr(self.n_sel), n_run, _ptr(computed),
+                                            _ptr(bt_off), _ptr(bt_pages), _ptr(self.b_computed),
+                                            _ptr(self.b_n_new), _ptr(self.b_bt_off),
+                                            _ptr(self.b_bt_pages), self.max_bt_pages,
+                                            self.stream), "fqa_gather_batch")
         self.prepare_inputs(self.b_computed, self.b_n_new, self.b_bt_off, self.b_bt_pages,
                             n_reqs=n_run, rows_bound=rows_bound, n_reqs_dev=self.n_sel)
 

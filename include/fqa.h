@@ -6,6 +6,7 @@
  * StepContext::PrepareInputs at model_runtime.cu:295-302 once per step):
  *
  *   fqa_schedule            <- Scheduler::BuildBatch token-budget selection   (scheduler.cc:116-143)
+ *   fqa_schedule_gather     <- the same selection + the chosen requests' batch, one launch
  *   fqa_pack                <- StepContext::PrepareInputs: UploadRows, PackBlockTables,
  *                              SplitDecodePrefill                             (model_runtime.cu:47-91, 295-302)
  *   fqa_rope_tables         <- RopeTables::Build                              (model_runtime.cu:111-126)
@@ -225,6 +226,17 @@ int fqa_gather_batch(const int32_t* batch_req, const int32_t* batch_n,
                      const int32_t* run_bt_off, const int32_t* run_bt_pages,
                      int32_t* out_computed, int32_t* out_n_new, int32_t* out_bt_off,
                      int32_t* out_bt_pages, int32_t bt_pages_cap, void* stream);
+
+/* fqa_schedule and fqa_gather_batch in one launch: every workgroup of the gather makes
+ * the selection itself (the same in each), workgroup 0 writes it to batch_req / batch_n
+ * / n_batch, and the chosen requests are gathered as fqa_gather_batch gathers them.
+ * The same arguments and results as the two calls in turn. */
+int fqa_schedule_gather(const int32_t* num_tokens, const int32_t* run_computed,
+                        int32_t n_running, int32_t token_budget, int32_t prefill_chunk,
+                        const int32_t* run_bt_off, const int32_t* run_bt_pages,
+                        int32_t* batch_req, int32_t* batch_n, int32_t* n_batch,
+                        int32_t* out_computed, int32_t* out_n_new, int32_t* out_bt_off,
+                        int32_t* out_bt_pages, int32_t bt_pages_cap, void* stream);
 
 /* The GPU pack (replaces StepContext::PrepareInputs' host loops + H2D copies,
  * model_runtime.cu:47-91): rows, slot mapping, padded block tables, decode/prefill

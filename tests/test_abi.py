@@ -86,6 +86,16 @@ def test_rejected_calls_return_codes_without_launching():
     assert lib.fqa_schedule(null, null, _lib.FQA_MAX_REQS + 1, 1, 1, null, null, null,
                             null) == _lib.FQA_EINVAL
     assert lib.fqa_schedule(null, null, 4, 1, 0, null, null, null, null) == _lib.FQA_EINVAL
+    # the fused selection + gather: the same bounds, and every pointer its work needs
+    i32 = (C.c_int32 * 8)()
+    assert lib.fqa_schedule_gather(null, null, _lib.FQA_MAX_REQS + 1, 1, 1, i32, i32, i32, i32,
+                                   i32, i32, i32, i32, i32, 8, null) == _lib.FQA_EINVAL
+    assert lib.fqa_schedule_gather(i32, i32, 4, 1, 0, i32, i32, i32, i32, i32, i32, i32, i32,
+                                   i32, 8, null) == _lib.FQA_EINVAL
+    assert lib.fqa_schedule_gather(i32, i32, 4, 1, 1, i32, null, i32, i32, i32, i32, i32, i32,
+                                   i32, 8, null) == _lib.FQA_EINVAL
+    assert lib.fqa_schedule_gather(null, i32, 4, 1, 1, i32, i32, i32, i32, i32, i32, i32, i32,
+                                   i32, 8, null) == _lib.FQA_EINVAL
     assert lib.fqa_rope_tables(4, 127, 1e6, null, null) == _lib.FQA_EINVAL
 
 

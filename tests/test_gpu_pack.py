@@ -174,9 +174,11 @@ def test_pack_status(gpu, case):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("seed", range(6))
-def test_schedule_gather_pack(gpu, seed):
-    """fqa_schedule + fqa_gather_batch + fqa_pack == oracle selection + oracle pack."""
+def test_schedule_gather_pack(gpu, seed, fused):
+    """fqa_schedule_gather + fqa_pack (fused) and fqa_schedule + fqa_gather_batch + fqa_pack
+    == oracle selection + oracle pack."""
     import torch
 
     from flashqwen_amd.step import AttnStep
@@ -198,7 +200,7 @@ def test_schedule_gather_pack(gpu, seed):
         pool = 8192
         tabs = [rng.integers(0, pool, size=synth.cdiv(int(c) + min(int(r), chunk) + 1, 16))
                 .astype(np.int32) for c, r in zip(comp, rem)]
-    print(f"[test_schedule_gather_pack] seed={seed} running={len(comp)} budget={budget} "
+    print(f"[test_schedule_gather_pack] seed={seed} fused={fused} running={len(comp)} budget={budget} "
           f"chunk={chunk}", flush=True)
     run = synth._assemble("run", comp, np.zeros(len(comp), np.int32), tabs, pool, 8192)
     sel_req, sel_n = orc.schedule(ntok, comp, budget, chunk)
@@ -207,7 +209,8 @@ def test_schedule_gather_pack(gpu, seed):
     step = AttnStep(max_rows=max_rows, max_reqs=len(comp), max_ctx=8192, pool_pages=pool,
                     device=gpu, dec_grid_waves=128, dec_min_pages=4)
     t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(gpu)  # noqa: E731
-    step.schedule_and_prepare(t(ntok), t(comp), t(run.bt_off), t(run.bt_pages), budget, chunk)
+    step.schedule_and_prepare(t(ntok), t(comp), t(run.bt_off), t(run.bt_pages), budget, chunk,
+                              fused=fused)
     torch.cuda.synchronize()
     Rb = int(step.n_sel.cpu().item())
     assert Rb == len(sel_req)
