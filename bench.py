@@ -65,6 +65,10 @@ def parse():
                          "prefill row counts) beside torch.matmul (hipBLASLt)")
     ap.add_argument("--gemm-rows", type=str, default="128,256,1024,8192",
                     help="row counts for --gemm")
+    ap.add_argument("--compat-append", action="store_true",
+                    help="also time the compat route's norm/RoPE and append as two launches "
+                         "(fqa_qknorm_rope + fqa_store_kv, as fqa_compat.hpp issues them) "
+                         "beside the fused fqa_qknorm_rope_append")
     return ap.parse_args()
 
 
@@ -95,20 +99,16 @@ def main():
         return
 
     device = None if args.profile_kernels else device_info()
-    line = run_config(args, args.config, steps=args.steps, warmup=args.warmup,
-                      with_cpu=not args.no_cpu)
-    if line is None:  # --profile-kernels
-        return
-    line["device"] = device
-    if args.config == 5 and not args.no_prefill_lines:
+    pre = None
+    if args.config == 5 and not args.no_prefill_lines and not args.profile_kernels:
         # the metric's second half: prefill MFMA utilisation on the two prefill configs,
-        # measured in the same process after config 5's pool is released
+        # measured in the same process before config 5 (right after config 5's 36-layer
+        # sweep over its 200 GB pool the prefill runs ~10% slower: the clock under sustained
+        # load); each config's pool is released before the next is built
         import gc
 
         import torch
 
-        gc.collect()
-        torch.cuda.empty_cache()
         pre = {}
         for c in (3, 4):
             sub = run_config(args, c, steps=max(args.steps, 20), warmup=args.warmup,
@@ -119,10 +119,23 @@ def main():
                                  "rows_per_step": sub["config"]["rows_per_step"],
                                  "roofline": sub["roofline"],
                                  "kernels_us": sub["kernels_us"],
+                                 "step_floor_us": sub["step_floor_us"],
+                                 "step_over_floor_us": sub["step_over_floor_us"],
                                  "cpu_baseline": sub["cpu_baseline"]}
             gc.collect()
             torch.cuda.empty_cache()
+    line = run_config(args, args.config, steps=args.steps, warmup=args.warmup,
+                      with_cpu=not args.no_cpu)
+    if line is None:  # --profile-kernels
+        return
+    line["device"] = device
+    if pre is not None:
         line["prefill"] = pre
+        # the same rooflines, compact, beside the decode's
+        line["roofline"]["prefill_configs"] = {
+            k: {f: v["roofline"][f] for f in ("achieved", "peak", "unit", "frac", "launch_us",
+                                               "flops_per_launch")}
+            for k, v in pre.items()}
     print(json.dumps(line))
 
 
@@ -262,6 +275,25 @@ def run_config(args, config, *, steps, warmup, with_cpu):
     kernels = {"pack": pack,
                "qknorm_rope_append": lambda: step.head_norm_rope_store_kv(qkv, pool[0], wq_d,
                                                                           wk_d)}
+    if args.compat_append:
+        import ctypes as C
+
+        from flashqwen_amd import _lib
+
+        lib = _lib.load()
+
+        def two_launch():
+            s = step.stream
+            _lib.check(lib.fqa_qknorm_rope(
+                C.byref(step.dims), qkv.data_ptr(), wq_d.data_ptr(), wk_d.data_ptr(),
+                step.cos.data_ptr(), step.sin.data_ptr(), step.max_ctx,
+                step.positions.data_ptr(), step.meta.data_ptr(), step.rows_bound, s),
+                "fqa_qknorm_rope")
+            _lib.check(lib.fqa_store_kv(
+                C.byref(step.dims), qkv.data_ptr(), step.positions.data_ptr(),
+                step.slot_mapping.data_ptr(), step.meta.data_ptr(), step.rows_bound,
+                pool[0].data_ptr(), cfg.pool_pages, s), "fqa_store_kv")
+        kernels["compat_norm_then_store"] = two_launch
     if has_decode:
         kernels["decode"] = lambda: step.attn_decode(qkv, pool[0], out)
         # the same plan's pages read with the same loads and no arithmetic: the floor
@@ -338,6 +370,12 @@ def run_config(args, config, *, steps, warmup, with_cpu):
     if with_cpu:
         cpu = cpu_baseline(cfg, comp_sel, n_sel, T, args.cpu_seconds)
 
+    # the step's floor: its kernels back to back at their isolated durations, the decode at
+    # its read floor (the same pages read with no arithmetic); the rest of the step time is
+    # launch gaps and what the kernels lose to each other
+    floor_us = (kern_ms["pack"] + layers * (kern_ms["qknorm_rope_append"] +
+                                            kern_ms.get("decode_read_floor", 0.0) +
+                                            kern_ms.get("prefill", 0.0))) * 1e3
     tokens_per_step = T
     value = tokens_per_step / (ms_step * 1e-3)
     line = {
@@ -360,6 +398,8 @@ def run_config(args, config, *, steps, warmup, with_cpu):
                    "pre_items": int(meta[5])},
         "roofline": roof,
         "kernels_us": {k: round(v * 1e3, 2) for k, v in kern_ms.items()},
+        "step_floor_us": round(floor_us, 2),
+        "step_over_floor_us": round(ms_step * 1e3 - floor_us, 2),
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),
     }
