@@ -57,9 +57,13 @@ def parse():
     ap.add_argument("--sampler", action="store_true",
                     help="only measure fqa_sample (256 rows x 151936 logits: greedy, "
                          "temperature, temperature + top-p 0.9)")
+    ap.add_argument("--no-dec-share", action="store_true",
+                    help="mixed steps with the second stream: plan the decode for the whole "
+                         "device (no dec_share)")
     ap.add_argument("--no-overlap", action="store_true",
                     help="mixed steps: keep the decode on the step's stream (by default it "
-                         "runs on a second stream, queued after the prefill)")
+                         "runs on a second stream beside the prefill, planned for the CUs "
+                         "the prefill leaves: dec_share)")
     ap.add_argument("--gemm", action="store_true",
                     help="only measure fqa_gemm on the Qwen3-8B projections (decode and "
                          "prefill row counts) beside torch.matmul (hipBLASLt)")
@@ -120,7 +124,8 @@ def main():
                                  "roofline": sub["roofline"],
                                  "kernels_us": sub["kernels_us"],
                                  "step_floor_us": sub["step_floor_us"],
-                                 "step_over_floor_us": sub["step_over_floor_us"],
+                                 "step_minus_floor_us": sub["step_minus_floor_us"],
+                                 "decode_beside_prefill": sub["decode_beside_prefill"],
                                  "cpu_baseline": sub["cpu_baseline"]}
             gc.collect()
             torch.cuda.empty_cache()
@@ -204,7 +209,8 @@ def run_config(args, config, *, steps, warmup, with_cpu):
     step = AttnStep(max_rows=T, max_reqs=cfg.n_reqs, max_ctx=cfg.max_ctx,
                     pool_pages=cfg.pool_pages, device=dev,
                     dec_grid_waves=args.dec_grid_waves, dec_min_pages=args.dec_min_pages,
-                    pre_tile_q=args.pre_tile_q)
+                    pre_tile_q=args.pre_tile_q,
+                    dec_share=not (args.no_overlap or args.no_dec_share))
     d_computed, d_n_new = t(cfg.computed), t(cfg.n_new)
     d_off, d_pages = t(cfg.bt_off), t(cfg.bt_pages)
     d_ntok = t(cfg.num_tokens) if scheduled else None
@@ -363,7 +369,10 @@ def run_config(args, config, *, steps, warmup, with_cpu):
                 "counters": _profile_mfma_util(config)}
         if has_decode:
             logical, _ = synth.decode_bytes(_selected(cfg, comp_sel, n_sel))
-            roof["decode_GBps"] = round(logical / (kern_ms["decode"] * 1e-3) / 1e9, 1)
+            # the decode alone on the step's plan (with dec_share: the waves it gets beside
+            # the prefill, so less than the whole device)
+            roof["decode_GBps_alone"] = round(logical / (kern_ms["decode"] * 1e-3) / 1e9, 1)
+            roof["decode_waves"] = int(meta[4])
 
     # ---- CPU baseline (OpenMP fp32 oracle, bounded sample) ------------------------------
     cpu = None
@@ -372,7 +381,8 @@ def run_config(args, config, *, steps, warmup, with_cpu):
 
     # the step's floor: its kernels back to back at their isolated durations, the decode at
     # its read floor (the same pages read with no arithmetic); the rest of the step time is
-    # launch gaps and what the kernels lose to each other
+    # launch gaps and what the kernels lose to each other.  A mixed step whose decode runs
+    # beside the prefill (dec_share) can end below it: the two kernels overlap.
     floor_us = (kern_ms["pack"] + layers * (kern_ms["qknorm_rope_append"] +
                                             kern_ms.get("decode_read_floor", 0.0) +
                                             kern_ms.get("prefill", 0.0))) * 1e3
@@ -399,7 +409,8 @@ def run_config(args, config, *, steps, warmup, with_cpu):
         "roofline": roof,
         "kernels_us": {k: round(v * 1e3, 2) for k, v in kern_ms.items()},
         "step_floor_us": round(floor_us, 2),
-        "step_over_floor_us": round(ms_step * 1e3 - floor_us, 2),
+        "step_minus_floor_us": round(ms_step * 1e3 - floor_us, 2),
+        "decode_beside_prefill": bool(side is not None and has_decode and has_prefill),
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),
     }

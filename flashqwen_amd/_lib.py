@@ -83,6 +83,7 @@ class FqaPackCfg(C.Structure):
         ("dec_wave_cap", I32),
         ("pre_tile_q", I32),
         ("pre_item_cap", I32),
+        ("dec_share", I32),
     ]
 
 

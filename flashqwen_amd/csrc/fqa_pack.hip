@@ -132,6 +132,38 @@ __device__ __forceinline__ int upper_index(const int* a, int n, int x) {
   return lo;
 }
 
+// The decode wavefronts of a step whose decode runs beside its prefill (fqa.h,
+// dec_share); INT_MAX when the plan is left as it is.
+__device__ int dec_share_waves(int N, long long dpages, unsigned long long keyrows) {
+  constexpr int kStep = FQA_DEC_SHARE_STEP;
+  if (keyrows == 0 || dpages <= 0 || N < 2 * kStep || N > 4096) return INT_MAX;
+  unsigned long long D = (unsigned long long)FQA_DEC_SHARE_RATE * (unsigned long long)dpages;
+  unsigned long long P = keyrows;
+  while (D >= (1ull << 30) || P >= (1ull << 30)) {
+    D >>= 1;
+    P >>= 1;
+  }
+  const unsigned long long n = (unsigned long long)N;
+  // decode(G) ~ D (36 G + 25 N) / (50 G), prefill(G) ~ P N / (N - G)
+  // prefill no slower than decode at G (true at small G, false past the crossing)
+  auto ok = [&](int G) {
+    const unsigned long long g = (unsigned long long)G;
+    return 50 * P * n * g <= D * (36 * g + 25 * n) * (n - g);
+  };
+  const int top = (N - kStep) / kStep * kStep;
+  int lo = kStep, hi = top;
+  if (!ok(lo)) return lo;
+  while (lo < hi) {  // largest multiple of kStep in [kStep, top] with ok()
+    const int mid = (lo + hi + kStep) / (2 * kStep) * kStep;
+    if (ok(mid)) lo = mid; else hi = mid - kStep;
+  }
+  // one step further when the prefill there ends before the decode does at lo
+  const unsigned long long g = (unsigned long long)lo;
+  if (lo + kStep <= top && 50 * P * n * g < D * (36 * g + 25 * n) * (n - g - kStep))
+    lo += kStep;
+  return lo;
+}
+
 struct PackArgs {
   fqa_batch b;
   fqa_pack_cfg c;
@@ -156,6 +188,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   __shared__ Stats s_stats[kPackWaves];
   __shared__ Counts s_counts[kPackWaves];
   __shared__ int sh32[kPackWaves];
+  __shared__ unsigned long long s_keyrows;  // prefill key-rows: sum n*c + n(n+1)/2
 
   const int tid = threadIdx.x;
   int R = a.b.n_reqs_dev ? *a.b.n_reqs_dev : a.b.n_reqs;
@@ -168,6 +201,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     s_hkey[i] = -1;
     s_hcnt[i] = 0;
   }
+  if (tid == 0) s_keyrows = 0;
 
   // ---- per request: load, structural checks, totals, and the five exclusive scans
   // (rows, decode / prefill indices, decode pages, prefill items), one pass per 1024
@@ -231,6 +265,9 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       } else {
         s_prer[pi] = r;
         s_pit[pi] = carry.v[4] + e.v[4];
+        if (a.c.dec_share && n > 0 && c >= 0)
+          atomicAdd(&s_keyrows, (unsigned long long)n * (unsigned long long)c +
+                                    (unsigned long long)n * (n + 1) / 2);
       }
     }
 #pragma unroll
@@ -265,6 +302,8 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   if (W > 0) {
     const int minp = a.c.dec_min_pages > 0 ? a.c.dec_min_pages : 1;
     G = (int)min((long long)a.c.dec_grid_waves, (W + minp - 1) / minp);
+    if (a.c.dec_share)  // CUs shared with a concurrent prefill (fqa.h)
+      G = min(G, dec_share_waves(a.c.dec_grid_waves, dpages, s_keyrows));
   }
   if (G > a.c.dec_wave_cap || npi > a.c.pre_item_cap || dpages > INT_MAX / 8) {
     if (blockIdx.x == 0 && tid < FQA_META_LEN)

@@ -63,7 +63,10 @@ class AttnStep:
 
     def __init__(self, *, max_rows: int, max_reqs: int, max_ctx: int, pool_pages: int,
                  device="cuda", dec_grid_waves: int | None = None, dec_min_pages: int = 8,
-                 pre_tile_q: int = _lib.FQA_PRE_TILE_Q, max_bt_pages: int | None = None):
+                 pre_tile_q: int = _lib.FQA_PRE_TILE_Q, max_bt_pages: int | None = None,
+                 dec_share: bool = False):
+        """dec_share: run_layer will be given a side stream, so a step with both decode
+        and prefill rows plans its decode for the CUs the prefill leaves (fqa.h)."""
         self.lib = _lib.load()
         if max_reqs > _lib.FQA_MAX_REQS:
             raise ValueError(f"max_reqs {max_reqs} > {_lib.FQA_MAX_REQS}")
@@ -78,8 +81,10 @@ class AttnStep:
         self.dec_grid_waves = dec_grid_waves
         self.dec_wave_cap = int(self.lib.fqa_dec_wave_bound(max_reqs, dec_grid_waves))
         self.pre_cap = int(self.lib.fqa_pre_item_bound(max_reqs, max_rows, pre_tile_q))
+        self.dec_share = bool(dec_share)
         self.cfg = FqaPackCfg(max_rows, self.max_blocks, pool_pages, dec_grid_waves,
-                              dec_min_pages, self.dec_wave_cap, pre_tile_q, self.pre_cap)
+                              dec_min_pages, self.dec_wave_cap, pre_tile_q, self.pre_cap,
+                              int(dec_share))
         i32 = dict(dtype=torch.int32, device=self.device)
         R = max_reqs
         self.cu_seqlens = torch.zeros(R + 1, **i32)
@@ -198,16 +203,18 @@ class AttnStep:
     def run_layer(self, qkv, pool_layer, q_norm_w, k_norm_w, out, write_k=False,
                   decode=True, prefill=True, side_stream=None):
         """The attention block of one layer (model_runtime.cu:263-278).  With side_stream
-        (and both kinds of rows), the decode runs on it concurrently with the prefill: the
-        two write disjoint output rows and only read the pool, and the decode is HBM-bound
-        while the prefill is MFMA-bound."""
+        (and both kinds of rows), the decode runs on it concurrently with the prefill,
+        queued first so that its workgroups take their CUs before the prefill's fill the
+        rest (with dec_share the decode plan leaves the prefill its share): the two write
+        disjoint output rows and only read the pool, and the decode is HBM-bound while the
+        prefill is MFMA-bound."""
         self.head_norm_rope_store_kv(qkv, pool_layer, q_norm_w, k_norm_w, write_k)
         if decode and prefill and side_stream is not None:
             cur = torch.cuda.current_stream(self.device)
             side_stream.wait_stream(cur)
-            self.attn_prefill(qkv, pool_layer, out)
             with torch.cuda.stream(side_stream):  # self.stream follows the current stream
                 self.attn_decode(qkv, pool_layer, out)
+            self.attn_prefill(qkv, pool_layer, out)
             cur.wait_stream(side_stream)
             return
         if decode:

@@ -163,7 +163,30 @@ typedef struct fqa_pack_cfg {
   int32_t dec_wave_cap;      /* capacity of dec_waves (>= dec_grid_waves)  */
   int32_t pre_tile_q;        /* query rows per prefill item: 32, 64 or 128 */
   int32_t pre_item_cap;      /* capacity of pre_items                      */
+  int32_t dec_share;         /* nonzero: the decode runs beside the prefill (see below) */
 } fqa_pack_cfg;
+
+/* dec_share: the caller runs the step's decode concurrently with its prefill (the decode
+ * queued first on a second stream; fqa_step.hpp's RunLayer with a side stream, the
+ * Python AttnStep with dec_share=True).  A decode workgroup holds a CU alone (its LDS
+ * reservation), so when the batch has both decode and prefill rows the decode plan is
+ * cut to fewer wavefronts and the prefill gets the other CUs.  With N = dec_grid_waves
+ * (<= 4096; N = 4 x CUs is the device), the decode's time on G of the N wavefronts beside
+ * the prefill is modelled as D (0.72 + 0.5 N/G) (it streams HBM: half the CUs still read
+ * at ~2/3 of the rate, and the prefill beside it costs it ~22%) and the prefill's as
+ * P N / (N - G) (it is MFMA-bound), with
+ *   D = FQA_DEC_SHARE_RATE * decode pages,  P = prefill key-rows = sum n*c + n(n+1)/2
+ * (FQA_DEC_SHARE_RATE: prefill key-rows per decode page at the two kernels' measured
+ * rates on MI355X, ~78k key-rows and ~100 pages per microsecond; 0.72 and 0.5 fit the
+ * decode alone and beside config 4's prefill at 512-1024 wavefronts).  G is a multiple of
+ * 32 (one 4-wavefront workgroup per XCD, 8 XCDs, so every XCD keeps the same CUs for the
+ * prefill) in [32, N - 32]: the largest Glo with prefill <= decode, i.e.
+ * 50 P N Glo <= D (36 Glo + 25 N)(N - Glo), or Glo + 32 if the prefill there is shorter
+ * than the decode at Glo (50 P N Glo < D (36 Glo + 25 N)(N - Glo - 32)); never more
+ * than the plan without dec_share.  D and P are first shifted right together until both
+ * fit 30 bits.  Zero: the plan as without it. */
+#define FQA_DEC_SHARE_RATE 783
+#define FQA_DEC_SHARE_STEP 32
 
 /* --- host-side helpers (no device work) ------------------------------------------ */
 

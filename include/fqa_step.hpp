@@ -68,8 +68,10 @@ struct BatchInput {
 
 class StepContext {
  public:
+  // dec_share: RunLayer / RunLayerBounded will be given a side stream, so the pack plans a
+  // mixed batch's decode for the CUs the concurrent prefill leaves (fqa.h, dec_share).
   StepContext(int max_rows, int slots, int max_ctx, int64_t pool_pages, int device = 0,
-              int dec_grid_waves = 0, int dec_min_pages = 8)
+              int dec_grid_waves = 0, int dec_min_pages = 8, bool dec_share = false)
       : max_rows_(max_rows), slots_(slots), max_ctx_(max_ctx), pool_pages_(pool_pages) {
     if (slots > FQA_MAX_REQS) throw std::runtime_error("slots > FQA_MAX_REQS");
     max_blocks_ = (max_ctx + FQA_PAGE_TOKENS - 1) / FQA_PAGE_TOKENS;
@@ -79,7 +81,7 @@ class StepContext {
     dec_cap_ = fqa_dec_wave_bound(slots, dec_grid_waves);
     pre_cap_ = fqa_pre_item_bound(slots, max_rows, FQA_PRE_TILE_Q);
     cfg_ = {max_rows, max_blocks_, pool_pages, dec_grid_waves, dec_min_pages, dec_cap_, FQA_PRE_TILE_Q,
-            pre_cap_};
+            pre_cap_, dec_share ? 1 : 0};
     computed_ = DeviceBuffer<int32_t>(slots);
     n_new_ = DeviceBuffer<int32_t>(slots);
     bt_off_ = DeviceBuffer<int32_t>(slots + 1);
@@ -154,7 +156,7 @@ class StepContext {
   }
   // RunLayer for any batch within the bounds: rows and requests bounded by max_rows and
   // slots, both attention kernels launched (each does nothing without its kind of rows).
-  // With `side`, the decode runs on it after the prefill was queued (see RunLayer).
+  // With `side`, the decode runs on it beside the prefill, queued first (see RunLayer).
   void RunLayerBounded(uint16_t* qkv, const float* q_norm, const float* k_norm,
                        uint16_t* pool_layer, uint16_t* out, hipStream_t stream,
                        hipStream_t side = nullptr) const {
@@ -163,12 +165,12 @@ class StepContext {
                                  pool_pages_, 0, stream),
           "fqa_qknorm_rope_append");
     if (side) Fork(stream, side);
-    Check(fqa_prefill(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_, cu_.D(),
-                      pos_.D(), items_.D(), meta_.D(), FQA_PRE_TILE_Q, pre_cap_, out, stream),
-          "fqa_prefill");
     Check(fqa_decode(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_, dwaves_.D(),
                      dseqs_.D(), meta_.D(), dec_cap_, slots_, ws_.D(), out, side ? side : stream),
           "fqa_decode");
+    Check(fqa_prefill(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_, cu_.D(),
+                      pos_.D(), items_.D(), meta_.D(), FQA_PRE_TILE_Q, pre_cap_, out, stream),
+          "fqa_prefill");
     if (side) Join(stream, side);
   }
 
@@ -209,17 +211,19 @@ class StepContext {
           "fqa_prefill");
   }
   // The attention block of one layer (model_runtime.cu:263-278).  With `side` and a
-  // mixed batch, the prefill is queued on `stream` first and the decode on `side` after
-  // it: the two write disjoint output rows and only read the pool, and the decode's
-  // workgroups fill the CUs the prefill's tail leaves idle (config 4: 4% per step).
+  // mixed batch, the decode is queued on `side` first and the prefill on `stream` after
+  // it: the two write disjoint output rows and only read the pool.  Each decode workgroup
+  // holds a CU alone (its LDS reservation), so the decode takes its CUs first and the
+  // prefill fills the others; with dec_share the decode plan leaves the prefill a share of
+  // the CUs in proportion to its work (config 4: 0.695 -> 0.653 ms per step).
   // `stream` waits for `side` before returning.
   void RunLayer(uint16_t* qkv, const float* q_norm, const float* k_norm, uint16_t* pool_layer,
                 uint16_t* out, hipStream_t stream, hipStream_t side = nullptr) const {
     HeadNormRopeStoreKV(qkv, q_norm, k_norm, pool_layer, stream);
     if (side && has_decode_ && has_prefill_) {
       Fork(stream, side);
-      AttnPrefill(qkv, pool_layer, out, stream);
       AttnDecode(qkv, pool_layer, out, side);
+      AttnPrefill(qkv, pool_layer, out, stream);
       Join(stream, side);
       return;
     }

@@ -115,7 +115,8 @@ static int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t* bt_off,
              const int32_t* bt_pages, int max_rows, int max_blocks, int64_t pool_pages,
              int dec_grid_waves, int dec_min_pages, int dec_wave_cap, int pre_tile_q,
-             int pre_item_cap, int32_t* cu_seqlens, int32_t* qlen, int32_t* positions,
+             int pre_item_cap, int dec_share, int32_t* cu_seqlens, int32_t* qlen,
+             int32_t* positions,
              int32_t* row_req, int32_t* slot_mapping, int32_t* block_tables,
              int32_t* decode_rids, int32_t* prefill_rids, int32_t* dec_seqs,
              int32_t* dec_waves, int32_t* pre_items, int32_t* meta) {
@@ -189,6 +190,32 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
   if (W > 0) {
     int64_t gmax = (W + minp - 1) / minp;
     G = (int)(dec_grid_waves < gmax ? dec_grid_waves : gmax);
+    /* dec_share (this library's plan for a decode that runs beside the prefill, fqa.h):
+     * D = 783 * decode pages, P = prefill key-rows */
+    uint64_t P = 0;
+    if (dec_share)
+      for (int pi = 0; pi < np; ++pi) {
+        uint64_t n = (uint64_t)n_new[prefill_rids[pi]], c = (uint64_t)computed[prefill_rids[pi]];
+        P += n * c + n * (n + 1) / 2;
+      }
+    /* a multiple of 32 waves in [32, N - 32] where the modelled decode time
+     * D (36 G + 25 N) / (50 G) meets the prefill's P N / (N - G) (fqa.h) */
+    if (dec_share && P > 0 && dec_grid_waves >= 64 && dec_grid_waves <= 4096) {
+      uint64_t D = 783ull * (uint64_t)total, N = (uint64_t)dec_grid_waves;
+      while (D >= (1ull << 30) || P >= (1ull << 30)) {
+        D >>= 1;
+        P >>= 1;
+      }
+      int gs = 32, top = (dec_grid_waves - 32) / 32 * 32;
+      for (int g = 32; g <= top; g += 32) /* prefill(g) <= decode(g) */
+        if (50 * P * N * (uint64_t)g <= D * (36 * (uint64_t)g + 25 * N) * (N - (uint64_t)g))
+          gs = g;
+      { /* one step further if the prefill there ends before the decode at gs */
+        uint64_t g = (uint64_t)gs;
+        if (gs + 32 <= top && 50 * P * N * g < D * (36 * g + 25 * N) * (N - g - 32)) gs += 32;
+      }
+      if (gs < G) G = gs;
+    }
   }
   /* prefill plan: query tiles of pre_tile_q rows, ordered by key count descending
    * (longest first), ties by (prefill index, tile) ascending */

@@ -95,8 +95,8 @@ static void run_step(int R, int max_ctx, int pool_pages, int mode) {
   int32_t* items = xcalloc((size_t)item_cap * 4, 4);
   int32_t meta[16];
   int st = fqo_pack(R, computed, n_new, bt_off, bt_pages, max_rows, max_blocks, pool_pages,
-                    waves, 4, wave_cap, tile, item_cap, cu, qlen, pos, req, slot, bt, drids,
-                    prids, dseqs, dwaves, items, meta);
+                    waves, 4, wave_cap, tile, item_cap, mode == 0, cu, qlen, pos, req, slot, bt,
+                    drids, prids, dseqs, dwaves, items, meta);
   printf("step R=%d mode=%d rows=%d status=%d\n", R, mode, rows, st);
   if (st == 0 || st == 4) { /* accepted (4: a page id outside the pool, flagged only) */
     EXPECT(meta[0] == rows, "rows %d != %d", meta[0], rows);

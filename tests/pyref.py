@@ -40,7 +40,7 @@ def _cdiv(a, b):
 
 
 def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_waves,
-         dec_min_pages, dec_wave_cap, pre_tile_q, pre_item_cap):
+         dec_min_pages, dec_wave_cap, pre_tile_q, pre_item_cap, dec_share=0):
     R = len(computed)
     meta = [0] * 16
     meta[8] = R
@@ -96,6 +96,24 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
         P += pages
     W = len(runs)
     G = min(dec_grid_waves, _cdiv(W, max(1, dec_min_pages))) if W else 0
+    # dec_share: a decode beside the prefill gets a multiple of 32 wavefronts in
+    # [32, N - 32]: the largest g whose modelled prefill time P N / (N - g) is no more than
+    # the decode's D (36 g + 25 N) / (50 g), or g + 32 when the prefill there ends before
+    # the decode at g; D = 783 x decode pages, P = prefill key-rows, halved together until
+    # both fit 30 bits
+    keyrows = sum(n_new[r] * computed[r] + n_new[r] * (n_new[r] + 1) // 2 for r in pre)
+    N = dec_grid_waves
+    if dec_share and W and keyrows and 64 <= N <= 4096:
+        D, K = 783 * P, keyrows
+        while D >= 1 << 30 or K >= 1 << 30:
+            D, K = D >> 1, K >> 1
+        top = (N - 32) // 32 * 32
+        ok = [g for g in range(32, top + 1, 32)
+              if 50 * K * N * g <= D * (36 * g + 25 * N) * (N - g)]
+        g = max(ok) if ok else 32
+        if g + 32 <= top and 50 * K * N * g < D * (36 * g + 25 * N) * (N - g - 32):
+            g += 32
+        G = min(G, g)
     waves = []
     for w in range(G):
         g0, g1 = w * W // G, (w + 1) * W // G

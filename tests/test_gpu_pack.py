@@ -39,7 +39,7 @@ def rand_batch(rng, R, max_ctx=4096, pool_pages=4096, share=False):
 
 
 def run_both(gpu, comp, nnew, tabs, *, max_rows=None, max_ctx=4096, pool_pages=4096,
-             dec_grid_waves=64, dec_min_pages=2, pre_tile_q=64, max_reqs=None):
+             dec_grid_waves=64, dec_min_pages=2, pre_tile_q=64, max_reqs=None, dec_share=0):
     import torch
 
     from flashqwen_amd.step import AttnStep
@@ -51,10 +51,11 @@ def run_both(gpu, comp, nnew, tabs, *, max_rows=None, max_ctx=4096, pool_pages=4
     max_rows = max(int(np.sum(nnew)) if R else 0, 1) if max_rows is None else max_rows
     step = AttnStep(max_rows=max_rows, max_reqs=max_reqs, max_ctx=max_ctx, pool_pages=pool_pages,
                     device=gpu, dec_grid_waves=dec_grid_waves, dec_min_pages=dec_min_pages,
-                    pre_tile_q=pre_tile_q)
+                    pre_tile_q=pre_tile_q, dec_share=bool(dec_share))
     kw = dict(max_rows=max_rows, max_blocks=cfg.max_blocks, pool_pages=pool_pages,
               dec_grid_waves=dec_grid_waves, dec_min_pages=dec_min_pages,
-              dec_wave_cap=step.dec_wave_cap, pre_tile_q=pre_tile_q, pre_item_cap=step.pre_cap)
+              dec_wave_cap=step.dec_wave_cap, pre_tile_q=pre_tile_q, pre_item_cap=step.pre_cap,
+              dec_share=dec_share)
     ref = orc.pack(cfg.computed, cfg.n_new, cfg.bt_off, cfg.bt_pages, **kw)
     t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(gpu)  # noqa: E731
     pages = cfg.bt_pages if len(cfg.bt_pages) else np.zeros(1, np.int32)
@@ -94,9 +95,11 @@ def test_pack_random(gpu, seed):
     comp, nnew, tabs = rand_batch(rng, R, share=seed % 2 == 0)
     tile = int(rng.choice([32, 64, 128]))
     target = int(rng.choice([1, 7, 50, 2048]))
-    print(f"[test_pack_random] seed={seed} R={R} tile={tile} target={target}", flush=True)
+    share = seed % 3 == 1  # the decode plan for CUs shared with the prefill
+    print(f"[test_pack_random] seed={seed} R={R} tile={tile} target={target} share={share}",
+          flush=True)
     step, ref, R, kw = run_both(gpu, comp, nnew, tabs, pre_tile_q=tile, dec_grid_waves=target,
-                                dec_min_pages=int(rng.choice([0, 1, 8])))
+                                dec_min_pages=int(rng.choice([0, 1, 8])), dec_share=int(share))
     assert ref["status"] == 0
     assert_pack_equal(step, ref, R, kw)
 

@@ -49,7 +49,7 @@ def gpu_chain(cfg, qkv_host, pool, wq, wk, dev, kw, schedule=False, side_stream=
     step = AttnStep(max_rows=kw["max_rows"], max_reqs=cfg.n_reqs, max_ctx=cfg.max_ctx,
                     pool_pages=cfg.pool_pages, device=dev,
                     dec_grid_waves=kw["dec_grid_waves"], dec_min_pages=kw["dec_min_pages"],
-                    pre_tile_q=kw["pre_tile_q"])
+                    pre_tile_q=kw["pre_tile_q"], dec_share=bool(kw.get("dec_share", 0)))
     qkv = _t(qkv_host.view(np.int16), dev).view(torch.bfloat16)
     out = torch.zeros((kw["max_rows"], N_Q * HEAD_DIM), dtype=torch.bfloat16, device=dev)
     if schedule:
@@ -217,7 +217,10 @@ def test_pages_outside_pool_read_as_zeros(gpu):
 @pytest.mark.gpu
 def test_mixed_step_decode_on_side_stream(gpu):
     """Config 4 with the decode on a second stream, concurrent with the prefill: the output
-    and the pool are bit-identical to the one-stream step (the two write disjoint rows)."""
+    and the pool are bit-identical to the one-stream step (the two write disjoint rows).
+    With dec_share the decode plan is cut for the CUs the prefill leaves: the pool and the
+    prefill rows stay bit-identical, the decode rows within one bf16 step (other cuts of
+    the same streams), and the plan equals the oracle's."""
     import torch
 
     from oracle import oracle as orc
@@ -234,14 +237,28 @@ def test_mixed_step_decode_on_side_stream(gpu):
     qkv_host = synth.rand_bf16(rng, (sub.rows, QKV_STRIDE))
     wq, wk = synth.norm_weights()
     res = []
-    for side in (None, torch.cuda.Stream(device=gpu)):
+    for side, share in ((None, 0), (torch.cuda.Stream(device=gpu), 0),
+                        (torch.cuda.Stream(device=gpu), 1)):
         pool = make_pool(cfg.pool_pages, 105, gpu)
-        _, qkv, out = gpu_chain(cfg, qkv_host, pool, wq, wk, gpu, kw, schedule=True,
-                                side_stream=side)
+        kws = dict(kw, dec_share=share)
+        step, qkv, out = gpu_chain(cfg, qkv_host, pool, wq, wk, gpu, kws, schedule=True,
+                                   side_stream=side)
         res.append((out.view(torch.int16).cpu().numpy(), pool.view(torch.int16).cpu().numpy()))
+        if share:
+            ref = orc.pack(sub.computed, sub.n_new, sub.bt_off, sub.bt_pages, **kws)
+            check_pack(step, ref, sub.n_reqs, sub.rows, kws)
+            waves = int(step.meta_host()[4])
+            print(f"  dec_share: {waves} decode waves of {kw['dec_grid_waves']}", flush=True)
+            assert 4 <= waves < kw["dec_grid_waves"] and waves % 4 == 0
+            drows = ref["cu_seqlens"][ref["decode_rids"][: int(ref["meta"][1])]]
         del pool
     assert np.array_equal(res[0][0], res[1][0])
     assert np.array_equal(res[0][1], res[1][1])
+    assert np.array_equal(res[0][1], res[2][1])
+    prow = np.setdiff1d(np.arange(sub.rows), drows)
+    assert np.array_equal(res[0][0][prow], res[2][0][prow])
+    bits = lambda o: o[drows].view(np.uint16)  # noqa: E731
+    sc.assert_decode_rows_close(bits(res[2][0]), bits(res[0][0]), "dec_share")
 
 
 @pytest.mark.gpu
@@ -399,7 +416,8 @@ def test_random_steps(gpu, seed):
     tile = int(rng.choice([32, 64]))
     print(f"[test_random_steps] seed={seed} reqs={cfg.n_reqs} rows={cfg.rows} "
           f"waves={waves} min_pages={min_pages} tile={tile}", flush=True)
-    kw = sc.pack_kwargs(cfg, dec_grid_waves=waves, dec_min_pages=min_pages, pre_tile_q=tile)
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=waves, dec_min_pages=min_pages, pre_tile_q=tile,
+                        dec_share=seed % 2)
     _check_step(cfg, cfg, dict(kw, device=gpu), 500 + seed, f"random{seed}")
 
 

@@ -357,7 +357,40 @@ def test_pack_against_python_restatement(seed):
     kw["dec_wave_cap"] = kw["dec_grid_waves"]
     kw["pre_item_cap"] = kw["max_rows"] // kw["pre_tile_q"] + R
     _compare_pack(comp, nnew, tabs, kw)
+    _compare_pack(comp, nnew, tabs, dict(kw, dec_share=1))
 
+
+def test_dec_share_known_answer():
+    """The decode plan beside a concurrent prefill (dec_share), by hand.  With N = 1024,
+    D = 783 x decode pages and P = prefill key-rows, the modelled decode time on G waves is
+    D (36 G + 25 N) / (50 G), the prefill's P N / (N - G); G is the largest multiple of 32
+    where the prefill is no slower, or one step more if the prefill there ends first.
+    * 400 decode pages (D = 313200) beside a 400-row prompt on 583 cached keys
+      (P = 400*583 + 400*401/2 = 313400): with D ~ P the times meet where
+      36 G^2 + 39 N G - 25 N^2 = 0, G = 0.452 N = 463; 448 is the last multiple of 32
+      below (50 P N 448 = 7.19e12 <= D (36*448 + 25 N)(N - 448) = 7.53e12), and the
+      prefill at 480 (P N / 544 = 5.90e5) ends after the decode at 448
+      (D * 41728 / 22400 = 5.83e5): 448 (1024 without dec_share).
+    * One decode sequence of 100 keys (7 pages, 56 runs, D = 5481) beside a 64-row prompt
+      on 32 cached keys (P = 4128): the meeting point is far above the 56 runs: 56.
+    * The same decode beside a 2000-row prompt on 10000 cached keys (P = 22001000): even
+      G = 32 leaves the prefill slower, so the floor of 32 wavefronts."""
+    base = dict(max_rows=65, max_blocks=256, pool_pages=4096, dec_grid_waves=1024,
+                dec_min_pages=1, dec_wave_cap=1024, pre_tile_q=64, pre_item_cap=4)
+    tabs3 = [np.arange(400, dtype=np.int32), np.arange(400, 462, dtype=np.int32)]
+    c3 = dict(base, max_rows=401, max_blocks=512, pre_item_cap=16, dec_share=1)
+    got = orc.pack([6399, 583], [1, 400], [0, 400, 462], np.concatenate(tabs3), **c3)
+    assert got["meta"][4] == 448
+    got = orc.pack([6399, 583], [1, 400], [0, 400, 462], np.concatenate(tabs3),
+                   **dict(c3, dec_share=0))
+    assert got["meta"][4] == 1024
+    tabs = [np.arange(7, dtype=np.int32), np.arange(7, 13, dtype=np.int32)]
+    got = orc.pack([99, 32], [1, 64], [0, 7, 13], np.concatenate(tabs), **dict(base, dec_share=1))
+    assert got["meta"][4] == 56
+    tabs2 = [np.arange(7, dtype=np.int32), np.arange(7, 7 + 751, dtype=np.int32)]
+    big = dict(base, max_rows=2001, max_blocks=1024, pre_item_cap=40, dec_share=1)
+    got = orc.pack([99, 10000], [1, 2000], [0, 7, 758], np.concatenate(tabs2), **big)
+    assert got["meta"][4] == 32
 
 def test_pack_known_answer():
     # request 0: decode at context 18 (pages 5,9); request 1: 3-row chunk on a 15-token
