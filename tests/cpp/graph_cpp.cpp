@@ -5,12 +5,17 @@
 // layer's decode on a parallel branch (StepGraph's side stream).  For
 // tests/test_gpu_graph.py.
 //
+// With the environment variable FQA_DEC_SHARE=1 both runs build the context with dec_share
+// (the pack plans a mixed batch's decode for the CUs the concurrent prefill leaves) and the
+// eager run also puts decode on the side stream.
+//
 // argv: script norm_weights [out];  script as tests/cpp/serve_cpp.cpp.  Prints
 // "steps S layers L compared N mismatched M" and exits 0 iff M == 0.  With `out`, the
 // graph run's steps are written for the oracle check (little-endian, per step):
 //   int32 t, R, T; computed[R], n_new[R], bt_off[R+1], bt_pages[bt_off[R]];
 //   per layer: uint16 qkv[T*6144] (the step's input), uint16 attn[T*4096]; int32 meta[16]
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <fstream>
 #include <map>
@@ -64,6 +69,8 @@ int main(int argc, char** argv) {
     std::fclose(f);
   }
   constexpr int kLayers = 3;
+  const char* share_env = std::getenv("FQA_DEC_SHARE");
+  const bool dec_share = share_env && share_env[0] == '1';
   long long compared = 0, mismatched = 0;
   int steps_run = 0;
   try {
@@ -78,7 +85,7 @@ int main(int argc, char** argv) {
     std::vector<uint16_t> eager_pools;
 
     for (int mode = 0; mode < 2; ++mode) {
-      fqa::StepContext ctx(budget, n_slots, max_ctx, n_blocks);
+      fqa::StepContext ctx(budget, n_slots, max_ctx, n_blocks, 0, 0, 8, dec_share);
       std::vector<fqa::DeviceBuffer<uint16_t>> pool, qkv, out;
       std::vector<fqa::LayerBuffers> lb;
       for (int l = 0; l < kLayers; ++l) {
@@ -132,7 +139,8 @@ int main(int argc, char** argv) {
         fqa::BatchInput bi{b.computed, b.n_new, b.block_tables};
         if (mode == 0) {
           ctx.PrepareInputs(bi, s);
-          for (auto& l : lb) ctx.RunLayer(l.qkv, l.q_norm, l.k_norm, l.pool, l.out, s);
+          for (auto& l : lb) ctx.RunLayer(l.qkv, l.q_norm, l.k_norm, l.pool, l.out, s,
+                                     dec_share ? side : nullptr);
         } else {
           ctx.UploadBatch(bi, s);
           graph->Launch(s);

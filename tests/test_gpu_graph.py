@@ -7,11 +7,13 @@ eager run of the same workload (tests/cpp/graph_cpp), and every replay's output 
 layer is checked against the CPU oracle replaying the same steps on its own pools."""
 from __future__ import annotations
 
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 import pytest
+import torch
 
 from flashqwen_amd import synth
 from tests import stepcase as sc
@@ -21,7 +23,10 @@ EXE = Path(__file__).resolve().parent / "cpp" / "graph_cpp"
 
 
 @pytest.mark.gpu
-def test_step_graph_replays_match_eager(gpu, tmp_path):
+@pytest.mark.parametrize("dec_share", [0, 1])
+def test_step_graph_replays_match_eager(gpu, tmp_path, dec_share):
+    """dec_share=1: both runs plan each mixed batch's decode for the CUs the prefill leaves,
+    and the eager run also queues decode on the side stream."""
     if not EXE.exists():
         pytest.fail(f"{EXE} not built (run __graft_entry__.build())")
     rng = np.random.default_rng(78)
@@ -35,9 +40,12 @@ def test_step_graph_replays_match_eager(gpu, tmp_path):
     (tmp_path / "s.txt").write_text(_script((20, 6, 96, 48, True), 16, specs) + "512\n")
     wq, wk = synth.norm_weights()
     np.concatenate([wq.astype(np.float32), wk.astype(np.float32)]).tofile(tmp_path / "w.bin")
-    print("[test_step_graph_replays_match_eager] 10 seqs, 16 steps, 3 layers", flush=True)
+    print(f"[test_step_graph_replays_match_eager] 10 seqs, 16 steps, 3 layers, "
+          f"dec_share={dec_share}", flush=True)
+    env = dict(os.environ, FQA_DEC_SHARE=str(dec_share))
     r = subprocess.run([str(EXE), str(tmp_path / "s.txt"), str(tmp_path / "w.bin"),
-                        str(tmp_path / "graph.bin")], capture_output=True, text=True, timeout=120)
+                        str(tmp_path / "graph.bin")], capture_output=True, text=True,
+                       timeout=120, env=env)
     print(r.stdout.strip(), r.stderr.strip())
     assert r.returncode == 0, (r.returncode, r.stdout, r.stderr)
     steps = int(r.stdout.split()[1])
@@ -55,7 +63,9 @@ def test_step_graph_replays_match_eager(gpu, tmp_path):
         return a
 
     pools = [np.zeros(sc.pool_elems(n_blocks), np.uint16) for _ in range(layers)]
-    n_checked = 0
+    n_checked = shared = 0
+    # the decode grid StepContext takes by default: one wavefront per SIMD
+    grid = 4 * torch.cuda.get_device_properties(gpu).multi_processor_count
     while o < raw.size:
         t, R, T = (int(x) for x in take(np.int32, 3))
         computed, n_new = take(np.int32, R), take(np.int32, R)
@@ -66,12 +76,14 @@ def test_step_graph_replays_match_eager(gpu, tmp_path):
         meta = take(np.int32, 16)
         tables = [pages[off[i]:off[i + 1]] for i in range(R)]
         cfg = synth._assemble(f"step{t}", computed, n_new, tables, n_blocks, 512)
-        kw = sc.pack_kwargs(cfg, max_rows=budget, dec_grid_waves=int(meta[4]) or 1,
-                            dec_min_pages=8, max_reqs=slots)
+        kw = sc.pack_kwargs(cfg, max_rows=budget, dec_grid_waves=grid, dec_min_pages=8,
+                            max_reqs=slots, dec_share=dec_share)
         for l, (qkv_in, attn) in enumerate(per_layer):
             ref = sc.oracle_chain(cfg, qkv_in, pools[l], wq, wk, kw)
             if l == 0:
-                assert meta[:4].tolist() == ref["pack"]["meta"][:4].tolist(), t
+                # rows, decode and prefill counts, and the decode plan's wavefront count
+                assert meta[:5].tolist() == ref["pack"]["meta"][:5].tolist(), t
+                shared += int(meta[4]) < grid
                 assert meta[7] == 0
             mx, mean = sc.att_errors(attn, ref["out"])
             assert mx <= sc.ATT_MAX_ABS and mean <= sc.ATT_MEAN_ABS, (t, l, mx, mean)
@@ -79,3 +91,4 @@ def test_step_graph_replays_match_eager(gpu, tmp_path):
             n_checked += 1
         print(f"graph step {t}: R={R} T={T} checked {layers} layers (last max-abs {mx:.2e})")
     assert n_checked == steps * layers
+    print(f"steps whose decode plan left CUs to the prefill: {shared}")
