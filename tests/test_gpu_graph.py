@@ -83,7 +83,11 @@ def test_step_graph_replays_match_eager(gpu, tmp_path, dec_share):
             if l == 0:
                 # rows, decode and prefill counts, and the decode plan's wavefront count
                 assert meta[:5].tolist() == ref["pack"]["meta"][:5].tolist(), t
-                shared += int(meta[4]) < grid
+                if dec_share:  # steps whose plan the share changed
+                    from oracle import oracle as orc
+                    whole = orc.pack(cfg.computed, cfg.n_new, cfg.bt_off, cfg.bt_pages,
+                                     **dict(kw, dec_share=0))
+                    shared += int(meta[4]) != int(whole["meta"][4])
                 assert meta[7] == 0
             mx, mean = sc.att_errors(attn, ref["out"])
             assert mx <= sc.ATT_MAX_ABS and mean <= sc.ATT_MEAN_ABS, (t, l, mx, mean)
@@ -91,4 +95,6 @@ def test_step_graph_replays_match_eager(gpu, tmp_path, dec_share):
             n_checked += 1
         print(f"graph step {t}: R={R} T={T} checked {layers} layers (last max-abs {mx:.2e})")
     assert n_checked == steps * layers
-    print(f"steps whose decode plan left CUs to the prefill: {shared}")
+    # (this workload's batches are small: the share rarely moves their plans; config 4's
+    # binding share is checked in test_gpu_path.py::test_mixed_step_decode_on_side_stream)
+    print(f"steps whose decode plan the share changed: {shared}")
