@@ -28,6 +28,8 @@
 #endif
 
 #define PAGE 16
+/* pages compared for a shared decode prefix (FQA_DEC_PREFIX_CAP, include/fqa.h) */
+#define FQA_DEC_PREFIX_CAP 8192
 
 float fqo_bf16_to_f32(uint16_t b) {
   uint32_t bits = (uint32_t)b << 16;
@@ -115,11 +117,12 @@ static int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t* bt_off,
              const int32_t* bt_pages, int max_rows, int max_blocks, int64_t pool_pages,
              int dec_grid_waves, int dec_min_pages, int dec_wave_cap, int pre_tile_q,
-             int pre_item_cap, int dec_share, int32_t* cu_seqlens, int32_t* qlen,
-             int32_t* positions,
+             int pre_item_cap, int dec_share, int dec_prefix_pages, int dec_pre_cap,
+             int32_t* cu_seqlens, int32_t* qlen, int32_t* positions,
              int32_t* row_req, int32_t* slot_mapping, int32_t* block_tables,
              int32_t* decode_rids, int32_t* prefill_rids, int32_t* dec_seqs,
-             int32_t* dec_waves, int32_t* pre_items, int32_t* meta) {
+             int32_t* dec_waves, int32_t* pre_items, int32_t* dec_prefix,
+             int32_t* dec_pre_items, int32_t* meta) {
   for (int i = 0; i < 16; ++i) meta[i] = 0;
   meta[8] = R;
   /* structural checks: the smallest violated code wins */
@@ -180,10 +183,61 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
     }
   }
 
-  /* decode plan (stream-K): the (decode sequence, kv head) page streams end to end,
-   * W = 8 * total pages runs cut into G equal shares [w*W/G, (w+1)*W/G) */
+  /* Shared prefixes (this library's decode plan; the reference reads every sequence's
+   * pages itself): decode sequences with the same first page id (>= 0) form a group led
+   * by the first of them.  Each member's common prefix with the leader (its LCP, at most
+   * FQA_DEC_PREFIX_CAP pages; the leader's own is its page count) is capped at
+   * computed / 16, so that every member keeps the page of its last key; the group's
+   * prefix P is the minimum over the members.  With P >= dec_prefix_pages the members'
+   * pages [0, P) are attended once for the whole group (prefix items) and each member's
+   * decode streams cover pages [P, pages) only. */
+  int32_t* pfx = (int32_t*)calloc(nd > 0 ? nd : 1, sizeof(int32_t));    /* P per member */
+  int32_t* lead = (int32_t*)malloc(sizeof(int32_t) * (nd > 0 ? nd : 1)); /* leader or -1 */
+  int n_groups = 0, n_pitems = 0;
+  if (dec_prefix_pages > 0) {
+    for (int di = 0; di < nd; ++di) {
+      const int32_t f = bt_pages[bt_off[decode_rids[di]]];
+      int first = -1, count = 0;
+      for (int dj = 0; f >= 0 && dj < nd; ++dj)
+        if (bt_pages[bt_off[decode_rids[dj]]] == f) {
+          if (first < 0) first = dj;
+          ++count;
+        }
+      lead[di] = count >= 2 ? first : -1;
+    }
+    for (int l = 0; l < nd; ++l) {
+      if (lead[l] != l) continue; /* l leads a group */
+      const int rl = decode_rids[l], pl = computed[rl] / PAGE + 1;
+      int P = 0x7fffffff;
+      for (int di = 0; di < nd; ++di) {
+        if (lead[di] != l) continue;
+        const int r = decode_rids[di], pages = computed[r] / PAGE + 1;
+        int k = 0;
+        if (di == l) k = pages;
+        else
+          while (k < pages && k < pl && bt_pages[bt_off[r] + k] == bt_pages[bt_off[rl] + k]) ++k;
+        if (k > FQA_DEC_PREFIX_CAP) k = FQA_DEC_PREFIX_CAP;
+        if (k > computed[r] / PAGE) k = computed[r] / PAGE;
+        if (k < P) P = k;
+      }
+      if (P < dec_prefix_pages) continue;
+      int M = 0;
+      for (int di = 0; di < nd; ++di) M += lead[di] == l;
+      const int Q = (M + 3) / 4, CP = P / 16 > 16 ? (P + 15) / 16 : 16, Cn = (P + CP - 1) / CP;
+      ++n_groups;
+      n_pitems += 8 * Cn * Q;
+      for (int di = 0; di < nd; ++di)
+        if (lead[di] == l) pfx[di] = P;
+    }
+    if (n_pitems > dec_pre_cap) { /* more prefix work than the plan holds: none */
+      n_groups = n_pitems = 0;
+      for (int di = 0; di < nd; ++di) pfx[di] = 0;
+    }
+  }
+  /* decode plan (stream-K): the (decode sequence, kv head) page streams [P, pages) end to
+   * end, W = 8 * total stream pages cut into G equal shares [w*W/G, (w+1)*W/G) */
   int64_t total = 0;
-  for (int di = 0; di < nd; ++di) total += computed[decode_rids[di]] / PAGE + 1;
+  for (int di = 0; di < nd; ++di) total += computed[decode_rids[di]] / PAGE + 1 - pfx[di];
   int64_t W = 8 * total;
   int minp = dec_min_pages > 0 ? dec_min_pages : 1;
   int G = 0;
@@ -226,12 +280,14 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
     for (int i = 0; i < 16; ++i) meta[i] = 0;
     meta[8] = R;
     meta[7] = 6;
+    free(pfx);
+    free(lead);
     return 6;
   }
   {
     int64_t P = 0; /* page prefix over decode indices */
     for (int di = 0; di < nd; ++di) {
-      int r = decode_rids[di], pages = computed[r] / PAGE + 1;
+      int r = decode_rids[di], pages = computed[r] / PAGE + 1 - pfx[di];
       dec_seqs[4 * di + 0] = r;
       dec_seqs[4 * di + 1] = cu_seqlens[r];
       dec_seqs[4 * di + 2] = computed[r] + 1;
@@ -243,14 +299,14 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
     int64_t start = 0; /* 8 * P[di] */
     for (int w = 0; w < G; ++w) {
       int64_t g0 = (int64_t)w * W / G, g1 = (int64_t)(w + 1) * W / G;
-      int pages = computed[decode_rids[di]] / PAGE + 1;
+      int pages = computed[decode_rids[di]] / PAGE + 1 - pfx[di];
       while (g0 >= start + 8 * (int64_t)pages) {
         start += 8 * (int64_t)pages;
         ++di;
-        pages = computed[decode_rids[di]] / PAGE + 1;
+        pages = computed[decode_rids[di]] / PAGE + 1 - pfx[di];
       }
       int64_t rem = g0 - start;
-      int r = decode_rids[di], page = (int)(rem % pages);
+      int r = decode_rids[di], page = pfx[di] + (int)(rem % pages);
       dec_waves[8 * w + 0] = di;
       dec_waves[8 * w + 1] = (int32_t)(rem / pages);
       dec_waves[8 * w + 2] = page;
@@ -269,10 +325,48 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
       int shared = 0;
       for (int b = 0; id >= 0 && b < nd && !shared; ++b)
         shared = b != a && bt_pages[bt_off[decode_rids[b]]] == id;
-      if (shared) dec_seqs[4 * a + 2] |= 1 << 30;
+      if (shared && pfx[a] == 0) dec_seqs[4 * a + 2] |= 1 << 30; /* members: own pages */
     }
     for (int w = 0; w < G; ++w) dec_waves[8 * w + 6] |= dec_seqs[4 * dec_waves[8 * w] + 2] & (1 << 30);
   }
+  /* prefix items, groups by leader: for each kv head, chunk c of CP pages and quad q of
+   * 4 members, {leader, kvh, page0, page1, member di x 4 (-1 past the group)}; member k
+   * of a group: dec_prefix[di] = {P, first item, C | Q << 16, k} */
+  for (int di = 0; di < nd; ++di)
+    for (int k = 0; k < 8; ++k) dec_prefix[8 * di + k] = 0;
+  {
+    int item = 0;
+    for (int l = 0; l < nd && n_groups > 0; ++l) {
+      if (lead[l] != l || pfx[l] == 0) continue;
+      const int P = pfx[l];
+      int M = 0;
+      for (int di = 0; di < nd; ++di) M += lead[di] == l;
+      const int Q = (M + 3) / 4, CP = P / 16 > 16 ? (P + 15) / 16 : 16, Cn = (P + CP - 1) / CP;
+      int32_t* mem = (int32_t*)malloc(sizeof(int32_t) * 4 * Q);
+      for (int k = 0; k < 4 * Q; ++k) mem[k] = -1;
+      for (int di = 0, k = 0; di < nd; ++di)
+        if (lead[di] == l) {
+          dec_prefix[8 * di + 0] = P;
+          dec_prefix[8 * di + 1] = item;
+          dec_prefix[8 * di + 2] = Cn | (Q << 16);
+          dec_prefix[8 * di + 3] = k;
+          mem[k++] = di;
+        }
+      for (int kvh = 0; kvh < 8; ++kvh)
+        for (int c = 0; c < Cn; ++c)
+          for (int q = 0; q < Q; ++q, ++item) {
+            int32_t* it = dec_pre_items + 8 * (int64_t)item;
+            it[0] = l;
+            it[1] = kvh;
+            it[2] = c * CP;
+            it[3] = (c + 1) * CP < P ? (c + 1) * CP : P;
+            for (int j = 0; j < 4; ++j) it[4 + j] = mem[4 * q + j];
+          }
+      free(mem);
+    }
+  }
+  free(pfx);
+  free(lead);
   {
     int32_t* tmp = (int32_t*)malloc(sizeof(int32_t) * 4 * (npi > 0 ? npi : 1));
     int k = 0;
@@ -306,6 +400,8 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
   meta[6] = G ? (int32_t)((W + G - 1) / G) : 0;
   meta[7] = bad_page ? 4 : 0;
   meta[9] = (int32_t)total;
+  meta[10] = n_pitems;
+  meta[11] = n_groups;
   return meta[7];
 }
 

@@ -28,11 +28,12 @@ int fqo_schedule(int n_running, const int32_t* num_tokens, const int32_t* comput
 int fqo_pack(int n_reqs, const int32_t* computed, const int32_t* n_new, const int32_t* bt_off,
              const int32_t* bt_pages, int max_rows, int max_blocks, int64_t pool_pages,
              int dec_grid_waves, int dec_min_pages, int dec_wave_cap, int pre_tile_q,
-             int pre_item_cap, int dec_share, int32_t* cu_seqlens, int32_t* qlen,
-             int32_t* positions,
+             int pre_item_cap, int dec_share, int dec_prefix_pages, int dec_pre_cap,
+             int32_t* cu_seqlens, int32_t* qlen, int32_t* positions,
              int32_t* row_req, int32_t* slot_mapping, int32_t* block_tables,
              int32_t* decode_rids, int32_t* prefill_rids, int32_t* dec_seqs,
-             int32_t* dec_waves, int32_t* pre_items, int32_t* meta);
+             int32_t* dec_waves, int32_t* pre_items, int32_t* dec_prefix,
+             int32_t* dec_pre_items, int32_t* meta);
 
 void fqo_qknorm_rope_append(int n_q, int n_kv, int head_dim, int qkv_stride, float eps,
                             uint16_t* qkv, const float* wq, const float* wk,

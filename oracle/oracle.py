@@ -70,7 +70,7 @@ def schedule(num_tokens, computed, token_budget: int, prefill_chunk: int):
 
 def pack(computed, n_new, bt_off, bt_pages, *, max_rows, max_blocks, pool_pages,
          dec_grid_waves, dec_min_pages, dec_wave_cap, pre_tile_q, pre_item_cap,
-         dec_share=0) -> dict:
+         dec_share=0, dec_prefix_pages=0, dec_pre_cap=0) -> dict:
     computed, n_new, bt_off = i32(computed), i32(n_new), i32(bt_off)
     bt_pages = i32(bt_pages) if len(bt_pages) else np.zeros(1, np.int32)
     R = computed.shape[0]
@@ -84,13 +84,17 @@ def pack(computed, n_new, bt_off, bt_pages, *, max_rows, max_blocks, pool_pages,
         dec_seqs=np.zeros((max(R, 1), 4), np.int32),
         dec_waves=np.zeros((max(dec_wave_cap, 1), 8), np.int32),
         pre_items=np.zeros((max(pre_item_cap, 1), 4), np.int32),
+        dec_prefix=np.zeros((max(R, 1), 8), np.int32),
+        dec_pre_items=np.zeros((max(dec_pre_cap, 1), 8), np.int32),
         meta=np.zeros(16, np.int32))
     status = load().fqo_pack(
         R, _p(computed), _p(n_new), _p(bt_off), _p(bt_pages), max_rows, max_blocks,
         C.c_int64(pool_pages), dec_grid_waves, dec_min_pages, dec_wave_cap, pre_tile_q,
-        pre_item_cap, int(dec_share), *[_p(out[k]) for k in (
+        pre_item_cap, int(dec_share), int(dec_prefix_pages), int(dec_pre_cap),
+        *[_p(out[k]) for k in (
             "cu_seqlens", "qlen", "positions", "row_req", "slot_mapping", "block_tables",
-            "decode_rids", "prefill_rids", "dec_seqs", "dec_waves", "pre_items", "meta")])
+            "decode_rids", "prefill_rids", "dec_seqs", "dec_waves", "pre_items", "dec_prefix",
+            "dec_pre_items", "meta")])
     out["status"] = status
     return out
 

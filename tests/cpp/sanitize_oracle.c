@@ -93,10 +93,14 @@ static void run_step(int R, int max_ctx, int pool_pages, int mode) {
   int32_t* dseqs = xcalloc((size_t)R * 4, 4);
   int32_t* dwaves = xcalloc((size_t)wave_cap * 8, 4);
   int32_t* items = xcalloc((size_t)item_cap * 4, 4);
+  const int pre_cap = 8 * 16 * R;
+  int32_t* dpfx = xcalloc((size_t)R * 8 + 8, 4);
+  int32_t* ditems = xcalloc((size_t)pre_cap * 8 + 8, 4);
   int32_t meta[16];
   int st = fqo_pack(R, computed, n_new, bt_off, bt_pages, max_rows, max_blocks, pool_pages,
-                    waves, 4, wave_cap, tile, item_cap, mode == 0, cu, qlen, pos, req, slot, bt,
-                    drids, prids, dseqs, dwaves, items, meta);
+                    waves, 4, wave_cap, tile, item_cap, mode == 0, mode == 0 ? 2 : 0, pre_cap, cu,
+                    qlen, pos, req, slot, bt, drids, prids, dseqs, dwaves, items, dpfx, ditems,
+                    meta);
   printf("step R=%d mode=%d rows=%d status=%d\n", R, mode, rows, st);
   if (st == 0 || st == 4) { /* accepted (4: a page id outside the pool, flagged only) */
     EXPECT(meta[0] == rows, "rows %d != %d", meta[0], rows);
@@ -132,7 +136,7 @@ static void run_step(int R, int max_ctx, int pool_pages, int mode) {
   }
   free(computed), free(n_new), free(bt_off), free(bt_pages), free(perm), free(cu), free(qlen);
   free(pos), free(req), free(slot), free(bt), free(drids), free(prids), free(dseqs);
-  free(dwaves), free(items);
+  free(dwaves), free(items), free(dpfx), free(ditems);
 }
 
 static void run_schedule(int n) {

@@ -40,7 +40,8 @@ def _cdiv(a, b):
 
 
 def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_waves,
-         dec_min_pages, dec_wave_cap, pre_tile_q, pre_item_cap, dec_share=0):
+         dec_min_pages, dec_wave_cap, pre_tile_q, pre_item_cap, dec_share=0,
+         dec_prefix_pages=0, dec_pre_cap=0, prefix_cap=8192):
     R = len(computed)
     meta = [0] * 16
     meta[8] = R
@@ -83,7 +84,45 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
         bt.extend(row)
     res["block_tables"] = bt
 
-    # decode stream-K plan: concatenate streams (di, kvh), cut into G equal shares
+    # shared prefixes: decode sequences grouped by their first page id (>= 0), led by the
+    # first; a group's prefix is the shortest of its members' common runs of leading pages
+    # with the leader (capped at prefix_cap, and at computed // 16 so that every member
+    # keeps its last key's page), used when it reaches dec_prefix_pages
+    groups = {}
+    for di, r in enumerate(dec):
+        if tables[r][0] >= 0:
+            groups.setdefault(tables[r][0], []).append(di)
+    prefix = [0] * len(dec)
+    group_list = []  # (members, P), by leader
+    if dec_prefix_pages > 0:
+        for members in sorted(groups.values(), key=lambda m: m[0]):
+            if len(members) < 2:
+                continue
+            lt = tables[dec[members[0]]]
+            P = None
+            for di in members:
+                t = tables[dec[di]]
+                pages = computed[dec[di]] // PAGE + 1
+                common = 0
+                for a, b in zip(t[:pages], lt[:computed[dec[members[0]]] // PAGE + 1]):
+                    if a != b:
+                        break
+                    common += 1
+                common = min(common, prefix_cap, computed[dec[di]] // PAGE)
+                P = common if P is None else min(P, common)
+            if P >= dec_prefix_pages:
+                group_list.append((members, P))
+        n_items = 0
+        for members, P in group_list:
+            cp = max(16, -(-P // 16))
+            n_items += 8 * -(-P // cp) * -(-len(members) // 4)
+        if n_items > dec_pre_cap:
+            group_list = []
+        for members, P in group_list:
+            for di in members:
+                prefix[di] = P
+    # decode stream-K plan: concatenate streams (di, kvh) over pages [prefix, pages), cut
+    # into G equal shares
     runs = []  # (di, kvh, page) for every page run, in order
     seqs = []
     P = 0
@@ -91,9 +130,9 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
         pages = computed[r] // PAGE + 1
         seqs.append([r, res["cu_seqlens"][r], computed[r] + 1, 8 * P])
         for kvh in range(8):
-            for pg in range(pages):
+            for pg in range(prefix[di], pages):
                 runs.append((di, kvh, pg))
-        P += pages
+        P += pages - prefix[di]
     W = len(runs)
     G = min(dec_grid_waves, _cdiv(W, max(1, dec_min_pages))) if W else 0
     # dec_share: a decode beside the prefill gets a multiple of 32 wavefronts in
@@ -137,7 +176,8 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
     # (FQA_DEC_SHARED) in both n_keys fields
     from collections import Counter
     firsts = Counter(tables[r][0] for r in dec if tables[r][0] >= 0)
-    shared = [tables[r][0] >= 0 and firsts[tables[r][0]] > 1 for r in dec]
+    shared = [tables[r][0] >= 0 and firsts[tables[r][0]] > 1 and not prefix[di]
+              for di, r in enumerate(dec)]
     for di, s in enumerate(seqs):
         s[2] |= (1 << 30) if shared[di] else 0
     for wv in waves:
@@ -145,6 +185,23 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
     res["dec_seqs"] = seqs
     res["dec_waves"] = waves
     res["pre_items"] = items
+    # prefix items: per group (by leader), kv head, chunk of cp pages, quad of 4 members
+    pitems, dpfx = [], [[0, 0, 0, 0] for _ in dec]
+    for members, Pg in group_list:
+        cp = max(16, -(-Pg // 16))
+        nc, nq = -(-Pg // cp), -(-len(members) // 4)
+        base = len(pitems)
+        for k, di in enumerate(members):
+            dpfx[di] = [Pg, base, nc | (nq << 16), k]
+        padded = members + [-1] * (4 * nq - len(members))
+        for kvh in range(8):
+            for c in range(nc):
+                for q in range(nq):
+                    pitems.append([members[0], kvh, c * cp, min((c + 1) * cp, Pg)]
+                                  + padded[4 * q:4 * q + 4])
+    res["dec_prefix"] = dpfx
+    res["dec_pre_items"] = pitems
+    meta[10], meta[11] = len(pitems), len(group_list)
     meta[0] = rows_total
     meta[1], meta[2] = len(dec), len(pre)
     meta[3] = max([1] + [n_new[r] for r in pre])

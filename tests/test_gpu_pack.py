@@ -13,8 +13,12 @@ from tests import stepcase as sc
 
 
 def rand_batch(rng, R, max_ctx=4096, pool_pages=4096, share=False):
+    """share=True: tables of 4 pages or more start with the same 4 pages; share="deep":
+    tables start with the same run of 1..all of their pages (one of 3 run sets)."""
     comp, nnew, tabs = [], [], []
     shared = rng.permutation(pool_pages)[:32].astype(np.int32)
+    runs = [rng.permutation(pool_pages)[:synth.cdiv(max_ctx, synth.PAGE)].astype(np.int32)
+            for _ in range(3)]
     for _ in range(R):
         kind = rng.integers(0, 4)
         if kind == 0:  # decode
@@ -30,7 +34,10 @@ def rand_batch(rng, R, max_ctx=4096, pool_pages=4096, share=False):
         extra = int(rng.integers(0, 3))
         nb = min(need + extra, synth.cdiv(max_ctx, synth.PAGE))
         t = rng.integers(0, pool_pages, size=nb).astype(np.int32)
-        if share and nb >= 4:
+        if share == "deep":
+            k = int(rng.integers(1, nb + 1))
+            t[:k] = runs[int(rng.integers(0, 3))][:k]
+        elif share and nb >= 4:
             t[:4] = shared[:4]
         comp.append(c)
         nnew.append(n)

@@ -341,6 +341,8 @@ def _compare_pack(comp, nnew, tabs, kw):
     assert got["dec_seqs"][:nd].tolist() == ref["dec_seqs"]
     assert got["dec_waves"][:G].tolist() == ref["dec_waves"]
     assert got["pre_items"][:npi].tolist() == ref["pre_items"]
+    assert got["dec_prefix"][:nd, :4].tolist() == ref["dec_prefix"]
+    assert got["dec_pre_items"][:ref["meta"][10]].tolist() == ref["dec_pre_items"]
     return got, ref
 
 
@@ -358,6 +360,115 @@ def test_pack_against_python_restatement(seed):
     kw["pre_item_cap"] = kw["max_rows"] // kw["pre_tile_q"] + R
     _compare_pack(comp, nnew, tabs, kw)
     _compare_pack(comp, nnew, tabs, dict(kw, dec_share=1))
+    _compare_pack(comp, nnew, tabs, dict(kw, dec_prefix_pages=1, dec_pre_cap=64 * R + 8))
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_pack_prefix_groups_against_python_restatement(seed):
+    """Shared-prefix groups over tables that share leading runs of any length (1..all of
+    their pages, from 3 run sets), with and without dec_share, at minimum prefix lengths
+    1, 2 and 8 pages, and with a prefix-item capacity too small for the plan (the plan
+    then has no groups)."""
+    from tests.test_gpu_pack import rand_batch
+
+    rng = np.random.default_rng(100 + seed)
+    R = int(rng.choice([2, 9, 40, 150]))
+    comp, nnew, tabs = rand_batch(rng, R, share="deep")
+    kw = _kw(R, max_rows=max(1, int(np.sum(nnew))), dec_grid_waves=int(rng.choice([3, 64, 1024])),
+             dec_min_pages=int(rng.choice([1, 8])), pre_tile_q=64)
+    kw["dec_wave_cap"] = kw["dec_grid_waves"]
+    kw["pre_item_cap"] = kw["max_rows"] // 64 + R
+    seen = 0
+    for minp in (1, 2, 8):
+        got, ref = _compare_pack(comp, nnew, tabs, dict(kw, dec_prefix_pages=minp,
+                                                        dec_pre_cap=64 * R + 8))
+        seen += ref["meta"][11]
+        _compare_pack(comp, nnew, tabs, dict(kw, dec_prefix_pages=minp, dec_pre_cap=64 * R + 8,
+                                             dec_share=1))
+    if ref["meta"][10] > 0:
+        small = dict(kw, dec_prefix_pages=8, dec_pre_cap=ref["meta"][10] - 1)
+        got, ref2 = _compare_pack(comp, nnew, tabs, small)
+        assert ref2["meta"][10] == ref2["meta"][11] == 0
+    assert R < 40 or seen > 0
+
+
+def test_pack_prefix_known_answer():
+    """Shared-prefix groups by hand.  Decodes: r0 (41 keys, pages 5 6 7), r1 (48 keys,
+    5 6 9), r2 (21 keys, 8 1), r4 (71 keys, 5 6 7 2 3); r3 is a prefill starting at page 5
+    too (prefills neither join nor cause groups).  The group of first page 5 is led by r0
+    (decode index 0); common runs with it: r0 3 pages, capped at 40 // 16 = 2; r1 2; r4 3.
+    So P = 2: pages 0 and 1 of the three are attended once (8 items, one per kv head, one
+    chunk, one quad {0, 1, 3, -1}) and their streams start at page 2, with the shared flag
+    cleared (their own pages are private).  At dec_prefix_pages = 3 the group is not used."""
+    comp = [40, 47, 20, 0, 70]
+    nnew = [1, 1, 1, 10, 1]
+    tabs = [[5, 6, 7], [5, 6, 9], [8, 1], [5], [5, 6, 7, 2, 3]]
+    kw = _kw(5, max_rows=16, max_blocks=8, dec_grid_waves=7, dec_min_pages=1, dec_wave_cap=7,
+             pre_tile_q=32, pre_item_cap=8, pool_pages=64, dec_prefix_pages=2, dec_pre_cap=8)
+    got, _ = _compare_pack(comp, nnew, tabs, kw)
+    m = got["meta"]
+    assert (int(m[1]), int(m[9]), int(m[10]), int(m[11])) == (4, 7, 8, 1)
+    assert got["dec_prefix"][:4, :4].tolist() == [[2, 0, 1 | 1 << 16, 0], [2, 0, 1 | 1 << 16, 1],
+                                                  [0, 0, 0, 0], [2, 0, 1 | 1 << 16, 2]]
+    assert got["dec_pre_items"][:8].tolist() == [[0, h, 0, 2, 0, 1, 3, -1] for h in range(8)]
+    flag = 1 << 30
+    seqs = got["dec_seqs"][:4]
+    assert [int(z) for z in seqs[:, 2]] == [41, 48, 21, 71]  # no flags: groups read their own
+    assert [int(z) for z in seqs[:, 3]] == [0, 8, 16, 32]  # streams of 1, 1, 2, 3 pages
+    # 7 shares of 8 runs: {di, kvh, page (absolute), runs, r, row, n_keys, page id}
+    assert [list(map(int, w[:4])) + [int(w[7])] for w in got["dec_waves"][:7]] == [
+        [0, 0, 2, 8, 7], [1, 0, 2, 8, 9], [2, 0, 0, 8, 8], [2, 4, 0, 8, 8],
+        [3, 0, 2, 8, 7], [3, 2, 4, 8, 3], [3, 5, 3, 8, 2]]
+    off, _ = _compare_pack(comp, nnew, tabs, dict(kw, dec_prefix_pages=3))
+    assert (int(off["meta"][9]), int(off["meta"][10]), int(off["meta"][11])) == (13, 0, 0)
+    assert [bool(z & flag) for z in off["dec_seqs"][:4, 2]] == [True, True, False, True]
+
+
+def test_pack_prefix_covers_every_page_once():
+    """For every decode sequence and kv head, the prefix items of its group (pages
+    [page0, page1) of the leader's table, which equal the member's) and the plan's shares
+    of its stream together cover each of its pages exactly once, and each member is in
+    exactly one quad slot of its group's items per (kv head, chunk)."""
+    from tests.test_gpu_pack import rand_batch
+
+    for seed in range(6):
+        rng = np.random.default_rng(300 + seed)
+        R = 60
+        comp, nnew, tabs = rand_batch(rng, R, share="deep")
+        kw = _kw(R, max_rows=max(1, int(np.sum(nnew))), dec_grid_waves=97, dec_min_pages=3,
+                 dec_wave_cap=97, pre_tile_q=64, dec_prefix_pages=1, dec_pre_cap=64 * R)
+        kw["pre_item_cap"] = kw["max_rows"] // 64 + R
+        got, ref = _compare_pack(comp, nnew, tabs, kw)
+        meta = got["meta"]
+        nd, G, npx = int(meta[1]), int(meta[4]), int(meta[10])
+        seqs, waves = got["dec_seqs"][:nd], got["dec_waves"][:G]
+        drids = got["decode_rids"][:nd]
+        count = {}
+        for it in got["dec_pre_items"][:npx]:
+            lead, kvh, p0, p1 = (int(x) for x in it[:4])
+            for di in it[4:]:
+                if di < 0:
+                    continue
+                r, rl = int(drids[di]), int(drids[lead])
+                for p in range(p0, p1):
+                    assert tabs[r][p] == tabs[rl][p]
+                    count[(int(di), kvh, p)] = count.get((int(di), kvh, p), 0) + 1
+        # walk the shares: runs (di, kvh, page) in stream order
+        for w in waves:
+            di, kvh, page, n = (int(x) for x in w[:4])
+            while n > 0:
+                r = int(drids[di])
+                pages = comp[r] // 16 + 1
+                P = int(got["dec_prefix"][di, 0])
+                take = min(pages - page, n)
+                for p in range(page, page + take):
+                    count[(di, kvh, p)] = count.get((di, kvh, p), 0) + 1
+                n -= take
+                page = P if kvh < 7 else int(got["dec_prefix"][di + 1, 0]) if di + 1 < nd else 0
+                kvh, di = (kvh + 1, di) if kvh < 7 else (0, di + 1)
+        want = {(di, kvh, p) for di in range(nd) for kvh in range(8)
+                for p in range(comp[int(drids[di])] // 16 + 1)}
+        assert set(count) == want and all(v == 1 for v in count.values()), seed
 
 
 def test_dec_share_known_answer():
