@@ -23,6 +23,7 @@ FQA_PRE_TILE_Q = 64  # prefill rows per work item the step helpers plan with (fq
 META_ROWS, META_N_DECODE, META_N_PREFILL, META_MAX_QLEN = 0, 1, 2, 3
 META_DEC_WAVES, META_PRE_ITEMS, META_DEC_WAVE_PAGES, META_STATUS = 4, 5, 6, 7
 META_REQS, META_DEC_PAGES = 8, 9
+META_DEC_PRE_ITEMS, META_DEC_GROUPS = 10, 11
 META_LEN = 16
 
 PACK_OK, PACK_SHORT_TABLE, PACK_WIDE_TABLE, PACK_ROWS = 0, 1, 2, 3
@@ -70,6 +71,8 @@ class FqaPackOut(C.Structure):
         ("dec_waves", P),
         ("pre_items", P),
         ("meta", P),
+        ("dec_prefix", P),
+        ("dec_pre_items", P),
     ]
 
 
@@ -84,6 +87,8 @@ class FqaPackCfg(C.Structure):
         ("pre_tile_q", I32),
         ("pre_item_cap", I32),
         ("dec_share", I32),
+        ("dec_prefix_pages", I32),
+        ("dec_pre_cap", I32),
     ]
 
 
@@ -131,6 +136,12 @@ SIGNATURES = {
     "fqa_gemm_argmax_workspace_bytes": (I64, [I32, I32, I32]),
     "fqa_gemm_argmax": (C.c_int, [P, I64, P, I64, I32, I32, I32, P, P, I64, P]),
     "fqa_decode_read_floor": (C.c_int, [P, I64, P, I32, P, P, P, I32, P, P]),
+    "fqa_decode_read_floor_prefix": (C.c_int, [P, I64, P, I32, P, P, P, P, I32, P, P]),
+    "fqa_decode_prefix_workspace_bytes": (I64, [C.POINTER(FqaDims), I32, I32]),
+    "fqa_decode_prefix": (
+        C.c_int,
+        [C.POINTER(FqaDims), P, P, I64, P, I32, P, P, P, P, P, I32, I32, I32, P, P, P],
+    ),
     "fqa_version": (C.c_char_p, []),
 }
 

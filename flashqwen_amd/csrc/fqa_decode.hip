@@ -68,6 +68,13 @@ struct DecArgs {
   int stride;
   float scale_log2;  // softmax scale * log2(e): scores live in the exp2 domain
   int wave_cap;      // rows of `waves`
+  // shared-prefix plans (fqa_decode_prefix; NULL otherwise)
+  const int32_t* prefix;  // [n_decode][8] {P, first item, C | Q << 16, k}
+  const int32_t* pitems;  // [pre_cap][8] {leader, kvh, page0, page1, member x 4}
+  float* pws_m;           // prefix partials: [pre_cap][16 columns]
+  float* pws_l;
+  float* pws_acc;         // [pre_cap][16][128]
+  int pre_cap;
 };
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -223,6 +230,86 @@ __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* bt
   }
 }
 
+// The state a shared-prefix member's (kv head) stream starts from: the log-sum-exp merge
+// of its group's C chunk partials (decode_prefix_kernel) for its 4 query heads, in the
+// layout of DecState (lane: column n = head, rows d = b*16 + 4g + j; l on lane group 0).
+__device__ void prefix_state(const DecArgs& a, int di, int kvh, int lane, DecState& st) {
+  const int n = lane & 15, g = lane >> 4;
+  if (n >= kG) return;  // columns past the 4 heads carry nothing
+  const int4 info = *reinterpret_cast<const int4*>(a.prefix + 8LL * di);
+  const int C = info.z & 0xFFFF, Q = info.z >> 16, k = info.w;
+  // the pack's items fit dec_pre_cap; a workspace planned for fewer is never read past
+  if ((long long)info.y + 8LL * C * Q > a.pre_cap) return;
+  const int col = (k & 3) * kG + n;
+  auto slot = [&](int c) { return ((long long)info.y + ((long long)kvh * C + c) * Q + (k >> 2)) * 16 + col; };
+  float m0 = -1e30f;
+  for (int c = 0; c < C; ++c) m0 = fmaxf(m0, a.pws_m[slot(c)]);
+  float l = 0.f;
+  float4_t acc[8];
+#pragma unroll
+  for (int b = 0; b < 8; ++b) acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < C; ++c) {
+    const long long sl = slot(c);
+    const float wgt = __builtin_amdgcn_exp2f(a.pws_m[sl] - m0);
+    l += wgt * a.pws_l[sl];
+    const float* src = a.pws_acc + sl * kD + g * 4;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) acc[b] += wgt * *reinterpret_cast<const float4_t*>(src + b * 16);
+  }
+  st.m = m0;
+  st.l = g == 0 ? l : 0.f;
+#pragma unroll
+  for (int b = 0; b < 8; ++b) st.acc[b] = acc[b];
+}
+
+// Shared-prefix items: one wavefront per item streams pages [page0, page1) of the group
+// leader's table (which its members' tables equal there) once for the 4 query heads of
+// each of up to 4 members (the 16 MFMA columns: member j, head h at column 4j + h), with
+// the decode's page loop and arithmetic, and leaves the 16 columns' fp32 partials.
+__global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_prefix_kernel(DecArgs a) {
+  const int w = blockIdx.x * kDecWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15, g = lane >> 4;
+  const int n_items = a.meta[FQA_META_DEC_PRE_ITEMS];
+  if (w >= n_items || w >= a.pre_cap) return;
+  const int4* it = reinterpret_cast<const int4*>(a.pitems + 8LL * w);
+  const int4 i0 = it[0], i1 = it[1];
+  const int lead = __builtin_amdgcn_readfirstlane(i0.x), kvh = __builtin_amdgcn_readfirstlane(i0.y);
+  const int p0 = __builtin_amdgcn_readfirstlane(i0.z), p1 = __builtin_amdgcn_readfirstlane(i0.w);
+  const int r = __builtin_amdgcn_readfirstlane(a.seqs[4LL * lead]);
+  const int mj = (n >> 2) == 0 ? i1.x : (n >> 2) == 1 ? i1.y : (n >> 2) == 2 ? i1.z : i1.w;
+  bf16x8 qf[4];
+  if (mj >= 0) {
+    const int row = a.seqs[4LL * mj + 1];
+    const uint16_t* q = a.qkv + (long long)row * a.stride + (kvh * kG + (n & 3)) * kD + g * 8;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(q + ks * 32);
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qf[ks][i] = (__bf16)0.0f;
+  }
+  DecState st;
+#pragma unroll
+  for (int b = 0; b < 8; ++b) st.acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
+  st.m = -1e30f;
+  st.l = 0.f;
+  // every key of [page0, page1) precedes each member's own (the prefix ends at or before
+  // computed / 16 pages), so no key is masked: L = 16 * page1
+  stream_pages<kDecBufs, false>(a, a.bt + (long long)r * a.max_blocks, kvh, p0, p1, p1 * kPage,
+                                qf, lane, st, -1);
+  const float l_run = sum_rows4(st.l);
+  const long long slot = (long long)w * 16 + n;
+  if (g == 0) {
+    a.pws_m[slot] = st.m;
+    a.pws_l[slot] = l_run;
+  }
+  float* wa = a.pws_acc + slot * kD + g * 4;
+#pragma unroll
+  for (int b = 0; b < 8; ++b) *reinterpret_cast<float4_t*>(wa + b * 16) = st.acc[b];
+}
+
 // One wavefront per share of the stream-K plan.  A share walks consecutive streams:
 // the first may start mid-stream, the last may end mid-stream, the ones between are
 // whole.  Whole streams are written as bf16 output; a cut stream leaves its partial in
@@ -249,10 +336,14 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
   asm volatile("" ::"s"(desc.x), "s"(n_waves));  // both loads issued before the branch
   if (w >= n_waves) return;
   int di = desc.x, kvh = desc.y, page = desc.z, left = desc.w;
+  // shared-prefix plans: a stream covers pages [P, pages) of its sequence
+  int P = a.prefix ? __builtin_amdgcn_readfirstlane(a.prefix[8LL * di]) : 0;
   for (int seg = 0; left > 0; ++seg) {
     if (seg > 0) {
       sq = uni4(*reinterpret_cast<const int4*>(a.seqs + 4 * (long long)di));
       sq.w = -1;  // first page id of a later stream: read from the block table
+      if (a.prefix) P = __builtin_amdgcn_readfirstlane(a.prefix[8LL * di]);
+      page = P;
     }
     // sequences that share their first page read through the caches (FQA_DEC_SHARED)
     const int r = sq.x, row = sq.y, L = sq.z & FQA_DEC_KEYS_MASK;
@@ -277,6 +368,7 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
     for (int b = 0; b < 8; ++b) st.acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
     st.m = -1e30f;
     st.l = 0.f;
+    if (P > 0 && page == P) prefix_state(a, di, kvh, lane, st);  // the stream's first pages
     if (shared)
       stream_pages<kBufs, false>(a, a.bt + (long long)r * a.max_blocks, kvh, page, page + cnt, L,
                                  qf, lane, st, sq.w);
@@ -286,7 +378,7 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
     const float l_run = sum_rows4(st.l);
 
     if (n < kG) {
-      if (page == 0 && cnt == pages) {  // whole stream: final output
+      if (page == P && cnt == pages - P) {  // whole stream: final output
         const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
         uint16_t* o = a.out + (long long)row * (kHq * kD) + (kvh * kG + n) * kD + g * 4;
 #pragma unroll
@@ -307,7 +399,7 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
       }
     }
     left -= cnt;
-    page = 0;
+    page = P;
     if (++kvh == kHkv) {
       kvh = 0;
       ++di;
@@ -339,11 +431,13 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_read_floor_k
   uint32_t sink = 0;
   while (left > 0) {
     const int4 sq = *reinterpret_cast<const int4*>(a.seqs + 4 * (long long)di);
+    const int P = a.prefix ? __builtin_amdgcn_readfirstlane(a.prefix[8LL * di]) : 0;
     const int r = __builtin_amdgcn_readfirstlane(sq.x);
     const int zf = __builtin_amdgcn_readfirstlane(sq.z);
     const int L = zf & FQA_DEC_KEYS_MASK;
     const bool shared = (zf & FQA_DEC_SHARED) != 0;  // the same load hints as the decode
     const int pages = (L + kPage - 1) / kPage;
+    if (page < 0) page = P;
     const int cnt = min(pages - page, left);
     const __attribute__((address_space(4))) int32_t* btc =
         (const __attribute__((address_space(4))) int32_t*)(a.bt + (long long)r * a.max_blocks);
@@ -384,7 +478,7 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_read_floor_k
     else
       walk(std::true_type{});
     left -= cnt;
-    page = 0;
+    page = -1;  // the next stream's first page: P, known once its sequence is read
     if (++kvh == kHkv) {
       kvh = 0;
       ++di;
@@ -404,12 +498,14 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_combine_kern
   // di < n_reqs_bound, the rows of `seqs`: the sequence is read with the counts (one round
   // trip, not two)
   const int4 sq = *reinterpret_cast<const int4*>(a.seqs + 4 * (long long)di);
+  const int pfx = a.prefix ? a.prefix[8LL * di] : 0;
   const int n_dec = a.meta[FQA_META_N_DECODE];
-  asm volatile("" ::"v"(sq.x), "s"(n_dec));
+  asm volatile("" ::"v"(sq.x), "v"(pfx), "s"(n_dec));
   if (di >= n_dec) return;
   const long long G = a.meta[FQA_META_DEC_WAVES];
   const long long W = 8LL * a.meta[FQA_META_DEC_PAGES];
-  const int pages = ((sq.z & FQA_DEC_KEYS_MASK) + kPage - 1) / kPage;
+  // a stream's pages: [P, pages) with a shared prefix
+  const int pages = ((sq.z & FQA_DEC_KEYS_MASK) + kPage - 1) / kPage - pfx;
   const long long S0 = sq.w + (long long)kvh * pages, S1 = S0 + pages;
   const long long wf = ((S0 + 1) * G - 1) / W, wl = (S1 * G - 1) / W;
   if (wf == wl) return;  // finished by one wavefront
@@ -460,7 +556,8 @@ int decode_launch(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* poo
                   int64_t pool_pages, const int32_t* block_tables, int32_t max_blocks,
                   const int32_t* dec_waves, const int32_t* dec_seqs, const int32_t* meta,
                   int32_t dec_wave_cap, int32_t n_reqs_bound, float* ws, uint16_t* out,
-                  hipStream_t stream) {
+                  hipStream_t stream, const int32_t* dec_prefix = nullptr,
+                  const int32_t* dec_pre_items = nullptr, int32_t dec_pre_cap = 0) {
   if (!dims) return FQA_EINVAL;
   if (!dims_ok(dims)) return FQA_EUNSUPPORTED;
   if (dec_wave_cap < 0 || n_reqs_bound < 0 || n_reqs_bound > FQA_MAX_REQS || max_blocks < 1 ||
@@ -472,6 +569,21 @@ int decode_launch(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* poo
   const long long slots = 2LL * dec_wave_cap * kG;
   DecArgs a{qkv, pool, pool_pages, block_tables, max_blocks, dec_waves, dec_seqs, meta, ws,
             ws + slots, ws + 2 * slots, out, dims->qkv_stride, dims->scale * kLog2e, dec_wave_cap};
+  if (dec_prefix) {
+    // prefix partials after the stream partials: m, l [pre_cap][16], acc [pre_cap][16][128]
+    float* pws = ws + slots * (2 + kD);
+    const long long ps = 16LL * dec_pre_cap;
+    a.prefix = dec_prefix;
+    a.pitems = dec_pre_items;
+    a.pws_m = pws;
+    a.pws_l = pws + ps;
+    a.pws_acc = pws + 2 * ps;
+    a.pre_cap = dec_pre_cap;
+    if (dec_pre_cap > 0)
+      hipLaunchKernelGGL(decode_prefix_kernel,
+                         dim3((dec_pre_cap + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
+                         dim3(kDecWavesPerBlock * kWave), 0, stream, a);
+  }
   hipLaunchKernelGGL(decode_split_kernel<kDecBufs>,
                      dim3((dec_wave_cap + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
                      dim3(kDecWavesPerBlock * kWave), 0, stream, a);
@@ -551,18 +663,48 @@ int fqa_decode_noalloc(const fqa_dims* dims, const uint16_t* qkv, const uint16_t
                        dec_seqs, meta, dec_wave_cap, n_reqs_bound, ws, out, (hipStream_t)stream);
 }
 
-int fqa_decode_read_floor(const uint16_t* pool, int64_t pool_pages, const int32_t* block_tables,
-                          int32_t max_blocks, const int32_t* dec_waves, const int32_t* dec_seqs,
-                          const int32_t* meta, int32_t dec_wave_cap, void* sink, void* stream) {
+int fqa_decode_read_floor_prefix(const uint16_t* pool, int64_t pool_pages,
+                                 const int32_t* block_tables, int32_t max_blocks,
+                                 const int32_t* dec_waves, const int32_t* dec_seqs,
+                                 const int32_t* dec_prefix, const int32_t* meta,
+                                 int32_t dec_wave_cap, void* sink, void* stream) {
   if (dec_wave_cap < 0 || max_blocks < 1 || pool_pages < 1 || !meta) return FQA_EINVAL;
   if (dec_wave_cap == 0) return FQA_OK;
   if (!pool || !block_tables || !dec_waves || !dec_seqs || !sink) return FQA_EINVAL;
   DecArgs a{nullptr, pool, pool_pages, block_tables, max_blocks, dec_waves, dec_seqs, meta,
             static_cast<float*>(sink), nullptr, nullptr, nullptr, kQkvStride, 0.f, dec_wave_cap};
+  a.prefix = dec_prefix;
   hipLaunchKernelGGL(decode_read_floor_kernel,
                      dim3((dec_wave_cap + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
                      dim3(kDecWavesPerBlock * kWave), 0, (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;
+}
+
+int fqa_decode_read_floor(const uint16_t* pool, int64_t pool_pages, const int32_t* block_tables,
+                          int32_t max_blocks, const int32_t* dec_waves, const int32_t* dec_seqs,
+                          const int32_t* meta, int32_t dec_wave_cap, void* sink, void* stream) {
+  return fqa_decode_read_floor_prefix(pool, pool_pages, block_tables, max_blocks, dec_waves,
+                                      dec_seqs, nullptr, meta, dec_wave_cap, sink, stream);
+}
+
+int64_t fqa_decode_prefix_workspace_bytes(const fqa_dims* dims, int32_t dec_wave_cap,
+                                          int32_t dec_pre_cap) {
+  if (dec_wave_cap < 0 || dec_pre_cap < 0) return 0;
+  return fqa_decode_workspace_bytes(dims, dec_wave_cap) +
+         16LL * dec_pre_cap * (2 + kD) * (int64_t)sizeof(float);
+}
+
+int fqa_decode_prefix(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
+                      int64_t pool_pages, const int32_t* block_tables, int32_t max_blocks,
+                      const int32_t* dec_waves, const int32_t* dec_seqs,
+                      const int32_t* dec_prefix, const int32_t* dec_pre_items,
+                      const int32_t* meta, int32_t dec_wave_cap, int32_t dec_pre_cap,
+                      int32_t n_reqs_bound, void* workspace, uint16_t* out, void* stream) {
+  if (dec_pre_cap < 0 || !dec_prefix || (dec_pre_cap > 0 && !dec_pre_items)) return FQA_EINVAL;
+  return decode_launch(dims, qkv, pool, pool_pages, block_tables, max_blocks, dec_waves,
+                       dec_seqs, meta, dec_wave_cap, n_reqs_bound,
+                       static_cast<float*>(workspace), out, (hipStream_t)stream, dec_prefix,
+                       dec_pre_items, dec_pre_cap);
 }
 
 }  // extern "C"

@@ -170,6 +170,186 @@ struct PackArgs {
   fqa_pack_out o;
 };
 
+// ---- shared-prefix groups (fqa_pack_cfg::dec_prefix_pages, fqa.h) ----------------------
+// Two launches before the pack.  prefix_lcp_kernel, one workgroup per request: a decode
+// request whose first page id (>= 0) starts another decode request too finds its group's
+// leader (the smallest such request index) and the length of its common run of leading
+// page ids with the leader's table (capped at FQA_DEC_PREFIX_CAP and at computed / 16),
+// into dec_prefix[r][4] (-1 for every other request) and the leader into [r][5].
+// prefix_plan_kernel, one workgroup: each group's prefix P (the smallest of its members'),
+// the groups that reach dec_prefix_pages, their items, and per request its P
+// (dec_prefix[r][6], which the pack reads with the other per-request values).
+constexpr int kLcpThreads = 256;
+
+__global__ void __launch_bounds__(kLcpThreads) prefix_lcp_kernel(PackArgs a) {
+  __shared__ int s_lead, s_cnt, s_mis;
+  const int r = blockIdx.x, tid = threadIdx.x;
+  int R = a.b.n_reqs_dev ? *a.b.n_reqs_dev : a.b.n_reqs;
+  R = min(max(R, 0), a.b.n_reqs);
+  if (r >= R) return;
+  if (tid == 0) {
+    s_lead = INT_MAX;
+    s_cnt = 0;
+    s_mis = INT_MAX;
+  }
+  const int n = a.b.n_new[r], c = a.b.computed[r], o0 = a.b.bt_off[r], o1 = a.b.bt_off[r + 1];
+  // the pack reports malformed requests; here they only stay out of every group
+  const bool dec = n == 1 && c >= 0 && o0 >= 0 && o1 > o0;
+  const int f = dec ? a.b.bt_pages[o0] : -1;
+  __syncthreads();
+  int q = -1, lead = -1;
+  if (f >= 0) {  // uniform
+    for (int j = tid; j < R; j += kLcpThreads) {
+      const int nj = a.b.n_new[j], oj = a.b.bt_off[j], oj1 = a.b.bt_off[j + 1];
+      const int cj = a.b.computed[j];
+      const int fj = (nj == 1 && cj >= 0 && oj >= 0 && oj1 > oj) ? a.b.bt_pages[oj] : -1;
+      if (fj == f) {
+        atomicMin(&s_lead, j);
+        atomicAdd(&s_cnt, 1);
+      }
+    }
+    __syncthreads();
+    if (s_cnt >= 2) {  // uniform
+      const int L = s_lead;
+      const int pages = min(c / kPage + 1, o1 - o0);
+      int lcp;
+      if (L == r) {
+        lcp = pages;
+      } else {
+        const int ol = a.b.bt_off[L], ol1 = a.b.bt_off[L + 1];
+        const int cmp = min(min(pages, min(a.b.computed[L] / kPage + 1, ol1 - ol)),
+                            FQA_DEC_PREFIX_CAP);
+        for (int base = 0; base < cmp; base += 4 * kLcpThreads) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int k = base + 4 * tid + e;
+            if (k < cmp && a.b.bt_pages[o0 + k] != a.b.bt_pages[ol + k]) atomicMin(&s_mis, k);
+          }
+          __syncthreads();
+          if (s_mis < cmp) break;  // uniform
+        }
+        lcp = min(s_mis, cmp);
+      }
+      q = min(min(lcp, FQA_DEC_PREFIX_CAP), c / kPage);
+      lead = L;
+    }
+  }
+  if (tid == 0) {
+    a.o.dec_prefix[8LL * r + 4] = q;
+    a.o.dec_prefix[8LL * r + 5] = lead;
+  }
+}
+
+__global__ void __launch_bounds__(kPackThreads) prefix_plan_kernel(PackArgs a) {
+  __shared__ int s_q[FQA_MAX_REQS], s_lead[FQA_MAX_REQS], s_di[FQA_MAX_REQS];
+  __shared__ int s_gmin[FQA_MAX_REQS], s_gcnt[FQA_MAX_REQS], s_gbase[FQA_MAX_REQS];
+  __shared__ int s_goff[FQA_MAX_REQS], s_mem[FQA_MAX_REQS], s_glist[FQA_MAX_REQS + 1];
+  __shared__ int sh[kPackWaves];
+  const int tid = threadIdx.x;
+  int R = a.b.n_reqs_dev ? *a.b.n_reqs_dev : a.b.n_reqs;
+  R = min(max(R, 0), a.b.n_reqs);
+  const int minp = a.c.dec_prefix_pages;
+  constexpr int kPasses = FQA_MAX_REQS / kPackThreads;
+  // per request: its LCP result, leader, and decode index (exclusive scan of n == 1)
+  int carry = 0;
+#pragma unroll
+  for (int pass = 0; pass < kPasses; ++pass) {
+    const int r = pass * kPackThreads + tid;
+    int isdec = 0;
+    if (r < R) {
+      const int q = a.o.dec_prefix[8LL * r + 4];
+      s_q[r] = q;
+      s_lead[r] = a.o.dec_prefix[8LL * r + 5];
+      isdec = a.b.n_new[r] == 1;
+      s_gmin[r] = INT_MAX;
+      s_gcnt[r] = 0;
+    }
+    int tot;
+    const int e = block_excl_scan(isdec, sh, &tot);
+    if (r < R) s_di[r] = isdec ? carry + e : -1;
+    carry += tot;
+  }
+  lds_sync();
+  for (int r = tid; r < R; r += kPackThreads)
+    if (s_q[r] >= 0) {
+      atomicMin(&s_gmin[s_lead[r]], s_q[r]);
+      atomicAdd(&s_gcnt[s_lead[r]], 1);
+    }
+  lds_sync();
+  // per leader (request order): items and members of its group if it is used
+  int carry_items = 0, carry_mem = 0, carry_groups = 0;
+#pragma unroll
+  for (int pass = 0; pass < kPasses; ++pass) {
+    const int r = pass * kPackThreads + tid;
+    int items = 0, mem = 0, grp = 0;
+    if (r < R && s_q[r] >= 0 && s_lead[r] == r && s_gmin[r] >= minp) {
+      const int P = s_gmin[r], M = s_gcnt[r];
+      const int CP = P / 16 > 16 ? (P + 15) / 16 : 16;
+      items = 8 * ((P + CP - 1) / CP) * ((M + 3) / 4);
+      mem = M;
+      grp = 1;
+    }
+    int ti, tm, tg;
+    const int ei = block_excl_scan(items, sh, &ti);
+    const int em = block_excl_scan(mem, sh, &tm);
+    const int eg = block_excl_scan(grp, sh, &tg);
+    if (r < R) {
+      s_gbase[r] = carry_items + ei;
+      s_goff[r] = carry_mem + em;
+      if (grp) s_glist[carry_groups + eg] = r;
+    }
+    carry_items += ti;
+    carry_mem += tm;
+    carry_groups += tg;
+  }
+  const bool use = carry_groups > 0 && carry_items <= a.c.dec_pre_cap;
+  const int n_items = use ? carry_items : 0, n_groups = use ? carry_groups : 0;
+  lds_sync();
+  // each member's rank in its group (members by request index = by decode index) and P
+  for (int r = tid; r < R; r += kPackThreads) {
+    const int L = s_lead[r];
+    int P = 0;
+    if (use && s_q[r] >= 0 && s_gmin[L] >= minp) {
+      P = s_gmin[L];
+      int k = 0;
+      for (int j = L; j < r; ++j) k += s_q[j] >= 0 && s_lead[j] == L;
+      s_mem[s_goff[L] + k] = s_di[r];
+      const int M = s_gcnt[L], CP = P / 16 > 16 ? (P + 15) / 16 : 16;
+      const int C = (P + CP - 1) / CP, Q = (M + 3) / 4;
+      *reinterpret_cast<int4*>(a.o.dec_prefix + 8LL * s_di[r]) =
+          make_int4(P, s_gbase[L], C | (Q << 16), k);
+    } else if (s_di[r] >= 0) {
+      *reinterpret_cast<int4*>(a.o.dec_prefix + 8LL * s_di[r]) = make_int4(0, 0, 0, 0);
+    }
+    a.o.dec_prefix[8LL * r + 6] = P;
+  }
+  if (tid == 0) {
+    s_glist[n_groups] = INT_MAX;
+    a.o.dec_prefix[7] = n_items | (n_groups << 20);
+  }
+  lds_sync();
+  // the items: group (binary search over the groups' first items), then kv head, chunk,
+  // quad
+  for (int i = tid; i < n_items; i += kPackThreads) {
+    int lo = 0, hi = n_groups - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_gbase[s_glist[mid]] <= i) lo = mid; else hi = mid - 1;
+    }
+    const int L = s_glist[lo], P = s_gmin[L], M = s_gcnt[L];
+    const int CP = P / 16 > 16 ? (P + 15) / 16 : 16;
+    const int C = (P + CP - 1) / CP, Q = (M + 3) / 4;
+    const int local = i - s_gbase[L];
+    const int qd = local % Q, ch = (local / Q) % C, kvh = local / (Q * C);
+    int m[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m[j] = 4 * qd + j < M ? s_mem[s_goff[L] + 4 * qd + j] : -1;
+    int4* dst = reinterpret_cast<int4*>(a.o.dec_pre_items + 8LL * i);
+    dst[0] = make_int4(s_di[L], kvh, ch * CP, min((ch + 1) * CP, P));
+    dst[1] = make_int4(m[0], m[1], m[2], m[3]);
+  }
+}
+
 __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   __shared__ int s_comp[FQA_MAX_REQS];
   __shared__ int s_n[FQA_MAX_REQS];
@@ -178,7 +358,8 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   __shared__ int s_decidx[FQA_MAX_REQS + 1];
   __shared__ int s_preidx[FQA_MAX_REQS + 1];
   __shared__ int s_dstart[FQA_MAX_REQS + 1];  // by decode index: 8 * page prefix
-  __shared__ int s_dpages[FQA_MAX_REQS];      // by decode index: pages
+  __shared__ int s_dpages[FQA_MAX_REQS];      // by decode index: stream pages
+  __shared__ int s_dpfx[FQA_MAX_REQS];        // by decode index: shared-prefix pages
   __shared__ int s_drid[FQA_MAX_REQS];        // by decode index: request
   __shared__ int s_dflag[FQA_MAX_REQS];       // by decode index: first page id, then the flag
   __shared__ int s_prer[FQA_MAX_REQS];        // by prefill index: request
@@ -220,7 +401,9 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     // a decode sequence's first page id, for the shared-prefix check below (in flight
     // across the scan's barriers; other lanes re-read their own table offset)
     const int first = *(n == 1 && o0 >= 0 && o1 > o0 ? a.b.bt_pages + o0 : a.b.bt_off + rc);
-    if (r >= R) c = n = o0 = 0;
+    // pages of its shared prefix (prefix_plan_kernel), which its decode streams skip
+    int pfx = a.c.dec_prefix_pages > 0 ? a.o.dec_prefix[8LL * rc + 6] : 0;
+    if (r >= R) c = n = o0 = pfx = 0;
     if (r < R) {
       int cc = 0;
       if (c < 0 || n < 0) cc = FQA_PACK_NEGATIVE;
@@ -230,7 +413,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
         else if (nb > maxb) cc = FQA_PACK_WIDE_TABLE;
         st.v[1] = min(st.v[1] + min(n, kPartCap), kPartCap + 1);
         if (n == 1) {
-          const int pg = c / kPage + 1;
+          const int pg = c / kPage + 1 - pfx;
           st.v[2] = min(st.v[2] + min(pg, kPartCap), kPartCap + 1);
           st.v[3] = max(pg, st.v[3]);
         } else {
@@ -241,7 +424,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       v.v[0] = n;
       v.v[1] = n == 1;
       v.v[2] = n != 1;
-      v.v[3] = n == 1 ? c / kPage + 1 : 0;  // pages of a decode stream
+      v.v[3] = n == 1 ? c / kPage + 1 - pfx : 0;  // pages of a decode stream
       v.v[4] = n != 1 ? (n + QT - 1) / QT : 0;
     }
     const bool last = base + kPackThreads >= R;
@@ -259,7 +442,8 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       s_preidx[r] = pi;
       if (n == 1) {
         s_dstart[di] = 8 * (carry.v[3] + e.v[3]);
-        s_dpages[di] = c / kPage + 1;
+        s_dpages[di] = c / kPage + 1 - pfx;
+        s_dpfx[di] = pfx;
         s_drid[di] = r;
         s_dflag[di] = first;
       } else {
@@ -323,7 +507,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     di = upper_index(s_dstart, nd, (int)g0);
     const int rem = (int)g0 - s_dstart[di], pg = s_dpages[di];
     kvh = rem / pg;
-    page = rem % pg;
+    page = s_dpfx[di] + rem % pg;
     n = (int)(g1 - g0);
     r = s_drid[di];
   };
@@ -408,7 +592,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
           break;
         }
     }
-    s_dflag[d] = shared ? FQA_DEC_SHARED : 0;
+    s_dflag[d] = shared && s_dpfx[d] == 0 ? FQA_DEC_SHARED : 0;  // a group member's own pages
   }
 
   // ---- prefill items, sorted by key count descending (stable) --------------------
@@ -479,6 +663,8 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   }
 
   if (blockIdx.x != 0) return;
+  // the shared-prefix item and group counts (prefix_plan_kernel)
+  const int pre_counts = a.c.dec_prefix_pages > 0 ? a.o.dec_prefix[7] : 0;
   // ---- workgroup 0: per-request arrays, meta, page-range check -------------------
   for (int r = tid; r <= R; r += kPackThreads) {
     a.o.cu_seqlens[r] = s_qstart[r];
@@ -534,6 +720,8 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       case FQA_META_STATUS: v = bad ? FQA_PACK_PAGE_RANGE : FQA_PACK_OK; break;
       case FQA_META_REQS: v = R; break;
       case FQA_META_DEC_PAGES: v = (int)dpages; break;
+      case FQA_META_DEC_PRE_ITEMS: v = pre_counts & 0xFFFFF; break;
+      case FQA_META_DEC_GROUPS: v = pre_counts >> 20; break;
       default: v = 0;
     }
     a.o.meta[tid] = v;
@@ -824,7 +1012,17 @@ int fqa_pack(const fqa_batch* batch, const fqa_pack_cfg* cfg, const fqa_pack_out
   if (cfg->max_rows > work) work = cfg->max_rows;
   long long grid = (work + kPackThreads - 1) / kPackThreads;
   grid = grid < 1 ? 1 : (grid > 256 ? 256 : grid);
+  if (cfg->dec_prefix_pages < 0 || (cfg->dec_prefix_pages > 0 && cfg->dec_pre_cap < 0))
+    return FQA_EINVAL;
+  if (cfg->dec_prefix_pages > 0 && (!out->dec_prefix || (cfg->dec_pre_cap > 0 && !out->dec_pre_items)))
+    return FQA_EINVAL;
   PackArgs a{*batch, *cfg, *out};
+  if (cfg->dec_prefix_pages > 0 && R > 0) {
+    hipLaunchKernelGGL(prefix_lcp_kernel, dim3((unsigned)R), dim3(kLcpThreads), 0,
+                       (hipStream_t)stream, a);
+    hipLaunchKernelGGL(prefix_plan_kernel, dim3(1), dim3(kPackThreads), 0, (hipStream_t)stream,
+                       a);
+  }
   hipLaunchKernelGGL(pack_kernel, dim3((unsigned)grid), dim3(kPackThreads), 0,
                      (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? FQA_OK : FQA_ELAUNCH;

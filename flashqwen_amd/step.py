@@ -64,9 +64,12 @@ class AttnStep:
     def __init__(self, *, max_rows: int, max_reqs: int, max_ctx: int, pool_pages: int,
                  device="cuda", dec_grid_waves: int | None = None, dec_min_pages: int = 8,
                  pre_tile_q: int = _lib.FQA_PRE_TILE_Q, max_bt_pages: int | None = None,
-                 dec_share: bool = False):
+                 dec_share: bool = False, dec_prefix_pages: int = 0, dec_pre_cap: int = 4096):
         """dec_share: run_layer will be given a side stream, so a step with both decode
-        and prefill rows plans its decode for the CUs the prefill leaves (fqa.h)."""
+        and prefill rows plans its decode for the CUs the prefill leaves (fqa.h).
+        dec_prefix_pages > 0: decode sequences sharing a prefix of at least that many pages
+        attend it once per group (fqa.h, dec_prefix_pages), with up to dec_pre_cap prefix
+        items per step (past that the step plans without groups)."""
         self.lib = _lib.load()
         if max_reqs > _lib.FQA_MAX_REQS:
             raise ValueError(f"max_reqs {max_reqs} > {_lib.FQA_MAX_REQS}")
@@ -82,9 +85,11 @@ class AttnStep:
         self.dec_wave_cap = int(self.lib.fqa_dec_wave_bound(max_reqs, dec_grid_waves))
         self.pre_cap = int(self.lib.fqa_pre_item_bound(max_reqs, max_rows, pre_tile_q))
         self.dec_share = bool(dec_share)
+        self.dec_prefix_pages = int(dec_prefix_pages)
+        self.dec_pre_cap = int(dec_pre_cap) if dec_prefix_pages > 0 else 0
         self.cfg = FqaPackCfg(max_rows, self.max_blocks, pool_pages, dec_grid_waves,
                               dec_min_pages, self.dec_wave_cap, pre_tile_q, self.pre_cap,
-                              int(dec_share))
+                              int(dec_share), self.dec_prefix_pages, self.dec_pre_cap)
         i32 = dict(dtype=torch.int32, device=self.device)
         R = max_reqs
         self.cu_seqlens = torch.zeros(R + 1, **i32)
@@ -99,7 +104,10 @@ class AttnStep:
         self.dec_waves = torch.zeros((max(self.dec_wave_cap, 1), 8), **i32)
         self.pre_items = torch.zeros((max(self.pre_cap, 1), 4), **i32)
         self.meta = torch.zeros(_lib.META_LEN, **i32)
-        ws = int(self.lib.fqa_decode_workspace_bytes(C.byref(self.dims), self.dec_wave_cap))
+        self.dec_prefix = torch.zeros((max(R, 1), 8), **i32)
+        self.dec_pre_items = torch.zeros((max(self.dec_pre_cap, 1), 8), **i32)
+        ws = int(self.lib.fqa_decode_prefix_workspace_bytes(C.byref(self.dims), self.dec_wave_cap,
+                                                            self.dec_pre_cap))
         self.workspace = torch.empty(max(ws, 16), dtype=torch.uint8, device=self.device)
         cos, sin = rope_tables(max_ctx)
         self.cos = torch.from_numpy(cos).to(self.device)
@@ -108,7 +116,8 @@ class AttnStep:
             _ptr(t) for t in (self.cu_seqlens, self.qlen, self.positions, self.row_req,
                               self.slot_mapping, self.block_tables, self.decode_rids,
                               self.prefill_rids, self.dec_seqs, self.dec_waves,
-                              self.pre_items, self.meta)])
+                              self.pre_items, self.meta, self.dec_prefix,
+                              self.dec_pre_items)])
         # device-side selection buffers (schedule_and_prepare)
         self.max_bt_pages = max_bt_pages if max_bt_pages is not None else R * self.max_blocks
         self.sel_req = torch.zeros(R, **i32)
@@ -177,7 +186,16 @@ class AttnStep:
             self.stream), "fqa_qknorm_rope_append")
 
     def attn_decode(self, qkv, pool_layer, out):
-        """LaunchAttnDecodeCute: split-K decode + combine."""
+        """LaunchAttnDecodeCute: split-K decode + combine (with dec_prefix_pages, the
+        groups' shared prefixes first)."""
+        if self.dec_prefix_pages > 0:
+            check(self.lib.fqa_decode_prefix(
+                C.byref(self.dims), _ptr(qkv), _ptr(pool_layer), self.pool_pages,
+                _ptr(self.block_tables), self.max_blocks, _ptr(self.dec_waves),
+                _ptr(self.dec_seqs), _ptr(self.dec_prefix), _ptr(self.dec_pre_items),
+                _ptr(self.meta), self.dec_wave_cap, self.dec_pre_cap, self.n_reqs_bound,
+                _ptr(self.workspace), _ptr(out), self.stream), "fqa_decode_prefix")
+            return
         check(self.lib.fqa_decode(
             C.byref(self.dims), _ptr(qkv), _ptr(pool_layer), self.pool_pages,
             _ptr(self.block_tables), self.max_blocks, _ptr(self.dec_waves),
@@ -187,10 +205,11 @@ class AttnStep:
     def decode_read_floor(self, pool_layer):
         """Read the decode plan's pages with fqa_decode's loads and no arithmetic (the HBM
         floor of this plan); the sink is the decode workspace."""
-        check(self.lib.fqa_decode_read_floor(
+        check(self.lib.fqa_decode_read_floor_prefix(
             _ptr(pool_layer), self.pool_pages, _ptr(self.block_tables), self.max_blocks,
-            _ptr(self.dec_waves), _ptr(self.dec_seqs), _ptr(self.meta), self.dec_wave_cap,
-            _ptr(self.workspace), self.stream), "fqa_decode_read_floor")
+            _ptr(self.dec_waves), _ptr(self.dec_seqs),
+            _ptr(self.dec_prefix) if self.dec_prefix_pages > 0 else None, _ptr(self.meta),
+            self.dec_wave_cap, _ptr(self.workspace), self.stream), "fqa_decode_read_floor")
 
     def attn_prefill(self, qkv, pool_layer, out):
         """LaunchAttnPrefillCute: varlen causal FA-2."""

@@ -72,6 +72,9 @@ extern "C" {
 #define FQA_DEC_SHARED (1 << 30)
 #define FQA_DEC_KEYS_MASK (FQA_DEC_SHARED - 1)
 #define FQA_MAX_REQS 2048 /* max requests in one step (reference: `slots`, args.h:13) */
+/* Pages of a decode sequence compared with its group leader's for a shared prefix
+ * (fqa_pack_cfg::dec_prefix_pages). */
+#define FQA_DEC_PREFIX_CAP 8192
 
 /* Indices into the int32 `meta` array written by fqa_pack. */
 enum {
@@ -84,7 +87,9 @@ enum {
   FQA_META_DEC_WAVE_PAGES = 6, /* max page runs one decode wavefront streams */
   FQA_META_STATUS = 7,       /* 0 or an FQA_PACK_* code                       */
   FQA_META_REQS = 8,         /* R                                             */
-  FQA_META_DEC_PAGES = 9,    /* sum over decode sequences of their pages      */
+  FQA_META_DEC_PAGES = 9,    /* sum over decode sequences of their stream pages */
+  FQA_META_DEC_PRE_ITEMS = 10, /* shared-prefix items (dec_prefix_pages)        */
+  FQA_META_DEC_GROUPS = 11,  /* shared-prefix groups                            */
   FQA_META_LEN = 16
 };
 
@@ -152,6 +157,11 @@ typedef struct fqa_pack_out {
   int32_t* dec_waves;      /* [dec_wave_cap][8] see the decode plan above     */
   int32_t* pre_items;      /* [pre_cap][4] {r, q0, q1, n_keys}                */
   int32_t* meta;           /* [FQA_META_LEN]                                  */
+  /* with dec_prefix_pages (otherwise NULL): */
+  int32_t* dec_prefix;     /* [R][8] per decode index {P, first item, C | Q << 16, k};
+                              columns 4..7 are the pack's working space         */
+  int32_t* dec_pre_items;  /* [dec_pre_cap][8] {leader di, kvh, page0, page1,
+                              member di x 4 (-1 past the group)}                */
 } fqa_pack_out;
 
 typedef struct fqa_pack_cfg {
@@ -164,7 +174,27 @@ typedef struct fqa_pack_cfg {
   int32_t pre_tile_q;        /* query rows per prefill item: 32, 64 or 128 */
   int32_t pre_item_cap;      /* capacity of pre_items                      */
   int32_t dec_share;         /* nonzero: the decode runs beside the prefill (see below) */
+  int32_t dec_prefix_pages;  /* >0: attend shared decode prefixes of at least this many
+                                pages once per group (see below); 0: off            */
+  int32_t dec_pre_cap;       /* capacity of dec_pre_items                    */
 } fqa_pack_cfg;
+
+/* dec_prefix_pages (shared-prefix decode): decode sequences whose first page id (>= 0)
+ * is the same form a group, led by the first of them in decode order.  Each member's
+ * common prefix with the leader (the longest run of equal leading page ids, at most
+ * FQA_DEC_PREFIX_CAP pages; the leader's is its own page count) is capped at
+ * computed / 16 pages (every member keeps the page of its last key); the group's prefix
+ * P is the smallest over its members.  When P >= dec_prefix_pages, keys [0, 16 P) of
+ * every member are attended once for the whole group: the group's M members in quads of
+ * 4 (Q = ceil(M/4)), its P pages in C chunks of CP = max(16, ceil(P/16)) pages, one
+ * prefix item per (kv head, chunk, quad), in that order, groups by leader:
+ * dec_pre_items[i] = {leader, kvh, c*CP, min((c+1)*CP, P), the quad's member decode
+ * indices}.  Member k of the group (by decode index) gets dec_prefix[di] = {P, the
+ * group's first item, C | Q << 16, k} and its decode streams cover pages [P, pages) only
+ * (the plan above with pages - P in place of pages, and dec_waves' page counted from the
+ * sequence's first page, so from P on; the shared flag is not set on it).
+ * If the groups need more than dec_pre_cap items, none is used.  Decode with
+ * fqa_decode_prefix: fqa_decode does not read these arrays. */
 
 /* dec_share: the caller runs the step's decode concurrently with its prefill (the decode
  * queued first on a second stream; fqa_step.hpp's RunLayer with a side stream, the
@@ -318,6 +348,24 @@ int fqa_decode(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
                int32_t dec_wave_cap, int32_t n_reqs_bound, void* workspace, uint16_t* out,
                void* stream);
 
+/* fqa_decode over a plan made with dec_prefix_pages (fqa_pack_cfg): first one wavefront
+ * per prefix item attends pages [page0, page1) of its group's leader for the 4 query heads
+ * of each of its (up to 4) members, at the decode's precision, leaving fp32 partials; then
+ * the split kernel starts each member's (kv head) stream from the log-sum-exp merge of its
+ * C chunk partials, and the combine runs as in fqa_decode.  dec_prefix / dec_pre_items
+ * are the pack's arrays, dec_pre_cap their capacity (0: no prefix items).  `workspace`
+ * must hold fqa_decode_prefix_workspace_bytes(dims, dec_wave_cap, dec_pre_cap) bytes.
+ * The same output as fqa_decode up to fp32 rounding (the prefix keys are summed in
+ * chunks, then merged). */
+int64_t fqa_decode_prefix_workspace_bytes(const fqa_dims* dims, int32_t dec_wave_cap,
+                                          int32_t dec_pre_cap);
+int fqa_decode_prefix(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
+                      int64_t pool_pages, const int32_t* block_tables, int32_t max_blocks,
+                      const int32_t* dec_waves, const int32_t* dec_seqs,
+                      const int32_t* dec_prefix, const int32_t* dec_pre_items,
+                      const int32_t* meta, int32_t dec_wave_cap, int32_t dec_pre_cap,
+                      int32_t n_reqs_bound, void* workspace, uint16_t* out, void* stream);
+
 /* fqa_decode without a workspace argument, for callers that cannot allocate device memory
  * (code under HIP graph capture, serving loops and harnesses that forbid hipMalloc).  No
  * counterpart in the reference.  The partials live in a fixed device array of the library
@@ -438,6 +486,13 @@ int fqa_qkv_proj_append(const fqa_dims* dims, const uint16_t* x, int64_t ldx,
 int fqa_decode_read_floor(const uint16_t* pool, int64_t pool_pages, const int32_t* block_tables,
                           int32_t max_blocks, const int32_t* dec_waves, const int32_t* dec_seqs,
                           const int32_t* meta, int32_t dec_wave_cap, void* sink, void* stream);
+/* The same over a plan made with dec_prefix_pages: the streams' pages only (the prefix
+ * items' reads are not included). */
+int fqa_decode_read_floor_prefix(const uint16_t* pool, int64_t pool_pages,
+                                 const int32_t* block_tables, int32_t max_blocks,
+                                 const int32_t* dec_waves, const int32_t* dec_seqs,
+                                 const int32_t* dec_prefix, const int32_t* meta,
+                                 int32_t dec_wave_cap, void* sink, void* stream);
 
 /* Library version string. */
 const char* fqa_version(void);

@@ -332,7 +332,7 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
   /* prefix items, groups by leader: for each kv head, chunk c of CP pages and quad q of
    * 4 members, {leader, kvh, page0, page1, member di x 4 (-1 past the group)}; member k
    * of a group: dec_prefix[di] = {P, first item, C | Q << 16, k} */
-  for (int di = 0; di < nd; ++di)
+  for (int di = 0; dec_prefix && di < nd; ++di) /* NULL when dec_prefix_pages is 0 */
     for (int k = 0; k < 8; ++k) dec_prefix[8 * di + k] = 0;
   {
     int item = 0;

@@ -62,10 +62,10 @@ int fqa_qknorm_rope(const fqa_dims*, uint16_t*, const float*, const float*, cons
 int fqa_pack(const fqa_batch* b, const fqa_pack_cfg* c, const fqa_pack_out* o, void*) {
   fqo_pack(b->n_reqs, b->computed, b->n_new, b->bt_off, b->bt_pages, c->max_rows,
            c->max_blocks, c->pool_pages, c->dec_grid_waves, c->dec_min_pages, c->dec_wave_cap,
-           c->pre_tile_q, c->pre_item_cap, c->dec_share, o->cu_seqlens, o->qlen, o->positions,
-           o->row_req,
-           o->slot_mapping, o->block_tables, o->decode_rids, o->prefill_rids, o->dec_seqs,
-           o->dec_waves, o->pre_items, o->meta);
+           c->pre_tile_q, c->pre_item_cap, c->dec_share, c->dec_prefix_pages, c->dec_pre_cap,
+           o->cu_seqlens, o->qlen, o->positions, o->row_req, o->slot_mapping, o->block_tables,
+           o->decode_rids, o->prefill_rids, o->dec_seqs, o->dec_waves, o->pre_items,
+           o->dec_prefix, o->dec_pre_items, o->meta);
   return FQA_OK;
 }
 }
@@ -182,8 +182,9 @@ int main() {
           it((size_t)ctx.PreItemCap() * 4), meta(16);
       fqo_pack(R, comp.data(), nnew.data(), off.data(), pages.empty() ? off.data() : pages.data(),
                T + 4, mb, 0x7fffffff, 1024, 8, ctx.DecWaveCap(), FQA_PRE_TILE_Q,
-               ctx.PreItemCap(), 0, cu.data(), ql.data(), pos.data(), req.data(), slot.data(),
-               bt.data(), dr.data(), pr.data(), ds.data(), dw.data(), it.data(), meta.data());
+               ctx.PreItemCap(), 0, 0, 0, cu.data(), ql.data(), pos.data(), req.data(),
+               slot.data(), bt.data(), dr.data(), pr.data(), ds.data(), dw.data(), it.data(),
+               nullptr, nullptr, meta.data());
       EXPECT(!std::memcmp(meta.data(), ctx.Meta(), 16 * 4), "meta");
       EXPECT(!std::memcmp(pos.data(), ctx.pos.D(), T * 4), "positions");
       EXPECT(!std::memcmp(slot.data(), ctx.SlotMapping(), T * 4), "slot mapping");

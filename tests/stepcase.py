@@ -15,7 +15,7 @@ ATT_MEAN_ABS = 2e-3
 
 
 def pack_kwargs(cfg: synth.StepConfig, max_rows=None, dec_grid_waves=1024, dec_min_pages=8,
-                pre_tile_q=64, max_reqs=None, dec_share=0):
+                pre_tile_q=64, max_reqs=None, dec_share=0, dec_prefix_pages=0, dec_pre_cap=0):
     from oracle import oracle as orc  # noqa: F401  (tests only)
 
     R = cfg.n_reqs if max_reqs is None else max_reqs
@@ -24,7 +24,8 @@ def pack_kwargs(cfg: synth.StepConfig, max_rows=None, dec_grid_waves=1024, dec_m
     return dict(max_rows=max_rows, max_blocks=cfg.max_blocks, pool_pages=cfg.pool_pages,
                 dec_grid_waves=dec_grid_waves, dec_min_pages=dec_min_pages,
                 dec_wave_cap=dec_grid_waves, pre_tile_q=pre_tile_q, pre_item_cap=pre_cap,
-                dec_share=int(dec_share))
+                dec_share=int(dec_share), dec_prefix_pages=int(dec_prefix_pages),
+                dec_pre_cap=int(dec_pre_cap) if dec_prefix_pages else 0)
 
 
 def pool_elems(pages: int) -> int:

@@ -46,7 +46,8 @@ def rand_batch(rng, R, max_ctx=4096, pool_pages=4096, share=False):
 
 
 def run_both(gpu, comp, nnew, tabs, *, max_rows=None, max_ctx=4096, pool_pages=4096,
-             dec_grid_waves=64, dec_min_pages=2, pre_tile_q=64, max_reqs=None, dec_share=0):
+             dec_grid_waves=64, dec_min_pages=2, pre_tile_q=64, max_reqs=None, dec_share=0,
+             dec_prefix_pages=0, dec_pre_cap=4096):
     import torch
 
     from flashqwen_amd.step import AttnStep
@@ -58,11 +59,13 @@ def run_both(gpu, comp, nnew, tabs, *, max_rows=None, max_ctx=4096, pool_pages=4
     max_rows = max(int(np.sum(nnew)) if R else 0, 1) if max_rows is None else max_rows
     step = AttnStep(max_rows=max_rows, max_reqs=max_reqs, max_ctx=max_ctx, pool_pages=pool_pages,
                     device=gpu, dec_grid_waves=dec_grid_waves, dec_min_pages=dec_min_pages,
-                    pre_tile_q=pre_tile_q, dec_share=bool(dec_share))
+                    pre_tile_q=pre_tile_q, dec_share=bool(dec_share),
+                    dec_prefix_pages=dec_prefix_pages, dec_pre_cap=dec_pre_cap)
     kw = dict(max_rows=max_rows, max_blocks=cfg.max_blocks, pool_pages=pool_pages,
               dec_grid_waves=dec_grid_waves, dec_min_pages=dec_min_pages,
               dec_wave_cap=step.dec_wave_cap, pre_tile_q=pre_tile_q, pre_item_cap=step.pre_cap,
-              dec_share=dec_share)
+              dec_share=dec_share, dec_prefix_pages=dec_prefix_pages,
+              dec_pre_cap=step.dec_pre_cap)
     ref = orc.pack(cfg.computed, cfg.n_new, cfg.bt_off, cfg.bt_pages, **kw)
     t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(gpu)  # noqa: E731
     pages = cfg.bt_pages if len(cfg.bt_pages) else np.zeros(1, np.int32)
@@ -92,6 +95,11 @@ def assert_pack_equal(step, ref, R, kw):
     nd, npi = int(meta[4]), int(meta[5])
     assert np.array_equal(step.dec_waves.cpu().numpy()[:nd], ref["dec_waves"][:nd])
     assert np.array_equal(step.pre_items.cpu().numpy()[:npi], ref["pre_items"][:npi])
+    if kw.get("dec_prefix_pages", 0) > 0:
+        npx = int(meta[10])
+        assert np.array_equal(step.dec_prefix.cpu().numpy()[:nd_seq, :4],
+                              ref["dec_prefix"][:nd_seq, :4])
+        assert np.array_equal(step.dec_pre_items.cpu().numpy()[:npx], ref["dec_pre_items"][:npx])
 
 
 @pytest.mark.gpu
@@ -109,6 +117,29 @@ def test_pack_random(gpu, seed):
                                 dec_min_pages=int(rng.choice([0, 1, 8])), dec_share=int(share))
     assert ref["status"] == 0
     assert_pack_equal(step, ref, R, kw)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(8))
+def test_pack_prefix_groups(gpu, seed):
+    """Shared-prefix groups (dec_prefix_pages): tables sharing leading runs of any length,
+    bit-exact against the oracle, with a prefix-item capacity that holds the plan and, on
+    odd seeds, one item short of it (no groups then)."""
+    rng = np.random.default_rng(500 + seed)
+    R = int(rng.choice([2, 20, 90, 400]))
+    comp, nnew, tabs = rand_batch(rng, R, share="deep")
+    minp = int(rng.choice([1, 2, 8]))
+    print(f"[test_pack_prefix_groups] seed={seed} R={R} min_pages={minp}", flush=True)
+    step, ref, R, kw = run_both(gpu, comp, nnew, tabs, dec_grid_waves=int(rng.choice([7, 1024])),
+                                dec_prefix_pages=minp, dec_share=seed % 3 == 0)
+    assert ref["status"] in (0, 4)
+    assert_pack_equal(step, ref, R, kw)
+    npx = int(ref["meta"][10])
+    if seed % 2 and npx > 0:
+        step, ref, R, kw = run_both(gpu, comp, nnew, tabs, dec_prefix_pages=minp,
+                                    dec_pre_cap=npx - 1)
+        assert int(ref["meta"][10]) == int(ref["meta"][11]) == 0
+        assert_pack_equal(step, ref, R, kw)
 
 
 @pytest.mark.gpu

@@ -49,7 +49,9 @@ def gpu_chain(cfg, qkv_host, pool, wq, wk, dev, kw, schedule=False, side_stream=
     step = AttnStep(max_rows=kw["max_rows"], max_reqs=cfg.n_reqs, max_ctx=cfg.max_ctx,
                     pool_pages=cfg.pool_pages, device=dev,
                     dec_grid_waves=kw["dec_grid_waves"], dec_min_pages=kw["dec_min_pages"],
-                    pre_tile_q=kw["pre_tile_q"], dec_share=bool(kw.get("dec_share", 0)))
+                    pre_tile_q=kw["pre_tile_q"], dec_share=bool(kw.get("dec_share", 0)),
+                    dec_prefix_pages=kw.get("dec_prefix_pages", 0),
+                    dec_pre_cap=kw.get("dec_pre_cap", 4096) or 4096)
     qkv = _t(qkv_host.view(np.int16), dev).view(torch.bfloat16)
     out = torch.zeros((kw["max_rows"], N_Q * HEAD_DIM), dtype=torch.bfloat16, device=dev)
     if schedule:
@@ -79,6 +81,11 @@ def check_pack(step, ref_pk, R, T, kw):
     nd, npi = int(meta[4]), int(meta[5])
     assert np.array_equal(step.dec_waves.cpu().numpy()[:nd], ref_pk["dec_waves"][:nd])
     assert np.array_equal(step.pre_items.cpu().numpy()[:npi], ref_pk["pre_items"][:npi])
+    if kw.get("dec_prefix_pages", 0) > 0:
+        npx = int(meta[10])
+        assert np.array_equal(step.dec_prefix.cpu().numpy()[: meta[1], :4],
+                              ref_pk["dec_prefix"][: meta[1], :4])
+        assert np.array_equal(step.dec_pre_items.cpu().numpy()[:npx], ref_pk["dec_pre_items"][:npx])
 
 
 def _check_step(cfg, sub, kw, seed, label, schedule=False, kernel_only=True):
@@ -189,6 +196,52 @@ def test_decode_long_and_shared_prefix(gpu):
     cfg = synth.config5(layers=1, pool_pages=70000)
     kw = sc.pack_kwargs(cfg, dec_grid_waves=1024, dec_min_pages=8)
     _check_step(cfg, cfg, dict(kw, device=gpu), 105, "config5", kernel_only=False)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("minp", [8, 1])
+def test_decode_shared_prefix_groups(gpu, minp):
+    """Config 5's decode batch with its shared prefixes attended once per group
+    (dec_prefix_pages): 4 groups of 24 sequences whose first 128 pages are the same; each
+    group's prefix items (8 kv heads x 8 chunks of 16 pages x 6 quads) leave partials that
+    start every member's streams at page 128.  Plan bit-exact against the oracle, decode
+    rows within tolerance and within one bf16 step of the oracle per element."""
+    print(f"[test_decode_shared_prefix_groups] config5, 1 layer, min pages {minp}", flush=True)
+    cfg = synth.config5(layers=1, pool_pages=70000)
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=1024, dec_min_pages=8, dec_prefix_pages=minp,
+                        dec_pre_cap=4096)
+    _check_step(cfg, cfg, dict(kw, device=gpu), 107, f"config5-prefix{minp}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(4))
+def test_decode_prefix_random_groups(gpu, seed):
+    """Random decode batches whose tables share leading runs of any length (groups of 2
+    or more with prefixes from 1 page up, chunked prefixes, quads with fewer than 4
+    members), beside prefill rows; the whole step against the oracle."""
+    rng = np.random.default_rng(700 + seed)
+    R = int(rng.choice([12, 40, 120]))
+    pool_pages = 16384
+    perm = iter(rng.permutation(pool_pages).astype(np.int32).tolist())
+    runs = [[next(perm) for _ in range(128)] for _ in range(3)]  # shared leading runs
+    comp, nnew, tabs = [], [], []
+    for _ in range(R):
+        dec = rng.random() < 0.7
+        c = int(rng.integers(0, 2000))
+        n = 1 if dec else int(rng.integers(2, 300))
+        nb = synth.cdiv(c + n, PAGE)
+        # a shared run covers only pages that hold cached keys of every reader (no row of
+        # this step writes into them); the rest are the request's own
+        k = min(int(rng.integers(0, nb + 1)), c // PAGE, 128)
+        run = runs[int(rng.integers(0, 3))]
+        tabs.append(np.array(run[:k] + [next(perm) for _ in range(nb - k)], np.int32))
+        comp.append(c)
+        nnew.append(n)
+    cfg = synth._assemble(f"prefix-rand{seed}", comp, nnew, tabs, pool_pages, 4096)
+    print(f"[test_decode_prefix_random_groups] seed={seed} R={R} rows={cfg.rows}", flush=True)
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=int(rng.choice([64, 1024])), dec_min_pages=2,
+                        dec_prefix_pages=1, dec_pre_cap=4096)
+    _check_step(cfg, cfg, dict(kw, device=gpu), 800 + seed, f"prefix-rand{seed}")
 
 
 @pytest.mark.gpu
