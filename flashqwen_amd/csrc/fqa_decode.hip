@@ -242,19 +242,33 @@ __device__ void prefix_state(const DecArgs& a, int di, int kvh, int lane, DecSta
   if ((long long)info.y + 8LL * C * Q > a.pre_cap) return;
   const int col = (k & 3) * kG + n;
   auto slot = [&](int c) { return ((long long)info.y + ((long long)kvh * C + c) * Q + (k >> 2)) * 16 + col; };
-  float m0 = -1e30f;
-  for (int c = 0; c < C; ++c) m0 = fmaxf(m0, a.pws_m[slot(c)]);
-  float l = 0.f;
+  // online log-sum-exp merge, 4 chunks' loads in flight at a time
+  float m0 = -1e30f, l = 0.f;
   float4_t acc[8];
 #pragma unroll
   for (int b = 0; b < 8; ++b) acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
-  for (int c = 0; c < C; ++c) {
-    const long long sl = slot(c);
-    const float wgt = __builtin_amdgcn_exp2f(a.pws_m[sl] - m0);
-    l += wgt * a.pws_l[sl];
-    const float* src = a.pws_acc + sl * kD + g * 4;
+  for (int c0 = 0; c0 < C; c0 += 4) {
+    float mc[4], lc[4];
+    float4_t xc[4][8];
 #pragma unroll
-    for (int b = 0; b < 8; ++b) acc[b] += wgt * *reinterpret_cast<const float4_t*>(src + b * 16);
+    for (int j = 0; j < 4; ++j) {
+      const long long sl = slot(min(c0 + j, C - 1));
+      mc[j] = a.pws_m[sl];
+      lc[j] = a.pws_l[sl];
+      const float* src = a.pws_acc + sl * kD + g * 4;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) xc[j][b] = *reinterpret_cast<const float4_t*>(src + b * 16);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (c0 + j >= C) break;
+      const float mn = fmaxf(m0, mc[j]);
+      const float co = __builtin_amdgcn_exp2f(m0 - mn), cn = __builtin_amdgcn_exp2f(mc[j] - mn);
+      l = l * co + lc[j] * cn;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) acc[b] = acc[b] * co + xc[j][b] * cn;
+      m0 = mn;
+    }
   }
   st.m = m0;
   st.l = g == 0 ? l : 0.f;
@@ -489,9 +503,10 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_read_floor_k
 
 // Log-sum-exp merge of a cut stream's partials (attn_cute.cu:225-238): one wave per
 // (decode sequence, kv head) stream, lane -> (head = lane/16, 8 dims).  The shares that
-// cut stream s = [S0, S1) are w_first..w_last (share w = [w*W/G, (w+1)*W/G)); the
-// stream is the last of w_first's streams (slot 2w+1), or its first (slot 2w) when
-// w_first's share starts exactly at S0, and the first of every later share (slot 2w).
+// hold stream s's page positions [F, S1) are w_first..w_last (share w = [w*W/G,
+// (w+1)*W/G)); the stream is the last of w_first's streams (slot 2w+1), or its first
+// (slot 2w) when w_first's share starts in s's own cost span [S0, F], and the first of
+// every later share (slot 2w).
 __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_combine_kernel(DecArgs a) {
   const int wave = blockIdx.x * kDecWavesPerBlock + (threadIdx.x >> 6);
   const int di = wave >> 3, kvh = wave & 7;
@@ -503,11 +518,13 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_combine_kern
   asm volatile("" ::"v"(sq.x), "v"(pfx), "s"(n_dec));
   if (di >= n_dec) return;
   const long long G = a.meta[FQA_META_DEC_WAVES];
-  const long long W = 8LL * a.meta[FQA_META_DEC_PAGES];
+  // the plan's cost positions (fqa.h): each stream's start positions, then its pages
+  const long long W = 8LL * (a.meta[FQA_META_DEC_PAGES] + (long long)FQA_DEC_STREAM_COST * n_dec);
   // a stream's pages: [P, pages) with a shared prefix
   const int pages = ((sq.z & FQA_DEC_KEYS_MASK) + kPage - 1) / kPage - pfx;
-  const long long S0 = sq.w + (long long)kvh * pages, S1 = S0 + pages;
-  const long long wf = ((S0 + 1) * G - 1) / W, wl = (S1 * G - 1) / W;
+  const long long S0 = sq.w + (long long)kvh * (pages + FQA_DEC_STREAM_COST);
+  const long long F = S0 + FQA_DEC_STREAM_COST, S1 = F + pages;  // page positions [F, S1)
+  const long long wf = ((F + 1) * G - 1) / W, wl = (S1 * G - 1) / W;
   if (wf == wl) return;  // finished by one wavefront
   const int lane = threadIdx.x & 63;
   const int h = lane >> 4, d0 = (lane & 15) * 8;
@@ -519,7 +536,8 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_combine_kern
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const long long w = w0 + k;
-      const long long sl = (w == wf && wf * W / G != S0) ? 2 * w + 1 : 2 * w;
+      // the stream is wf's first unless wf's share starts in an earlier stream
+      const long long sl = (w == wf && wf * W / G < S0) ? 2 * w + 1 : 2 * w;
       const long long slot = (w <= wl ? sl : 2 * wf) * kG + h;  // beyond wl: harmless reread
       m[k] = a.ws_m[slot];
       l[k] = a.ws_l[slot];

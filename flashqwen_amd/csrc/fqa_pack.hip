@@ -357,7 +357,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   __shared__ int s_btoff[FQA_MAX_REQS + 1];
   __shared__ int s_decidx[FQA_MAX_REQS + 1];
   __shared__ int s_preidx[FQA_MAX_REQS + 1];
-  __shared__ int s_dstart[FQA_MAX_REQS + 1];  // by decode index: 8 * page prefix
+  __shared__ int s_dstart[FQA_MAX_REQS + 1];  // by decode index: 8 * cost prefix
   __shared__ int s_dpages[FQA_MAX_REQS];      // by decode index: stream pages
   __shared__ int s_dpfx[FQA_MAX_REQS];        // by decode index: shared-prefix pages
   __shared__ int s_drid[FQA_MAX_REQS];        // by decode index: request
@@ -424,7 +424,8 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       v.v[0] = n;
       v.v[1] = n == 1;
       v.v[2] = n != 1;
-      v.v[3] = n == 1 ? c / kPage + 1 - pfx : 0;  // pages of a decode stream
+      // a decode stream's cost in the plan: its pages plus the per-stream overhead
+      v.v[3] = n == 1 ? c / kPage + 1 - pfx + FQA_DEC_STREAM_COST : 0;
       v.v[4] = n != 1 ? (n + QT - 1) / QT : 0;
     }
     const bool last = base + kPackThreads >= R;
@@ -458,9 +459,10 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     for (int k = 0; k < 5; ++k) carry.v[k] += tot.v[k];
   }
   const int nd = carry.v[1], np = carry.v[2], npi = carry.v[4];
-  // decode plan: W page runs (8 kv heads x pages) cut into G equal shares
+  // decode plan: W = 8 x (stream pages + FQA_DEC_STREAM_COST per stream) cost units cut
+  // into G equal shares
   const int dpages = st.v[2];
-  const long long W = 8LL * dpages;
+  const long long W = 8LL * ((long long)dpages + (long long)FQA_DEC_STREAM_COST * nd);
   if (tid == 0) {
     s_btoff[R] = bt_end;
     s_qstart[R] = carry.v[0];
@@ -489,7 +491,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     if (a.c.dec_share)  // CUs shared with a concurrent prefill (fqa.h)
       G = min(G, dec_share_waves(a.c.dec_grid_waves, dpages, s_keyrows));
   }
-  if (G > a.c.dec_wave_cap || npi > a.c.pre_item_cap || dpages > INT_MAX / 8) {
+  if (G > a.c.dec_wave_cap || npi > a.c.pre_item_cap || W > INT_MAX) {
     if (blockIdx.x == 0 && tid < FQA_META_LEN)
       a.o.meta[tid] = tid == FQA_META_STATUS ? FQA_PACK_ITEMS : (tid == FQA_META_REQS ? R : 0);
     return;
@@ -502,13 +504,26 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     r = upper_index(s_qstart, R, t);
     p = s_comp[r] + (t - s_qstart[r]);
   };
+  // Cost position x lies in stream (d, h) at offset off: the stream's first
+  // FQA_DEC_STREAM_COST positions are its overhead, then one per page.  Pages before x:
+  auto locate = [&](int x, int& d, int& h, int& off) {
+    d = upper_index(s_dstart, nd, x);
+    if (d >= nd) {  // x == W
+      h = off = 0;
+      return dpages * 8;
+    }
+    const int rem = x - s_dstart[d], cost = s_dpages[d] + FQA_DEC_STREAM_COST;
+    h = rem / cost;
+    off = rem % cost;
+    return s_dstart[d] - 8 * FQA_DEC_STREAM_COST * d + h * s_dpages[d] +
+           max(0, off - FQA_DEC_STREAM_COST);
+  };
   auto wave_of = [&](int w, int& di, int& kvh, int& page, int& n, int& r) {
-    const long long g0 = (long long)w * W / G, g1 = (long long)(w + 1) * W / G;
-    di = upper_index(s_dstart, nd, (int)g0);
-    const int rem = (int)g0 - s_dstart[di], pg = s_dpages[di];
-    kvh = rem / pg;
-    page = s_dpfx[di] + rem % pg;
-    n = (int)(g1 - g0);
+    const int g0 = (int)((long long)w * W / G), g1 = (int)((long long)(w + 1) * W / G);
+    int off, d1, h1, o1;
+    const int p0 = locate(g0, di, kvh, off);
+    n = locate(g1, d1, h1, o1) - p0;
+    page = s_dpfx[di] + max(0, off - FQA_DEC_STREAM_COST);
     r = s_drid[di];
   };
   auto bt_of = [&](int e, int& r, int& g) {

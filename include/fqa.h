@@ -72,6 +72,10 @@ extern "C" {
 #define FQA_DEC_SHARED (1 << 30)
 #define FQA_DEC_KEYS_MASK (FQA_DEC_SHARED - 1)
 #define FQA_MAX_REQS 2048 /* max requests in one step (reference: `slots`, args.h:13) */
+/* Cost of starting a decode stream in the stream-K plan, in page runs: each (sequence,
+ * kv head) stream counts its pages plus this, so a wavefront whose share holds many short
+ * streams gets fewer pages (a stream start costs a few dependent loads). */
+#define FQA_DEC_STREAM_COST 4
 /* Pages of a decode sequence compared with its group leader's for a shared prefix
  * (fqa_pack_cfg::dec_prefix_pages). */
 #define FQA_DEC_PREFIX_CAP 8192
@@ -84,7 +88,7 @@ enum {
   FQA_META_MAX_QLEN = 3,     /* max(1, max prefill qlen) (model_runtime.cu:82) */
   FQA_META_DEC_WAVES = 4,    /* decode wavefronts with work this step         */
   FQA_META_PRE_ITEMS = 5,    /* prefill work items (request, query tile)      */
-  FQA_META_DEC_WAVE_PAGES = 6, /* max page runs one decode wavefront streams */
+  FQA_META_DEC_WAVE_PAGES = 6, /* cost of a decode share (>= the pages it streams) */
   FQA_META_STATUS = 7,       /* 0 or an FQA_PACK_* code                       */
   FQA_META_REQS = 8,         /* R                                             */
   FQA_META_DEC_PAGES = 9,    /* sum over decode sequences of their stream pages */
@@ -133,15 +137,19 @@ typedef struct fqa_batch {
 /* Everything the pack writes (device arrays, caller-allocated at capacity).
  *
  * Decode plan (stream-K): the decode requests' (sequence, kv head) page streams are laid
- * end to end, stream (di, kvh) covering P[di]*8 + kvh*pages[di] .. + pages[di], where
- * pages = ceil(n_keys/16) and P is the exclusive prefix of pages over decode indices.
- * The W = 8*sum(pages) page runs are cut into G = min(dec_grid_waves,
+ * end to end in cost units, stream (di, kvh) of pages[di] pages costing
+ * c = pages[di] + FQA_DEC_STREAM_COST: it spans [X[di]*8 + kvh*c, + c), where pages =
+ * ceil(n_keys/16) and X is the exclusive prefix of the costs over decode indices; the
+ * first FQA_DEC_STREAM_COST positions of a stream stand for its start, the others for its
+ * pages in order.  The W = 8*sum(c) positions are cut into G = min(dec_grid_waves,
  * ceil(W/dec_min_pages)) equal contiguous shares, share w = [floor(w*W/G),
- * floor((w+1)*W/G)), one per decode wavefront; dec_waves[w] = {di, kvh, page, n_runs,
- * r, row, n_keys, page id} is where share w starts, how long it is, the first stream's
- * request, row and key count, and its first page (so a wavefront's first loads need no
- * further lookups).  dec_seqs[di] = {r, row = qstart[r], n_keys = computed[r]+1,
- * 8*P[di]}.  The n_keys fields of both carry FQA_DEC_SHARED.  Prefill plan: one item
+ * floor((w+1)*W/G)), one per decode wavefront, which streams the pages whose positions
+ * fall in it; dec_waves[w] = {di, kvh, page, n_runs, r, row, n_keys, page id} is the
+ * stream and page it starts at (a share that starts in a stream's start positions starts
+ * at its first page), how many pages it streams, the first stream's request, row and
+ * key count, and its first page (so a wavefront's first loads need no further lookups).
+ * dec_seqs[di] = {r, row = qstart[r], n_keys = computed[r]+1,
+ * 8*X[di]}.  The n_keys fields of both carry FQA_DEC_SHARED.  Prefill plan: one item
  * per pre_tile_q query rows of each prefill request, pre_items[i] = {r, q0, q1,
  * n_keys = computed + q1}, ordered by n_keys descending (stable). */
 typedef struct fqa_pack_out {

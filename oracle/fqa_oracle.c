@@ -30,6 +30,8 @@
 #define PAGE 16
 /* pages compared for a shared decode prefix (FQA_DEC_PREFIX_CAP, include/fqa.h) */
 #define FQA_DEC_PREFIX_CAP 8192
+/* per-stream start cost of the decode plan, in page runs (FQA_DEC_STREAM_COST, fqa.h) */
+#define FQA_DEC_STREAM_COST 4
 
 float fqo_bf16_to_f32(uint16_t b) {
   uint32_t bits = (uint32_t)b << 16;
@@ -235,10 +237,12 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
     }
   }
   /* decode plan (stream-K): the (decode sequence, kv head) page streams [P, pages) end to
-   * end, W = 8 * total stream pages cut into G equal shares [w*W/G, (w+1)*W/G) */
+   * end in cost positions (FQA_DEC_STREAM_COST start positions, then one per page),
+   * W = 8 * (total stream pages + FQA_DEC_STREAM_COST per sequence) cut into G equal
+   * shares [w*W/G, (w+1)*W/G) */
   int64_t total = 0;
   for (int di = 0; di < nd; ++di) total += computed[decode_rids[di]] / PAGE + 1 - pfx[di];
-  int64_t W = 8 * total;
+  int64_t W = 8 * (total + (int64_t)FQA_DEC_STREAM_COST * nd);
   int minp = dec_min_pages > 0 ? dec_min_pages : 1;
   int G = 0;
   if (W > 0) {
@@ -276,7 +280,7 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
   int npi = 0;
   for (int pi = 0; pi < np; ++pi) npi += ceil_div(n_new[prefill_rids[pi]], pre_tile_q);
 
-  if (G > dec_wave_cap || npi > pre_item_cap || total > 0x7fffffff / 8) {
+  if (G > dec_wave_cap || npi > pre_item_cap || W > 0x7fffffff) {
     for (int i = 0; i < 16; ++i) meta[i] = 0;
     meta[8] = R;
     meta[7] = 6;
@@ -285,37 +289,58 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
     return 6;
   }
   {
-    int64_t P = 0; /* page prefix over decode indices */
+    int64_t X = 0; /* cost prefix over decode indices */
     for (int di = 0; di < nd; ++di) {
       int r = decode_rids[di], pages = computed[r] / PAGE + 1 - pfx[di];
       dec_seqs[4 * di + 0] = r;
       dec_seqs[4 * di + 1] = cu_seqlens[r];
       dec_seqs[4 * di + 2] = computed[r] + 1;
-      dec_seqs[4 * di + 3] = (int32_t)(8 * P);
-      P += pages;
+      dec_seqs[4 * di + 3] = (int32_t)(8 * X);
+      X += pages + FQA_DEC_STREAM_COST;
     }
-    /* share w starts at global run g0: find its stream by walking the sequences */
-    int di = 0;
-    int64_t start = 0; /* 8 * P[di] */
+    /* Position x: the sequence, kv head and offset in the stream's cost span, and the
+     * pages at positions below x (every stream's pages come after its start positions). */
+    int64_t* pstart = (int64_t*)malloc(sizeof(int64_t) * (nd + 1)); /* 8 * page prefix */
+    pstart[0] = 0;
+    for (int di = 0; di < nd; ++di)
+      pstart[di + 1] = pstart[di] + 8 * (int64_t)(computed[decode_rids[di]] / PAGE + 1 - pfx[di]);
     for (int w = 0; w < G; ++w) {
       int64_t g0 = (int64_t)w * W / G, g1 = (int64_t)(w + 1) * W / G;
-      int pages = computed[decode_rids[di]] / PAGE + 1 - pfx[di];
-      while (g0 >= start + 8 * (int64_t)pages) {
-        start += 8 * (int64_t)pages;
-        ++di;
-        pages = computed[decode_rids[di]] / PAGE + 1 - pfx[di];
+      int64_t below[2];
+      int di = 0, kvh = 0, off = 0;
+      for (int e = 1; e >= 0; --e) { /* g1, then g0 (whose stream is the share's start) */
+        const int64_t x = e ? g1 : g0;
+        int64_t start = 0;
+        int d = 0;
+        while (d < nd) {
+          const int64_t cost = computed[decode_rids[d]] / PAGE + 1 - pfx[d] + FQA_DEC_STREAM_COST;
+          if (x < start + 8 * cost) break;
+          start += 8 * cost;
+          ++d;
+        }
+        if (d == nd) {
+          below[e] = pstart[nd];
+          continue;
+        }
+        const int64_t len = computed[decode_rids[d]] / PAGE + 1 - pfx[d];
+        const int64_t cost = len + FQA_DEC_STREAM_COST, rem = x - start;
+        const int64_t o = rem % cost, skip = o > FQA_DEC_STREAM_COST ? o - FQA_DEC_STREAM_COST : 0;
+        below[e] = pstart[d] + (rem / cost) * len + skip;
+        di = d;
+        kvh = (int)(rem / cost);
+        off = (int)skip;
       }
-      int64_t rem = g0 - start;
-      int r = decode_rids[di], page = pfx[di] + (int)(rem % pages);
+      int r = decode_rids[di], page = pfx[di] + off;
       dec_waves[8 * w + 0] = di;
-      dec_waves[8 * w + 1] = (int32_t)(rem / pages);
+      dec_waves[8 * w + 1] = kvh;
       dec_waves[8 * w + 2] = page;
-      dec_waves[8 * w + 3] = (int32_t)(g1 - g0);
+      dec_waves[8 * w + 3] = (int32_t)(below[1] - below[0]);
       dec_waves[8 * w + 4] = r;
       dec_waves[8 * w + 5] = cu_seqlens[r];
       dec_waves[8 * w + 6] = computed[r] + 1;
       dec_waves[8 * w + 7] = bt_pages[bt_off[r] + page];
     }
+    free(pstart);
     /* A decode sequence whose first page is also another decode sequence's first page
      * (a shared prefix) carries the shared flag (bit 30, FQA_DEC_SHARED in fqa.h) in both
      * n_keys fields; a negative id is never shared.  This build's load-hint policy; the

@@ -121,18 +121,22 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
         for members, P in group_list:
             for di in members:
                 prefix[di] = P
-    # decode stream-K plan: concatenate streams (di, kvh) over pages [prefix, pages), cut
-    # into G equal shares
-    runs = []  # (di, kvh, page) for every page run, in order
+    # decode stream-K plan: concatenate streams (di, kvh) over pages [prefix, pages), each
+    # preceded by STREAM_COST start positions (None: a position that streams no page), cut
+    # into G equal shares of positions
+    STREAM_COST = 4
+    runs = []  # None or (di, kvh, page), for every cost position, in order
     seqs = []
-    P = 0
+    P = X = 0
     for di, r in enumerate(dec):
         pages = computed[r] // PAGE + 1
-        seqs.append([r, res["cu_seqlens"][r], computed[r] + 1, 8 * P])
+        seqs.append([r, res["cu_seqlens"][r], computed[r] + 1, 8 * X])
         for kvh in range(8):
+            runs.extend([None] * STREAM_COST)
             for pg in range(prefix[di], pages):
                 runs.append((di, kvh, pg))
         P += pages - prefix[di]
+        X += pages - prefix[di] + STREAM_COST
     W = len(runs)
     G = min(dec_grid_waves, _cdiv(W, max(1, dec_min_pages))) if W else 0
     # dec_share: a decode beside the prefill gets a multiple of 32 wavefronts in
@@ -156,10 +160,11 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
     waves = []
     for w in range(G):
         g0, g1 = w * W // G, (w + 1) * W // G
-        di, kvh, pg = runs[g0]
+        # a share that starts at a stream's start positions starts at its first page
+        di, kvh, pg = next(x for x in runs[g0:] if x is not None)
         r = dec[di]
-        waves.append([di, kvh, pg, g1 - g0, r, res["cu_seqlens"][r], computed[r] + 1,
-                      tables[r][pg]])
+        n = sum(x is not None for x in runs[g0:g1])
+        waves.append([di, kvh, pg, n, r, res["cu_seqlens"][r], computed[r] + 1, tables[r][pg]])
     # prefill items: tiles sorted by key count descending, stable
     tiles = []
     for r in pre:

@@ -414,11 +414,14 @@ def test_pack_prefix_known_answer():
     flag = 1 << 30
     seqs = got["dec_seqs"][:4]
     assert [int(z) for z in seqs[:, 2]] == [41, 48, 21, 71]  # no flags: groups read their own
-    assert [int(z) for z in seqs[:, 3]] == [0, 8, 16, 32]  # streams of 1, 1, 2, 3 pages
-    # 7 shares of 8 runs: {di, kvh, page (absolute), runs, r, row, n_keys, page id}
+    # streams of 1, 1, 2, 3 pages cost 5, 5, 6, 7 positions (4 for a stream's start)
+    assert [int(z) for z in seqs[:, 3]] == [0, 40, 80, 128]
+    # W = 184 positions in 7 shares starting at 0, 26, 52, 78, 105, 131, 157:
+    # {di, kvh, page (absolute), pages streamed, page id}.  Share 3 holds one page of
+    # (1, 7) and both of (2, 0..3); share 5 starts in (3, 0)'s start positions.
     assert [list(map(int, w[:4])) + [int(w[7])] for w in got["dec_waves"][:7]] == [
-        [0, 0, 2, 8, 7], [1, 0, 2, 8, 9], [2, 0, 0, 8, 8], [2, 4, 0, 8, 8],
-        [3, 0, 2, 8, 7], [3, 2, 4, 8, 3], [3, 5, 3, 8, 2]]
+        [0, 0, 2, 5, 7], [0, 5, 2, 5, 7], [1, 2, 2, 5, 9], [1, 7, 2, 9, 9],
+        [2, 4, 0, 8, 8], [3, 0, 2, 12, 7], [3, 4, 2, 12, 7]]
     off, _ = _compare_pack(comp, nnew, tabs, dict(kw, dec_prefix_pages=3))
     assert (int(off["meta"][9]), int(off["meta"][10]), int(off["meta"][11])) == (13, 0, 0)
     assert [bool(z & flag) for z in off["dec_seqs"][:4, 2]] == [True, True, False, True]
@@ -482,8 +485,9 @@ def test_dec_share_known_answer():
       below (50 P N 448 = 7.19e12 <= D (36*448 + 25 N)(N - 448) = 7.53e12), and the
       prefill at 480 (P N / 544 = 5.90e5) ends after the decode at 448
       (D * 41728 / 22400 = 5.83e5): 448 (1024 without dec_share).
-    * One decode sequence of 100 keys (7 pages, 56 runs, D = 5481) beside a 64-row prompt
-      on 32 cached keys (P = 4128): the meeting point is far above the 56 runs: 56.
+    * One decode sequence of 100 keys (7 pages, D = 5481; 8 streams of 7 pages + 4 start
+      positions, 88 in all) beside a 64-row prompt on 32 cached keys (P = 4128): the
+      meeting point is far above the plan's 88 wavefronts: 88.
     * The same decode beside a 2000-row prompt on 10000 cached keys (P = 22001000): even
       G = 32 leaves the prefill slower, so the floor of 32 wavefronts."""
     base = dict(max_rows=65, max_blocks=256, pool_pages=4096, dec_grid_waves=1024,
@@ -497,7 +501,7 @@ def test_dec_share_known_answer():
     assert got["meta"][4] == 1024
     tabs = [np.arange(7, dtype=np.int32), np.arange(7, 13, dtype=np.int32)]
     got = orc.pack([99, 32], [1, 64], [0, 7, 13], np.concatenate(tabs), **dict(base, dec_share=1))
-    assert got["meta"][4] == 56
+    assert got["meta"][4] == 88
     tabs2 = [np.arange(7, dtype=np.int32), np.arange(7, 7 + 751, dtype=np.int32)]
     big = dict(base, max_rows=2001, max_blocks=1024, pre_item_cap=40, dec_share=1)
     got = orc.pack([99, 10000], [1, 2000], [0, 7, 758], np.concatenate(tabs2), **big)
@@ -519,14 +523,16 @@ def test_pack_known_answer():
     assert got["block_tables"][:12].tolist() == [5, 9, -1, 2, 7, -1, 11, -1, -1, 4, -1, -1]
     assert got["decode_rids"][:4].tolist() == [0, 2, -1, -1]
     assert got["prefill_rids"][:4].tolist() == [1, 3, -1, -1]
-    assert got["meta"][:10].tolist() == [5, 2, 2, 3, 5, 1, 5, 0, 4, 3]
-    # W = 8*(2+1) = 24 page runs over 5 waves: shares 4,5,5,5,5
-    assert got["dec_seqs"][:2].tolist() == [[0, 0, 18, 0], [2, 4, 1, 16]]
-    assert got["dec_waves"][:5, :4].tolist() == [[0, 0, 0, 4], [0, 2, 0, 5], [0, 4, 1, 5],
-                                                 [0, 7, 0, 5], [1, 3, 0, 5]]
+    assert got["meta"][:10].tolist() == [5, 2, 2, 3, 5, 1, 18, 0, 4, 3]
+    # streams of 2 and 1 pages cost 6 and 5 positions (4 for a stream's start):
+    # W = 8*(6+5) = 88 positions over 5 waves, shares from 0, 17, 35, 52, 70 holding 5, 6,
+    # 5, 4, 4 of the 24 page runs (share 4 starts in (1, 4)'s start positions)
+    assert got["dec_seqs"][:2].tolist() == [[0, 0, 18, 0], [2, 4, 1, 48]]
+    assert got["dec_waves"][:5, :4].tolist() == [[0, 0, 0, 5], [0, 2, 1, 6], [0, 5, 1, 5],
+                                                 [1, 0, 0, 4], [1, 4, 0, 4]]
     # {r, row, n_keys, first page id}: page 1 of request 0 is page id 9
-    assert got["dec_waves"][:5, 4:].tolist() == [[0, 0, 18, 5], [0, 0, 18, 5], [0, 0, 18, 9],
-                                                 [0, 0, 18, 5], [2, 4, 1, 11]]
+    assert got["dec_waves"][:5, 4:].tolist() == [[0, 0, 18, 5], [0, 0, 18, 9], [0, 0, 18, 9],
+                                                 [2, 4, 1, 11], [2, 4, 1, 11]]
     assert got["pre_items"][:1].tolist() == [[1, 0, 3, 18]]
 
 
