@@ -45,6 +45,9 @@ namespace {
 constexpr int kDecWavesPerBlock = 4;
 // Page buffers per wave: page p is computed while page p+1 loads (180 VGPRs).
 constexpr int kDecBufs = 2;
+// Page buffers of a shared-prefix item's wavefront: its pages come from the caches (the
+// group's other quads read them too), so more are kept in flight.
+constexpr int kPrefixBufs = 4;
 // LDS reserved by each split-kernel workgroup and never touched: with it one decode
 // workgroup (one wave per SIMD) holds a CU alone.  Neither a second decode workgroup nor
 // a prefill workgroup (48 KiB) fits beside it; a prefill wave sharing a SIMD with a decode
@@ -233,25 +236,26 @@ __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* bt
 // The state a shared-prefix member's (kv head) stream starts from: the log-sum-exp merge
 // of its group's C chunk partials (decode_prefix_kernel) for its 4 query heads, in the
 // layout of DecState (lane: column n = head, rows d = b*16 + 4g + j; l on lane group 0).
-__device__ void prefix_state(const DecArgs& a, int di, int kvh, int lane, DecState& st) {
+__device__ void prefix_state(const DecArgs& a, const int4 info, int kvh, int lane,
+                             DecState& st) {
   const int n = lane & 15, g = lane >> 4;
   if (n >= kG) return;  // columns past the 4 heads carry nothing
-  const int4 info = *reinterpret_cast<const int4*>(a.prefix + 8LL * di);
   const int C = info.z & 0xFFFF, Q = info.z >> 16, k = info.w;
   // the pack's items fit dec_pre_cap; a workspace planned for fewer is never read past
   if ((long long)info.y + 8LL * C * Q > a.pre_cap) return;
   const int col = (k & 3) * kG + n;
   auto slot = [&](int c) { return ((long long)info.y + ((long long)kvh * C + c) * Q + (k >> 2)) * 16 + col; };
-  // online log-sum-exp merge, 4 chunks' loads in flight at a time
+  // online log-sum-exp merge, 8 chunks' loads in flight at a time (C <= 16)
   float m0 = -1e30f, l = 0.f;
   float4_t acc[8];
 #pragma unroll
   for (int b = 0; b < 8; ++b) acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
-  for (int c0 = 0; c0 < C; c0 += 4) {
-    float mc[4], lc[4];
-    float4_t xc[4][8];
+  constexpr int kB = 8;
+  for (int c0 = 0; c0 < C; c0 += kB) {
+    float mc[kB], lc[kB];
+    float4_t xc[kB][8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kB; ++j) {
       const long long sl = slot(min(c0 + j, C - 1));
       mc[j] = a.pws_m[sl];
       lc[j] = a.pws_l[sl];
@@ -260,7 +264,7 @@ __device__ void prefix_state(const DecArgs& a, int di, int kvh, int lane, DecSta
       for (int b = 0; b < 8; ++b) xc[j][b] = *reinterpret_cast<const float4_t*>(src + b * 16);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kB; ++j) {
       if (c0 + j >= C) break;
       const float mn = fmaxf(m0, mc[j]);
       const float co = __builtin_amdgcn_exp2f(m0 - mn), cn = __builtin_amdgcn_exp2f(mc[j] - mn);
@@ -311,8 +315,8 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_prefix_kerne
   st.l = 0.f;
   // every key of [page0, page1) precedes each member's own (the prefix ends at or before
   // computed / 16 pages), so no key is masked: L = 16 * page1
-  stream_pages<kDecBufs, false>(a, a.bt + (long long)r * a.max_blocks, kvh, p0, p1, p1 * kPage,
-                                qf, lane, st, -1);
+  stream_pages<kPrefixBufs, false>(a, a.bt + (long long)r * a.max_blocks, kvh, p0, p1,
+                                   p1 * kPage, qf, lane, st, -1);
   const float l_run = sum_rows4(st.l);
   const long long slot = (long long)w * 16 + n;
   if (g == 0) {
@@ -350,13 +354,21 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
   asm volatile("" ::"s"(desc.x), "s"(n_waves));  // both loads issued before the branch
   if (w >= n_waves) return;
   int di = desc.x, kvh = desc.y, page = desc.z, left = desc.w;
-  // shared-prefix plans: a stream covers pages [P, pages) of its sequence
-  int P = a.prefix ? __builtin_amdgcn_readfirstlane(a.prefix[8LL * di]) : 0;
+  // shared-prefix plans: a stream covers pages [P, pages) of its sequence; the row also
+  // locates the group's prefix partials
+  auto prefix_row = [&](int d) {
+    const int4 v = *reinterpret_cast<const int4*>(a.prefix + 8LL * d);
+    return make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+                     __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
+  };
+  int4 pinfo = a.prefix ? prefix_row(di) : make_int4(0, 0, 0, 0);
+  int P = pinfo.x;
   for (int seg = 0; left > 0; ++seg) {
     if (seg > 0) {
       sq = uni4(*reinterpret_cast<const int4*>(a.seqs + 4 * (long long)di));
       sq.w = -1;  // first page id of a later stream: read from the block table
-      if (a.prefix) P = __builtin_amdgcn_readfirstlane(a.prefix[8LL * di]);
+      if (a.prefix) pinfo = prefix_row(di);
+      P = pinfo.x;
       page = P;
     }
     // sequences that share their first page read through the caches (FQA_DEC_SHARED)
@@ -382,7 +394,7 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
     for (int b = 0; b < 8; ++b) st.acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
     st.m = -1e30f;
     st.l = 0.f;
-    if (P > 0 && page == P) prefix_state(a, di, kvh, lane, st);  // the stream's first pages
+    if (P > 0 && page == P) prefix_state(a, pinfo, kvh, lane, st);  // the stream's start
     if (shared)
       stream_pages<kBufs, false>(a, a.bt + (long long)r * a.max_blocks, kvh, page, page + cnt, L,
                                  qf, lane, st, sq.w);
@@ -519,11 +531,12 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_combine_kern
   if (di >= n_dec) return;
   const long long G = a.meta[FQA_META_DEC_WAVES];
   // the plan's cost positions (fqa.h): each stream's start positions, then its pages
-  const long long W = 8LL * (a.meta[FQA_META_DEC_PAGES] + (long long)FQA_DEC_STREAM_COST * n_dec);
+  const long long W = a.meta[FQA_META_DEC_COST];
   // a stream's pages: [P, pages) with a shared prefix
   const int pages = ((sq.z & FQA_DEC_KEYS_MASK) + kPage - 1) / kPage - pfx;
-  const long long S0 = sq.w + (long long)kvh * (pages + FQA_DEC_STREAM_COST);
-  const long long F = S0 + FQA_DEC_STREAM_COST, S1 = F + pages;  // page positions [F, S1)
+  const int sc = FQA_DEC_STREAM_COST + (pfx > 0 ? FQA_DEC_PREFIX_STREAM_COST : 0);
+  const long long S0 = sq.w + (long long)kvh * (pages + sc);
+  const long long F = S0 + sc, S1 = F + pages;  // page positions [F, S1)
   const long long wf = ((F + 1) * G - 1) / W, wl = (S1 * G - 1) / W;
   if (wf == wl) return;  // finished by one wavefront
   const int lane = threadIdx.x & 63;

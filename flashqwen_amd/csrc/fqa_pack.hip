@@ -70,8 +70,9 @@ struct Stats {
   int v[6];  // code (min), rows (sum), dpages (sum), dmax (max), qmax (max), overflow (max)
 };
 
+constexpr int kCounts = 6;
 struct Counts {
-  int v[5];
+  int v[kCounts];
 };
 
 // Exclusive scans of 5 values over the workgroup (*total gets the 5 sums) and, when
@@ -83,7 +84,7 @@ __device__ Counts block_scan5_stats(const Counts& in, Counts* total, Stats* st, 
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
   Counts incl;
 #pragma unroll
-  for (int k = 0; k < 5; ++k) incl.v[k] = wave_incl_scan(in.v[k]);
+  for (int k = 0; k < kCounts; ++k) incl.v[k] = wave_incl_scan(in.v[k]);
   Stats r;
   if (stats) {
     r.v[0] = wave_extreme<false>(st->v[0], INT_MAX);
@@ -100,7 +101,7 @@ __device__ Counts block_scan5_stats(const Counts& in, Counts* total, Stats* st, 
   const Counts o = shc[have ? lane : 0];
   Counts out;
 #pragma unroll
-  for (int k = 0; k < 5; ++k) {
+  for (int k = 0; k < kCounts; ++k) {
     const int sc = wave_incl_scan(have ? o.v[k] : 0);  // lane i: total of waves 0..i
     total->v[k] = __builtin_amdgcn_readlane(sc, kPackWaves - 1);
     const int below = __builtin_amdgcn_readlane(sc, w == 0 ? 0 : w - 1);
@@ -162,6 +163,13 @@ __device__ int dec_share_waves(int N, long long dpages, unsigned long long keyro
   if (lo + kStep <= top && 50 * P * n * g < D * (36 * g + 25 * n) * (n - g - kStep))
     lo += kStep;
   return lo;
+}
+
+// A decode stream's start in the plan's cost units (fqa.h): FQA_DEC_STREAM_COST, plus
+// FQA_DEC_PREFIX_STREAM_COST for a shared-prefix member (it merges its group's partials
+// first).
+__host__ __device__ constexpr int stream_start_cost(int prefix_pages) {
+  return FQA_DEC_STREAM_COST + (prefix_pages > 0 ? FQA_DEC_PREFIX_STREAM_COST : 0);
 }
 
 struct PackArgs {
@@ -360,6 +368,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   __shared__ int s_dstart[FQA_MAX_REQS + 1];  // by decode index: 8 * cost prefix
   __shared__ int s_dpages[FQA_MAX_REQS];      // by decode index: stream pages
   __shared__ int s_dpfx[FQA_MAX_REQS];        // by decode index: shared-prefix pages
+  __shared__ int s_dpst[FQA_MAX_REQS + 1];    // by decode index: 8 * stream page prefix
   __shared__ int s_drid[FQA_MAX_REQS];        // by decode index: request
   __shared__ int s_dflag[FQA_MAX_REQS];       // by decode index: first page id, then the flag
   __shared__ int s_prer[FQA_MAX_REQS];        // by prefill index: request
@@ -388,11 +397,11 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   // (rows, decode / prefill indices, decode pages, prefill items), one pass per 1024
   // requests; the totals are reduced with the last pass's scans -------------------------
   Stats st = {{INT_MAX, 0, 0, 0, 1, 0}};
-  Counts carry = {{0, 0, 0, 0, 0}};
+  Counts carry = {{0, 0, 0, 0, 0, 0}};
   const int bt_end = a.b.bt_off[R];  // issued with the first loads, not after the scans
   for (int base = 0; base < R; base += kPackThreads) {
     const int r = base + tid;
-    Counts v = {{0, 0, 0, 0, 0}};
+    Counts v = {{0, 0, 0, 0, 0, 0}};
     // Loads at a clamped index, not under the lane condition: a conditional load is
     // waited for where its value merges with the default.
     const int rc = r < R ? r : R - 1;
@@ -424,8 +433,10 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       v.v[0] = n;
       v.v[1] = n == 1;
       v.v[2] = n != 1;
-      // a decode stream's cost in the plan: its pages plus the per-stream overhead
-      v.v[3] = n == 1 ? c / kPage + 1 - pfx + FQA_DEC_STREAM_COST : 0;
+      // a decode stream's cost in the plan: its pages plus the per-stream overhead (more
+      // for a shared-prefix member, which starts from its group's partials), and its pages
+      v.v[3] = n == 1 ? c / kPage + 1 - pfx + stream_start_cost(pfx) : 0;
+      v.v[5] = n == 1 ? c / kPage + 1 - pfx : 0;
       v.v[4] = n != 1 ? (n + QT - 1) / QT : 0;
     }
     const bool last = base + kPackThreads >= R;
@@ -443,6 +454,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       s_preidx[r] = pi;
       if (n == 1) {
         s_dstart[di] = 8 * (carry.v[3] + e.v[3]);
+        s_dpst[di] = 8 * (carry.v[5] + e.v[5]);
         s_dpages[di] = c / kPage + 1 - pfx;
         s_dpfx[di] = pfx;
         s_drid[di] = r;
@@ -456,19 +468,20 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       }
     }
 #pragma unroll
-    for (int k = 0; k < 5; ++k) carry.v[k] += tot.v[k];
+    for (int k = 0; k < kCounts; ++k) carry.v[k] += tot.v[k];
   }
   const int nd = carry.v[1], np = carry.v[2], npi = carry.v[4];
   // decode plan: W = 8 x (stream pages + FQA_DEC_STREAM_COST per stream) cost units cut
   // into G equal shares
   const int dpages = st.v[2];
-  const long long W = 8LL * ((long long)dpages + (long long)FQA_DEC_STREAM_COST * nd);
+  const long long W = 8LL * carry.v[3];
   if (tid == 0) {
     s_btoff[R] = bt_end;
     s_qstart[R] = carry.v[0];
     s_decidx[R] = nd;
     s_preidx[R] = np;
     s_dstart[nd] = (int)W;
+    s_dpst[nd] = 8 * dpages;
     s_pit[np] = npi;
   }
   lds_sync();
@@ -506,24 +519,24 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   };
   // Cost position x lies in stream (d, h) at offset off: the stream's first
   // FQA_DEC_STREAM_COST positions are its overhead, then one per page.  Pages before x:
-  auto locate = [&](int x, int& d, int& h, int& off) {
+  auto locate = [&](int x, int& d, int& h, int& skip) {
     d = upper_index(s_dstart, nd, x);
     if (d >= nd) {  // x == W
-      h = off = 0;
+      h = skip = 0;
       return dpages * 8;
     }
-    const int rem = x - s_dstart[d], cost = s_dpages[d] + FQA_DEC_STREAM_COST;
+    const int sc = stream_start_cost(s_dpfx[d]);
+    const int rem = x - s_dstart[d], cost = s_dpages[d] + sc;
     h = rem / cost;
-    off = rem % cost;
-    return s_dstart[d] - 8 * FQA_DEC_STREAM_COST * d + h * s_dpages[d] +
-           max(0, off - FQA_DEC_STREAM_COST);
+    skip = max(0, rem % cost - sc);  // pages of stream (d, h) before x
+    return s_dpst[d] + h * s_dpages[d] + skip;
   };
   auto wave_of = [&](int w, int& di, int& kvh, int& page, int& n, int& r) {
     const int g0 = (int)((long long)w * W / G), g1 = (int)((long long)(w + 1) * W / G);
-    int off, d1, h1, o1;
-    const int p0 = locate(g0, di, kvh, off);
-    n = locate(g1, d1, h1, o1) - p0;
-    page = s_dpfx[di] + max(0, off - FQA_DEC_STREAM_COST);
+    int skip, d1, h1, s1;
+    const int p0 = locate(g0, di, kvh, skip);
+    n = locate(g1, d1, h1, s1) - p0;
+    page = s_dpfx[di] + skip;
     r = s_drid[di];
   };
   auto bt_of = [&](int e, int& r, int& g) {
@@ -737,6 +750,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       case FQA_META_DEC_PAGES: v = (int)dpages; break;
       case FQA_META_DEC_PRE_ITEMS: v = pre_counts & 0xFFFFF; break;
       case FQA_META_DEC_GROUPS: v = pre_counts >> 20; break;
+      case FQA_META_DEC_COST: v = (int)W; break;
       default: v = 0;
     }
     a.o.meta[tid] = v;

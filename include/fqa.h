@@ -76,6 +76,9 @@ extern "C" {
  * kv head) stream counts its pages plus this, so a wavefront whose share holds many short
  * streams gets fewer pages (a stream start costs a few dependent loads). */
 #define FQA_DEC_STREAM_COST 4
+/* ... and this more for a shared-prefix member's stream (dec_prefix_pages), which first
+ * merges its group's prefix partials. */
+#define FQA_DEC_PREFIX_STREAM_COST 4
 /* Pages of a decode sequence compared with its group leader's for a shared prefix
  * (fqa_pack_cfg::dec_prefix_pages). */
 #define FQA_DEC_PREFIX_CAP 8192
@@ -94,6 +97,7 @@ enum {
   FQA_META_DEC_PAGES = 9,    /* sum over decode sequences of their stream pages */
   FQA_META_DEC_PRE_ITEMS = 10, /* shared-prefix items (dec_prefix_pages)        */
   FQA_META_DEC_GROUPS = 11,  /* shared-prefix groups                            */
+  FQA_META_DEC_COST = 12,    /* W: the decode plan's cost positions              */
   FQA_META_LEN = 16
 };
 
@@ -138,10 +142,11 @@ typedef struct fqa_batch {
  *
  * Decode plan (stream-K): the decode requests' (sequence, kv head) page streams are laid
  * end to end in cost units, stream (di, kvh) of pages[di] pages costing
- * c = pages[di] + FQA_DEC_STREAM_COST: it spans [X[di]*8 + kvh*c, + c), where pages =
- * ceil(n_keys/16) and X is the exclusive prefix of the costs over decode indices; the
- * first FQA_DEC_STREAM_COST positions of a stream stand for its start, the others for its
- * pages in order.  The W = 8*sum(c) positions are cut into G = min(dec_grid_waves,
+ * c = pages[di] + s, s = FQA_DEC_STREAM_COST (+ FQA_DEC_PREFIX_STREAM_COST for a
+ * shared-prefix member): it spans [X[di]*8 + kvh*c, + c), where pages = ceil(n_keys/16)
+ * and X is the exclusive prefix of the costs over decode indices; the first s positions
+ * of a stream stand for its start, the others for its pages in order.  The W = 8*sum(c)
+ * positions (meta[FQA_META_DEC_COST]) are cut into G = min(dec_grid_waves,
  * ceil(W/dec_min_pages)) equal contiguous shares, share w = [floor(w*W/G),
  * floor((w+1)*W/G)), one per decode wavefront, which streams the pages whose positions
  * fall in it; dec_waves[w] = {di, kvh, page, n_runs, r, row, n_keys, page id} is the

@@ -32,6 +32,11 @@
 #define FQA_DEC_PREFIX_CAP 8192
 /* per-stream start cost of the decode plan, in page runs (FQA_DEC_STREAM_COST, fqa.h) */
 #define FQA_DEC_STREAM_COST 4
+#define FQA_DEC_PREFIX_STREAM_COST 4
+/* a decode stream's start cost: more for a shared-prefix member */
+static int64_t stream_start_cost(int pfx) {
+  return FQA_DEC_STREAM_COST + (pfx > 0 ? FQA_DEC_PREFIX_STREAM_COST : 0);
+}
 
 float fqo_bf16_to_f32(uint16_t b) {
   uint32_t bits = (uint32_t)b << 16;
@@ -240,9 +245,13 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
    * end in cost positions (FQA_DEC_STREAM_COST start positions, then one per page),
    * W = 8 * (total stream pages + FQA_DEC_STREAM_COST per sequence) cut into G equal
    * shares [w*W/G, (w+1)*W/G) */
-  int64_t total = 0;
-  for (int di = 0; di < nd; ++di) total += computed[decode_rids[di]] / PAGE + 1 - pfx[di];
-  int64_t W = 8 * (total + (int64_t)FQA_DEC_STREAM_COST * nd);
+  int64_t total = 0, cost_total = 0;
+  for (int di = 0; di < nd; ++di) {
+    const int len = computed[decode_rids[di]] / PAGE + 1 - pfx[di];
+    total += len;
+    cost_total += len + stream_start_cost(pfx[di]);
+  }
+  int64_t W = 8 * cost_total;
   int minp = dec_min_pages > 0 ? dec_min_pages : 1;
   int G = 0;
   if (W > 0) {
@@ -296,7 +305,7 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
       dec_seqs[4 * di + 1] = cu_seqlens[r];
       dec_seqs[4 * di + 2] = computed[r] + 1;
       dec_seqs[4 * di + 3] = (int32_t)(8 * X);
-      X += pages + FQA_DEC_STREAM_COST;
+      X += pages + stream_start_cost(pfx[di]);
     }
     /* Position x: the sequence, kv head and offset in the stream's cost span, and the
      * pages at positions below x (every stream's pages come after its start positions). */
@@ -313,7 +322,7 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
         int64_t start = 0;
         int d = 0;
         while (d < nd) {
-          const int64_t cost = computed[decode_rids[d]] / PAGE + 1 - pfx[d] + FQA_DEC_STREAM_COST;
+          const int64_t cost = computed[decode_rids[d]] / PAGE + 1 - pfx[d] + stream_start_cost(pfx[d]);
           if (x < start + 8 * cost) break;
           start += 8 * cost;
           ++d;
@@ -323,8 +332,8 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
           continue;
         }
         const int64_t len = computed[decode_rids[d]] / PAGE + 1 - pfx[d];
-        const int64_t cost = len + FQA_DEC_STREAM_COST, rem = x - start;
-        const int64_t o = rem % cost, skip = o > FQA_DEC_STREAM_COST ? o - FQA_DEC_STREAM_COST : 0;
+        const int64_t sc = stream_start_cost(pfx[d]), cost = len + sc, rem = x - start;
+        const int64_t o = rem % cost, skip = o > sc ? o - sc : 0;
         below[e] = pstart[d] + (rem / cost) * len + skip;
         di = d;
         kvh = (int)(rem / cost);
@@ -427,6 +436,7 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
   meta[9] = (int32_t)total;
   meta[10] = n_pitems;
   meta[11] = n_groups;
+  meta[12] = (int32_t)W;
   return meta[7];
 }
 

@@ -124,19 +124,20 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
     # decode stream-K plan: concatenate streams (di, kvh) over pages [prefix, pages), each
     # preceded by STREAM_COST start positions (None: a position that streams no page), cut
     # into G equal shares of positions
-    STREAM_COST = 4
+    STREAM_COST, PREFIX_STREAM_COST = 4, 4  # a member's stream also merges its group's partials
     runs = []  # None or (di, kvh, page), for every cost position, in order
     seqs = []
     P = X = 0
     for di, r in enumerate(dec):
         pages = computed[r] // PAGE + 1
         seqs.append([r, res["cu_seqlens"][r], computed[r] + 1, 8 * X])
+        start = STREAM_COST + (PREFIX_STREAM_COST if prefix[di] else 0)
         for kvh in range(8):
-            runs.extend([None] * STREAM_COST)
+            runs.extend([None] * start)
             for pg in range(prefix[di], pages):
                 runs.append((di, kvh, pg))
         P += pages - prefix[di]
-        X += pages - prefix[di] + STREAM_COST
+        X += pages - prefix[di] + start
     W = len(runs)
     G = min(dec_grid_waves, _cdiv(W, max(1, dec_min_pages))) if W else 0
     # dec_share: a decode beside the prefill gets a multiple of 32 wavefronts in
@@ -206,7 +207,7 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
                                   + padded[4 * q:4 * q + 4])
     res["dec_prefix"] = dpfx
     res["dec_pre_items"] = pitems
-    meta[10], meta[11] = len(pitems), len(group_list)
+    meta[10], meta[11], meta[12] = len(pitems), len(group_list), W
     meta[0] = rows_total
     meta[1], meta[2] = len(dec), len(pre)
     meta[3] = max([1] + [n_new[r] for r in pre])

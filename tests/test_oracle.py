@@ -414,14 +414,16 @@ def test_pack_prefix_known_answer():
     flag = 1 << 30
     seqs = got["dec_seqs"][:4]
     assert [int(z) for z in seqs[:, 2]] == [41, 48, 21, 71]  # no flags: groups read their own
-    # streams of 1, 1, 2, 3 pages cost 5, 5, 6, 7 positions (4 for a stream's start)
-    assert [int(z) for z in seqs[:, 3]] == [0, 40, 80, 128]
-    # W = 184 positions in 7 shares starting at 0, 26, 52, 78, 105, 131, 157:
-    # {di, kvh, page (absolute), pages streamed, page id}.  Share 3 holds one page of
-    # (1, 7) and both of (2, 0..3); share 5 starts in (3, 0)'s start positions.
+    # streams of 1, 1, 2, 3 pages cost 9, 9, 6, 11 positions (4 for a stream's start, 4
+    # more for a member's, which merges its group's partials first)
+    assert [int(z) for z in seqs[:, 3]] == [0, 72, 144, 192]
+    # W = 280 positions in 7 shares starting at 0, 40, 80, 120, 160, 200, 240:
+    # {di, kvh, page (absolute), pages streamed, page id}.  Share 1 starts in (0, 4)'s
+    # start positions; share 3 holds pages of (1, 5..7) and (2, 0..1).
     assert [list(map(int, w[:4])) + [int(w[7])] for w in got["dec_waves"][:7]] == [
-        [0, 0, 2, 5, 7], [0, 5, 2, 5, 7], [1, 2, 2, 5, 9], [1, 7, 2, 9, 9],
-        [2, 4, 0, 8, 8], [3, 0, 2, 12, 7], [3, 4, 2, 12, 7]]
+        [0, 0, 2, 4, 7], [0, 4, 2, 4, 7], [1, 0, 2, 5, 9], [1, 5, 2, 7, 9],
+        [2, 2, 0, 12, 8], [3, 0, 2, 12, 7], [3, 4, 2, 12, 7]]
+    assert int(m[12]) == 280
     off, _ = _compare_pack(comp, nnew, tabs, dict(kw, dec_prefix_pages=3))
     assert (int(off["meta"][9]), int(off["meta"][10]), int(off["meta"][11])) == (13, 0, 0)
     assert [bool(z & flag) for z in off["dec_seqs"][:4, 2]] == [True, True, False, True]
