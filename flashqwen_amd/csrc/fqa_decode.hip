@@ -46,8 +46,11 @@ constexpr int kDecWavesPerBlock = 4;
 // Page buffers per wave: page p is computed while page p+1 loads (180 VGPRs).
 constexpr int kDecBufs = 2;
 // Page buffers of a shared-prefix item's wavefront: its pages come from the caches (the
-// group's other quads read them too), so more are kept in flight.
+// group's other octets read them too), so more are kept in flight.
 constexpr int kPrefixBufs = 4;
+// A shared-prefix item holds up to 8 members: 2 sets of 16 MFMA columns (4 heads each).
+constexpr int kPrefixSets = 2;
+constexpr int kPrefixCols = 16 * kPrefixSets;
 // LDS reserved by each split-kernel workgroup and never touched: with it one decode
 // workgroup (one wave per SIMD) holds a CU alone.  Neither a second decode workgroup nor
 // a prefill workgroup (48 KiB) fits beside it; a prefill wave sharing a SIMD with a decode
@@ -73,10 +76,10 @@ struct DecArgs {
   int wave_cap;      // rows of `waves`
   // shared-prefix plans (fqa_decode_prefix; NULL otherwise)
   const int32_t* prefix;  // [n_decode][8] {P, first item, C | Q << 16, k}
-  const int32_t* pitems;  // [pre_cap][8] {leader, kvh, page0, page1, member x 4}
-  float* pws_m;           // prefix partials: [pre_cap][16 columns]
+  const int32_t* pitems;  // [pre_cap][12] {leader, kvh, page0, page1, member x 8}
+  float* pws_m;           // prefix partials: [pre_cap][32 columns]
   float* pws_l;
-  float* pws_acc;         // [pre_cap][16][128]
+  float* pws_acc;         // [pre_cap][32][128]
   int pre_cap;
 };
 
@@ -123,7 +126,8 @@ struct DecState {
 };
 
 // One page (16 keys) of online softmax for the 4 heads: S^T = K Q^T, P^T = exp2(S^T - m),
-// O^T = O^T * corr + V^T P^T.
+// O^T = O^T * corr + V^T P^T.  kFull: every key of the page is below L (no masking).
+template <bool kFull>
 __device__ __forceinline__ void process_page(PageFrag& f, const bf16x8 (&qf)[4], int p, int L,
                                              int g, float scale_log2, DecState& st) {
   float4_t s = {0.f, 0.f, 0.f, 0.f};
@@ -135,10 +139,10 @@ __device__ __forceinline__ void process_page(PageFrag& f, const bf16x8 (&qf)[4],
   float mx = -INFINITY;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    sv[j] = key0 + j < L ? s[j] * scale_log2 : -INFINITY;
+    sv[j] = kFull || key0 + j < L ? s[j] * scale_log2 : -INFINITY;
     mx = fmaxf(mx, sv[j]);
   }
-  if ((p + 1) * kPage > L) {  // last page: unwritten slots must not reach PV
+  if (!kFull && (p + 1) * kPage > L) {  // last page: unwritten slots must not reach PV
 #pragma unroll
     for (int b = 0; b < 8; ++b)
 #pragma unroll
@@ -176,10 +180,12 @@ __device__ __forceinline__ void process_page(PageFrag& f, const bf16x8 (&qf)[4],
 }
 
 // Stream pages [pb, pe) of (sequence `seq`, kv head kvh) into `st`.
-template <int kBufs, bool kNT>
-__device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* btr, int kvh,
-                                             int pb, int pe, int L, const bf16x8 (&qf)[4],
-                                             int lane, DecState& st, int first_page) {
+// kS query sets (16 columns each) over the same pages: one page load feeds kS
+// process_page calls (shared-prefix items hold 8 members, 2 sets).  kFull: L = 16 * pe.
+template <int kBufs, bool kNT, int kS, bool kFull = false>
+__device__ __forceinline__ void stream_pages_n(const DecArgs& a, const int32_t* btr, int kvh,
+                                               int pb, int pe, int L, const bf16x8 (&qf)[kS][4],
+                                               int lane, DecState (&st)[kS], int first_page) {
   const int g = lane >> 4;
   // Page ids through the constant address space: scalar loads (lgkmcnt), so waiting for an
   // id does not also wait for the page loads issued before it.
@@ -217,20 +223,37 @@ __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* bt
     for (int i = 0; i < kBufs; ++i) {
       if (i > 0 && p + i >= pe) break;
       load(f[(i + kBufs - 1) % kBufs], ok[(i + kBufs - 1) % kBufs], p + i + kBufs - 1);
-      if (ok[i]) process_page(f[i], qf, p + i, L, g, a.scale_log2, st);
-      else n_zero += min(kPage, L - (p + i) * kPage);
+      if (ok[i]) {
+#pragma unroll
+        for (int q = 0; q < kS; ++q) process_page<kFull>(f[i], qf[q], p + i, L, g, a.scale_log2, st[q]);
+      } else {
+        n_zero += min(kPage, L - (p + i) * kPage);
+      }
     }
   }
   if (n_zero > 0) {  // n_zero keys with score 0 and value 0 (uniform, rare)
-    const float m_new = fmaxf(st.m, 0.f);
-    const float corr = __builtin_amdgcn_exp2f(st.m - m_new);
-    // st.l holds this lane's share of the row sum (summed over the 4 lanes of a column
-    // at the end): lane group g = 0 takes the zero keys
-    st.l = st.l * corr + ((lane >> 4) == 0 ? (float)n_zero * __builtin_amdgcn_exp2f(-m_new) : 0.f);
-    st.m = m_new;
 #pragma unroll
-    for (int b = 0; b < 8; ++b) st.acc[b] *= corr;
+    for (int q = 0; q < kS; ++q) {
+      const float m_new = fmaxf(st[q].m, 0.f);
+      const float corr = __builtin_amdgcn_exp2f(st[q].m - m_new);
+      // st.l holds this lane's share of the row sum (summed over the 4 lanes of a column
+      // at the end): lane group g = 0 takes the zero keys
+      st[q].l = st[q].l * corr +
+                ((lane >> 4) == 0 ? (float)n_zero * __builtin_amdgcn_exp2f(-m_new) : 0.f);
+      st[q].m = m_new;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) st[q].acc[b] *= corr;
+    }
   }
+}
+
+template <int kBufs, bool kNT>
+__device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* btr, int kvh,
+                                             int pb, int pe, int L, const bf16x8 (&qf)[4],
+                                             int lane, DecState& st, int first_page) {
+  stream_pages_n<kBufs, kNT, 1>(a, btr, kvh, pb, pe, L,
+                                reinterpret_cast<const bf16x8(&)[1][4]>(qf), lane,
+                                reinterpret_cast<DecState(&)[1]>(st), first_page);
 }
 
 // The state a shared-prefix member's (kv head) stream starts from: the log-sum-exp merge
@@ -243,8 +266,10 @@ __device__ void prefix_state(const DecArgs& a, const int4 info, int kvh, int lan
   const int C = info.z & 0xFFFF, Q = info.z >> 16, k = info.w;
   // the pack's items fit dec_pre_cap; a workspace planned for fewer is never read past
   if ((long long)info.y + 8LL * C * Q > a.pre_cap) return;
-  const int col = (k & 3) * kG + n;
-  auto slot = [&](int c) { return ((long long)info.y + ((long long)kvh * C + c) * Q + (k >> 2)) * 16 + col; };
+  const int col = (k & 7) * kG + n;  // member k & 7 of its item, head n
+  auto slot = [&](int c) {
+    return ((long long)info.y + ((long long)kvh * C + c) * Q + (k >> 3)) * kPrefixCols + col;
+  };
   // online log-sum-exp merge, 8 chunks' loads in flight at a time (C <= 16)
   float m0 = -1e30f, l = 0.f;
   float4_t acc[8];
@@ -282,50 +307,64 @@ __device__ void prefix_state(const DecArgs& a, const int4 info, int kvh, int lan
 
 // Shared-prefix items: one wavefront per item streams pages [page0, page1) of the group
 // leader's table (which its members' tables equal there) once for the 4 query heads of
-// each of up to 4 members (the 16 MFMA columns: member j, head h at column 4j + h), with
-// the decode's page loop and arithmetic, and leaves the 16 columns' fp32 partials.
+// each of up to 8 members (2 sets of 16 MFMA columns: member j, head h at column 4j + h),
+// with the decode's page loop and arithmetic, and leaves the 32 columns' fp32 partials.
 __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_prefix_kernel(DecArgs a) {
   const int w = blockIdx.x * kDecWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   const int n_items = a.meta[FQA_META_DEC_PRE_ITEMS];
   if (w >= n_items || w >= a.pre_cap) return;
-  const int4* it = reinterpret_cast<const int4*>(a.pitems + 8LL * w);
-  const int4 i0 = it[0], i1 = it[1];
+  const int4* it = reinterpret_cast<const int4*>(a.pitems + 12LL * w);
+  const int4 i0 = it[0], i1 = it[1], i2 = it[2];
   const int lead = __builtin_amdgcn_readfirstlane(i0.x), kvh = __builtin_amdgcn_readfirstlane(i0.y);
   const int p0 = __builtin_amdgcn_readfirstlane(i0.z), p1 = __builtin_amdgcn_readfirstlane(i0.w);
   const int r = __builtin_amdgcn_readfirstlane(a.seqs[4LL * lead]);
-  const int mj = (n >> 2) == 0 ? i1.x : (n >> 2) == 1 ? i1.y : (n >> 2) == 2 ? i1.z : i1.w;
-  bf16x8 qf[4];
-  if (mj >= 0) {
-    const int row = a.seqs[4LL * mj + 1];
-    const uint16_t* q = a.qkv + (long long)row * a.stride + (kvh * kG + (n & 3)) * kD + g * 8;
+  const int mem[8] = {i1.x, i1.y, i1.z, i1.w, i2.x, i2.y, i2.z, i2.w};
+  bf16x8 qf[kPrefixSets][4];
+  DecState st[kPrefixSets];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(q + ks * 32);
-  } else {
+  for (int q = 0; q < kPrefixSets; ++q) {
+    const int mj = mem[4 * q + (n >> 2)];
+    if (mj >= 0) {
+      const int row = a.seqs[4LL * mj + 1];
+      const uint16_t* src = a.qkv + (long long)row * a.stride + (kvh * kG + (n & 3)) * kD + g * 8;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+      for (int ks = 0; ks < 4; ++ks) qf[q][ks] = *reinterpret_cast<const bf16x8*>(src + ks * 32);
+    } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) qf[ks][i] = (__bf16)0.0f;
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qf[q][ks][i] = (__bf16)0.0f;
+    }
+#pragma unroll
+    for (int b = 0; b < 8; ++b) st[q].acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
+    st[q].m = -1e30f;
+    st[q].l = 0.f;
   }
-  DecState st;
-#pragma unroll
-  for (int b = 0; b < 8; ++b) st.acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
-  st.m = -1e30f;
-  st.l = 0.f;
   // every key of [page0, page1) precedes each member's own (the prefix ends at or before
-  // computed / 16 pages), so no key is masked: L = 16 * page1
-  stream_pages<kPrefixBufs, false>(a, a.bt + (long long)r * a.max_blocks, kvh, p0, p1,
-                                   p1 * kPage, qf, lane, st, -1);
-  const float l_run = sum_rows4(st.l);
-  const long long slot = (long long)w * 16 + n;
-  if (g == 0) {
-    a.pws_m[slot] = st.m;
-    a.pws_l[slot] = l_run;
-  }
-  float* wa = a.pws_acc + slot * kD + g * 4;
+  // computed / 16 pages), so no key is masked: L = 16 * page1.  An item whose second set
+  // is empty (4 members or fewer) streams the first set alone.
+  const int32_t* btr = a.bt + (long long)r * a.max_blocks;
+  if (__builtin_amdgcn_readfirstlane(i2.x) >= 0)
+    stream_pages_n<kPrefixBufs, false, kPrefixSets, true>(a, btr, kvh, p0, p1, p1 * kPage, qf, lane,
+                                                    st, -1);
+  else
+    stream_pages_n<kPrefixBufs, false, 1, true>(a, btr, kvh, p0, p1, p1 * kPage,
+                                          reinterpret_cast<const bf16x8(&)[1][4]>(qf[0]), lane,
+                                          reinterpret_cast<DecState(&)[1]>(st[0]), -1);
 #pragma unroll
-  for (int b = 0; b < 8; ++b) *reinterpret_cast<float4_t*>(wa + b * 16) = st.acc[b];
+  for (int q = 0; q < kPrefixSets; ++q) {
+    const float l_run = sum_rows4(st[q].l);
+    const long long slot = (long long)w * kPrefixCols + 16 * q + n;
+    if (g == 0) {
+      a.pws_m[slot] = st[q].m;
+      a.pws_l[slot] = l_run;
+    }
+    float* wa = a.pws_acc + slot * kD + g * 4;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) *reinterpret_cast<float4_t*>(wa + b * 16) = st[q].acc[b];
+  }
 }
 
 // One wavefront per share of the stream-K plan.  A share walks consecutive streams:
@@ -601,9 +640,9 @@ int decode_launch(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* poo
   DecArgs a{qkv, pool, pool_pages, block_tables, max_blocks, dec_waves, dec_seqs, meta, ws,
             ws + slots, ws + 2 * slots, out, dims->qkv_stride, dims->scale * kLog2e, dec_wave_cap};
   if (dec_prefix) {
-    // prefix partials after the stream partials: m, l [pre_cap][16], acc [pre_cap][16][128]
+    // prefix partials after the stream partials: m, l [pre_cap][32], acc [pre_cap][32][128]
     float* pws = ws + slots * (2 + kD);
-    const long long ps = 16LL * dec_pre_cap;
+    const long long ps = (long long)kPrefixCols * dec_pre_cap;
     a.prefix = dec_prefix;
     a.pitems = dec_pre_items;
     a.pws_m = pws;
@@ -722,7 +761,7 @@ int64_t fqa_decode_prefix_workspace_bytes(const fqa_dims* dims, int32_t dec_wave
                                           int32_t dec_pre_cap) {
   if (dec_wave_cap < 0 || dec_pre_cap < 0) return 0;
   return fqa_decode_workspace_bytes(dims, dec_wave_cap) +
-         16LL * dec_pre_cap * (2 + kD) * (int64_t)sizeof(float);
+         (int64_t)kPrefixCols * dec_pre_cap * (2 + kD) * (int64_t)sizeof(float);
 }
 
 int fqa_decode_prefix(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,

@@ -293,7 +293,7 @@ __global__ void __launch_bounds__(kPackThreads) prefix_plan_kernel(PackArgs a) {
     if (r < R && s_q[r] >= 0 && s_lead[r] == r && s_gmin[r] >= minp) {
       const int P = s_gmin[r], M = s_gcnt[r];
       const int CP = P / 16 > 16 ? (P + 15) / 16 : 16;
-      items = 8 * ((P + CP - 1) / CP) * ((M + 3) / 4);
+      items = 8 * ((P + CP - 1) / CP) * ((M + 7) / 8);
       mem = M;
       grp = 1;
     }
@@ -323,7 +323,7 @@ __global__ void __launch_bounds__(kPackThreads) prefix_plan_kernel(PackArgs a) {
       for (int j = L; j < r; ++j) k += s_q[j] >= 0 && s_lead[j] == L;
       s_mem[s_goff[L] + k] = s_di[r];
       const int M = s_gcnt[L], CP = P / 16 > 16 ? (P + 15) / 16 : 16;
-      const int C = (P + CP - 1) / CP, Q = (M + 3) / 4;
+      const int C = (P + CP - 1) / CP, Q = (M + 7) / 8;
       *reinterpret_cast<int4*>(a.o.dec_prefix + 8LL * s_di[r]) =
           make_int4(P, s_gbase[L], C | (Q << 16), k);
     } else if (s_di[r] >= 0) {
@@ -337,7 +337,7 @@ __global__ void __launch_bounds__(kPackThreads) prefix_plan_kernel(PackArgs a) {
   }
   lds_sync();
   // the items: group (binary search over the groups' first items), then kv head, chunk,
-  // quad
+  // octet
   for (int i = tid; i < n_items; i += kPackThreads) {
     int lo = 0, hi = n_groups - 1;
     while (lo < hi) {
@@ -346,15 +346,16 @@ __global__ void __launch_bounds__(kPackThreads) prefix_plan_kernel(PackArgs a) {
     }
     const int L = s_glist[lo], P = s_gmin[L], M = s_gcnt[L];
     const int CP = P / 16 > 16 ? (P + 15) / 16 : 16;
-    const int C = (P + CP - 1) / CP, Q = (M + 3) / 4;
+    const int C = (P + CP - 1) / CP, Q = (M + 7) / 8;
     const int local = i - s_gbase[L];
     const int qd = local % Q, ch = (local / Q) % C, kvh = local / (Q * C);
-    int m[4];
+    int m[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) m[j] = 4 * qd + j < M ? s_mem[s_goff[L] + 4 * qd + j] : -1;
-    int4* dst = reinterpret_cast<int4*>(a.o.dec_pre_items + 8LL * i);
+    for (int j = 0; j < 8; ++j) m[j] = 8 * qd + j < M ? s_mem[s_goff[L] + 8 * qd + j] : -1;
+    int4* dst = reinterpret_cast<int4*>(a.o.dec_pre_items + 12LL * i);
     dst[0] = make_int4(s_di[L], kvh, ch * CP, min((ch + 1) * CP, P));
     dst[1] = make_int4(m[0], m[1], m[2], m[3]);
+    dst[2] = make_int4(m[4], m[5], m[6], m[7]);
   }
 }
 

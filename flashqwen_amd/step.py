@@ -105,7 +105,7 @@ class AttnStep:
         self.pre_items = torch.zeros((max(self.pre_cap, 1), 4), **i32)
         self.meta = torch.zeros(_lib.META_LEN, **i32)
         self.dec_prefix = torch.zeros((max(R, 1), 8), **i32)
-        self.dec_pre_items = torch.zeros((max(self.dec_pre_cap, 1), 8), **i32)
+        self.dec_pre_items = torch.zeros((max(self.dec_pre_cap, 1), 12), **i32)
         ws = int(self.lib.fqa_decode_prefix_workspace_bytes(C.byref(self.dims), self.dec_wave_cap,
                                                             self.dec_pre_cap))
         self.workspace = torch.empty(max(ws, 16), dtype=torch.uint8, device=self.device)

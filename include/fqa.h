@@ -173,8 +173,8 @@ typedef struct fqa_pack_out {
   /* with dec_prefix_pages (otherwise NULL): */
   int32_t* dec_prefix;     /* [R][8] per decode index {P, first item, C | Q << 16, k};
                               columns 4..7 are the pack's working space         */
-  int32_t* dec_pre_items;  /* [dec_pre_cap][8] {leader di, kvh, page0, page1,
-                              member di x 4 (-1 past the group)}                */
+  int32_t* dec_pre_items;  /* [dec_pre_cap][12] {leader di, kvh, page0, page1,
+                              member di x 8 (-1 past the group)}                */
 } fqa_pack_out;
 
 typedef struct fqa_pack_cfg {
@@ -198,10 +198,10 @@ typedef struct fqa_pack_cfg {
  * FQA_DEC_PREFIX_CAP pages; the leader's is its own page count) is capped at
  * computed / 16 pages (every member keeps the page of its last key); the group's prefix
  * P is the smallest over its members.  When P >= dec_prefix_pages, keys [0, 16 P) of
- * every member are attended once for the whole group: the group's M members in quads of
- * 4 (Q = ceil(M/4)), its P pages in C chunks of CP = max(16, ceil(P/16)) pages, one
- * prefix item per (kv head, chunk, quad), in that order, groups by leader:
- * dec_pre_items[i] = {leader, kvh, c*CP, min((c+1)*CP, P), the quad's member decode
+ * every member are attended once for the whole group: the group's M members in octets of
+ * 8 (Q = ceil(M/8)), its P pages in C chunks of CP = max(16, ceil(P/16)) pages, one
+ * prefix item per (kv head, chunk, octet), in that order, groups by leader:
+ * dec_pre_items[i] = {leader, kvh, c*CP, min((c+1)*CP, P), the octet's member decode
  * indices}.  Member k of the group (by decode index) gets dec_prefix[di] = {P, the
  * group's first item, C | Q << 16, k} and its decode streams cover pages [P, pages) only
  * (the plan above with pages - P in place of pages, and dec_waves' page counted from the
@@ -363,7 +363,7 @@ int fqa_decode(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
 
 /* fqa_decode over a plan made with dec_prefix_pages (fqa_pack_cfg): first one wavefront
  * per prefix item attends pages [page0, page1) of its group's leader for the 4 query heads
- * of each of its (up to 4) members, at the decode's precision, leaving fp32 partials; then
+ * of each of its (up to 8) members, at the decode's precision, leaving fp32 partials; then
  * the split kernel starts each member's (kv head) stream from the log-sum-exp merge of its
  * C chunk partials, and the combine runs as in fqa_decode.  dec_prefix / dec_pre_items
  * are the pack's arrays, dec_pre_cap their capacity (0: no prefix items).  `workspace`

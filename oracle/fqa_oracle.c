@@ -230,7 +230,7 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
       if (P < dec_prefix_pages) continue;
       int M = 0;
       for (int di = 0; di < nd; ++di) M += lead[di] == l;
-      const int Q = (M + 3) / 4, CP = P / 16 > 16 ? (P + 15) / 16 : 16, Cn = (P + CP - 1) / CP;
+      const int Q = (M + 7) / 8, CP = P / 16 > 16 ? (P + 15) / 16 : 16, Cn = (P + CP - 1) / CP;
       ++n_groups;
       n_pitems += 8 * Cn * Q;
       for (int di = 0; di < nd; ++di)
@@ -363,8 +363,8 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
     }
     for (int w = 0; w < G; ++w) dec_waves[8 * w + 6] |= dec_seqs[4 * dec_waves[8 * w] + 2] & (1 << 30);
   }
-  /* prefix items, groups by leader: for each kv head, chunk c of CP pages and quad q of
-   * 4 members, {leader, kvh, page0, page1, member di x 4 (-1 past the group)}; member k
+  /* prefix items, groups by leader: for each kv head, chunk c of CP pages and octet q of
+   * 8 members, {leader, kvh, page0, page1, member di x 8 (-1 past the group)}; member k
    * of a group: dec_prefix[di] = {P, first item, C | Q << 16, k} */
   for (int di = 0; dec_prefix && di < nd; ++di) /* NULL when dec_prefix_pages is 0 */
     for (int k = 0; k < 8; ++k) dec_prefix[8 * di + k] = 0;
@@ -375,9 +375,9 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
       const int P = pfx[l];
       int M = 0;
       for (int di = 0; di < nd; ++di) M += lead[di] == l;
-      const int Q = (M + 3) / 4, CP = P / 16 > 16 ? (P + 15) / 16 : 16, Cn = (P + CP - 1) / CP;
-      int32_t* mem = (int32_t*)malloc(sizeof(int32_t) * 4 * Q);
-      for (int k = 0; k < 4 * Q; ++k) mem[k] = -1;
+      const int Q = (M + 7) / 8, CP = P / 16 > 16 ? (P + 15) / 16 : 16, Cn = (P + CP - 1) / CP;
+      int32_t* mem = (int32_t*)malloc(sizeof(int32_t) * 8 * Q);
+      for (int k = 0; k < 8 * Q; ++k) mem[k] = -1;
       for (int di = 0, k = 0; di < nd; ++di)
         if (lead[di] == l) {
           dec_prefix[8 * di + 0] = P;
@@ -389,12 +389,12 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
       for (int kvh = 0; kvh < 8; ++kvh)
         for (int c = 0; c < Cn; ++c)
           for (int q = 0; q < Q; ++q, ++item) {
-            int32_t* it = dec_pre_items + 8 * (int64_t)item;
+            int32_t* it = dec_pre_items + 12 * (int64_t)item;
             it[0] = l;
             it[1] = kvh;
             it[2] = c * CP;
             it[3] = (c + 1) * CP < P ? (c + 1) * CP : P;
-            for (int j = 0; j < 4; ++j) it[4 + j] = mem[4 * q + j];
+            for (int j = 0; j < 8; ++j) it[4 + j] = mem[8 * q + j];
           }
       free(mem);
     }

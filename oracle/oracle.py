@@ -85,7 +85,7 @@ def pack(computed, n_new, bt_off, bt_pages, *, max_rows, max_blocks, pool_pages,
         dec_waves=np.zeros((max(dec_wave_cap, 1), 8), np.int32),
         pre_items=np.zeros((max(pre_item_cap, 1), 4), np.int32),
         dec_prefix=np.zeros((max(R, 1), 8), np.int32),
-        dec_pre_items=np.zeros((max(dec_pre_cap, 1), 8), np.int32),
+        dec_pre_items=np.zeros((max(dec_pre_cap, 1), 12), np.int32),
         meta=np.zeros(16, np.int32))
     status = load().fqo_pack(
         R, _p(computed), _p(n_new), _p(bt_off), _p(bt_pages), max_rows, max_blocks,

@@ -75,6 +75,14 @@ static void run_step(int R, int max_ctx, int pool_pages, int mode) {
     for (int g = 0; g < nb; ++g) bt_pages[bt_off[r] + g] = perm[used++];
     rows += n_new[r];
   }
+  /* mode 6: decodes share their first pages (up to 4, and only cached ones) from a common
+   * run at the end of the permutation, so shared-prefix groups form */
+  if (mode == 6)
+    for (int r = 0; r < R; ++r) {
+      if (n_new[r] != 1) continue;
+      const int k = computed[r] / PAGE < 4 ? computed[r] / PAGE : 4;
+      for (int j = 0; j < k; ++j) bt_pages[bt_off[r] + j] = perm[pool_pages - 1 - j];
+    }
   /* edge cases of the status codes */
   if (mode == 1 && R > 0) n_new[0] += PAGE * 4;  /* short table */
   if (mode == 2 && R > 0) computed[R - 1] = -3;   /* negative */
@@ -95,10 +103,11 @@ static void run_step(int R, int max_ctx, int pool_pages, int mode) {
   int32_t* items = xcalloc((size_t)item_cap * 4, 4);
   const int pre_cap = 8 * 16 * R;
   int32_t* dpfx = xcalloc((size_t)R * 8 + 8, 4);
-  int32_t* ditems = xcalloc((size_t)pre_cap * 8 + 8, 4);
+  int32_t* ditems = xcalloc((size_t)pre_cap * 12 + 12, 4);
   int32_t meta[16];
   int st = fqo_pack(R, computed, n_new, bt_off, bt_pages, max_rows, max_blocks, pool_pages,
-                    waves, 4, wave_cap, tile, item_cap, mode == 0, mode == 0 ? 2 : 0, pre_cap, cu,
+                    waves, 4, wave_cap, tile, item_cap, mode == 0, mode == 0 || mode == 6 ? 1 : 0,
+                    pre_cap, cu,
                     qlen, pos, req, slot, bt, drids, prids, dseqs, dwaves, items, dpfx, ditems,
                     meta);
   printf("step R=%d mode=%d rows=%d status=%d\n", R, mode, rows, st);
@@ -110,8 +119,16 @@ static void run_step(int R, int max_ctx, int pool_pages, int mode) {
     long long runs = 0;
     for (int w = 0; w < meta[4]; ++w) runs += dwaves[8 * w + 3];
     long long dpages = 0;
-    for (int i = 0; i < meta[1]; ++i) dpages += computed[drids[i]] / PAGE + 1;
+    long long ppages = 0, pruns = 0;
+    for (int i = 0; i < meta[1]; ++i) {
+      dpages += computed[drids[i]] / PAGE + 1 - dpfx[8 * i];
+      ppages += dpfx[8 * i];
+    }
     EXPECT(runs == 8 * dpages, "decode shares cover %lld of %lld runs", runs, 8 * dpages);
+    /* the prefix items cover each member's shared pages once per kv head */
+    for (int i = 0; i < meta[10]; ++i)
+      for (int j = 4; j < 12; ++j) pruns += ditems[12 * i + j] >= 0 ? ditems[12 * i + 3] - ditems[12 * i + 2] : 0;
+    EXPECT(pruns == 8 * ppages, "prefix items cover %lld of %lld runs", pruns, 8 * ppages);
 
     int T = meta[0];
     uint16_t* qkv = xcalloc((size_t)(T ? T : 1) * STRIDE, 2);
@@ -181,7 +198,8 @@ int main(void) {
              ((3LL * NKV + 2) * 2 + 1) * PAGE * D + 7 * PAGE + 5,
          "pool offset");
   run_step(0, 256, 64, 0);
-  for (int mode = 0; mode <= 5; ++mode) run_step(6, 512, 400, mode);
+  for (int mode = 0; mode <= 6; ++mode) run_step(6, 512, 400, mode);
+  for (int k = 0; k < 3; ++k) run_step(rnd(8, 40), 1024, 2000, 6);
   for (int k = 0; k < 4; ++k) run_step(rnd(1, 24), 1024, 2000, 0);
   run_schedule(0);
   run_schedule(1);

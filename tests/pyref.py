@@ -115,7 +115,7 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
         n_items = 0
         for members, P in group_list:
             cp = max(16, -(-P // 16))
-            n_items += 8 * -(-P // cp) * -(-len(members) // 4)
+            n_items += 8 * -(-P // cp) * -(-len(members) // 8)
         if n_items > dec_pre_cap:
             group_list = []
         for members, P in group_list:
@@ -191,20 +191,20 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
     res["dec_seqs"] = seqs
     res["dec_waves"] = waves
     res["pre_items"] = items
-    # prefix items: per group (by leader), kv head, chunk of cp pages, quad of 4 members
+    # prefix items: per group (by leader), kv head, chunk of cp pages, octet of 8 members
     pitems, dpfx = [], [[0, 0, 0, 0] for _ in dec]
     for members, Pg in group_list:
         cp = max(16, -(-Pg // 16))
-        nc, nq = -(-Pg // cp), -(-len(members) // 4)
+        nc, nq = -(-Pg // cp), -(-len(members) // 8)
         base = len(pitems)
         for k, di in enumerate(members):
             dpfx[di] = [Pg, base, nc | (nq << 16), k]
-        padded = members + [-1] * (4 * nq - len(members))
+        padded = members + [-1] * (8 * nq - len(members))
         for kvh in range(8):
             for c in range(nc):
                 for q in range(nq):
                     pitems.append([members[0], kvh, c * cp, min((c + 1) * cp, Pg)]
-                                  + padded[4 * q:4 * q + 4])
+                                  + padded[8 * q:8 * q + 8])
     res["dec_prefix"] = dpfx
     res["dec_pre_items"] = pitems
     meta[10], meta[11], meta[12] = len(pitems), len(group_list), W

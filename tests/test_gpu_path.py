@@ -203,7 +203,7 @@ def test_decode_long_and_shared_prefix(gpu):
 def test_decode_shared_prefix_groups(gpu, minp):
     """Config 5's decode batch with its shared prefixes attended once per group
     (dec_prefix_pages): 4 groups of 24 sequences whose first 128 pages are the same; each
-    group's prefix items (8 kv heads x 8 chunks of 16 pages x 6 quads) leave partials that
+    group's prefix items (8 kv heads x 8 chunks of 16 pages x 3 octets) leave partials that
     start every member's streams at page 128.  Plan bit-exact against the oracle, decode
     rows within tolerance and within one bf16 step of the oracle per element."""
     print(f"[test_decode_shared_prefix_groups] config5, 1 layer, min pages {minp}", flush=True)
@@ -217,7 +217,7 @@ def test_decode_shared_prefix_groups(gpu, minp):
 @pytest.mark.parametrize("seed", range(4))
 def test_decode_prefix_random_groups(gpu, seed):
     """Random decode batches whose tables share leading runs of any length (groups of 2
-    or more with prefixes from 1 page up, chunked prefixes, quads with fewer than 4
+    or more with prefixes from 1 page up, chunked prefixes, octets with fewer than 8
     members), beside prefill rows; the whole step against the oracle."""
     rng = np.random.default_rng(700 + seed)
     R = int(rng.choice([12, 40, 120]))

@@ -398,7 +398,7 @@ def test_pack_prefix_known_answer():
     too (prefills neither join nor cause groups).  The group of first page 5 is led by r0
     (decode index 0); common runs with it: r0 3 pages, capped at 40 // 16 = 2; r1 2; r4 3.
     So P = 2: pages 0 and 1 of the three are attended once (8 items, one per kv head, one
-    chunk, one quad {0, 1, 3, -1}) and their streams start at page 2, with the shared flag
+    chunk, one octet {0, 1, 3, -1 x 5}) and their streams start at page 2, with the shared flag
     cleared (their own pages are private).  At dec_prefix_pages = 3 the group is not used."""
     comp = [40, 47, 20, 0, 70]
     nnew = [1, 1, 1, 10, 1]
@@ -410,7 +410,8 @@ def test_pack_prefix_known_answer():
     assert (int(m[1]), int(m[9]), int(m[10]), int(m[11])) == (4, 7, 8, 1)
     assert got["dec_prefix"][:4, :4].tolist() == [[2, 0, 1 | 1 << 16, 0], [2, 0, 1 | 1 << 16, 1],
                                                   [0, 0, 0, 0], [2, 0, 1 | 1 << 16, 2]]
-    assert got["dec_pre_items"][:8].tolist() == [[0, h, 0, 2, 0, 1, 3, -1] for h in range(8)]
+    assert got["dec_pre_items"][:8].tolist() == [[0, h, 0, 2, 0, 1, 3] + [-1] * 5
+                                                 for h in range(8)]
     flag = 1 << 30
     seqs = got["dec_seqs"][:4]
     assert [int(z) for z in seqs[:, 2]] == [41, 48, 21, 71]  # no flags: groups read their own
@@ -433,7 +434,7 @@ def test_pack_prefix_covers_every_page_once():
     """For every decode sequence and kv head, the prefix items of its group (pages
     [page0, page1) of the leader's table, which equal the member's) and the plan's shares
     of its stream together cover each of its pages exactly once, and each member is in
-    exactly one quad slot of its group's items per (kv head, chunk)."""
+    exactly one octet slot of its group's items per (kv head, chunk)."""
     from tests.test_gpu_pack import rand_batch
 
     for seed in range(6):
