@@ -64,6 +64,11 @@ def parse():
                     help="mixed steps: keep the decode on the step's stream (by default it "
                          "runs on a second stream beside the prefill, planned for the CUs "
                          "the prefill leaves: dec_share)")
+    ap.add_argument("--dec-prefix-pages", type=int, default=None,
+                    help="decode sequences sharing at least this many leading pages attend "
+                         "them once per group (fqa_decode_prefix); default 8 on config 5 "
+                         "(its 4 groups of 24 sequences on 128-page prefixes), 0 (off) "
+                         "elsewhere.  The line also times the decode without it")
     ap.add_argument("--gemm", action="store_true",
                     help="only measure fqa_gemm on the Qwen3-8B projections (decode and "
                          "prefill row counts) beside torch.matmul (hipBLASLt)")
@@ -206,11 +211,19 @@ def run_config(args, config, *, steps, warmup, with_cpu):
         flat[s:e].normal_(generator=g)
     out = torch.zeros((T, synth.N_Q * synth.HEAD_DIM), dtype=torch.bfloat16, device=dev)
 
-    step = AttnStep(max_rows=T, max_reqs=cfg.n_reqs, max_ctx=cfg.max_ctx,
-                    pool_pages=cfg.pool_pages, device=dev,
-                    dec_grid_waves=args.dec_grid_waves, dec_min_pages=args.dec_min_pages,
-                    pre_tile_q=args.pre_tile_q,
-                    dec_share=not (args.no_overlap or args.no_dec_share))
+    prefix_pages = args.dec_prefix_pages
+    if prefix_pages is None:
+        prefix_pages = 8 if config == 5 else 0
+
+    def make_step(pp):
+        return AttnStep(max_rows=T, max_reqs=cfg.n_reqs, max_ctx=cfg.max_ctx,
+                        pool_pages=cfg.pool_pages, device=dev,
+                        dec_grid_waves=args.dec_grid_waves, dec_min_pages=args.dec_min_pages,
+                        pre_tile_q=args.pre_tile_q,
+                        dec_share=not (args.no_overlap or args.no_dec_share),
+                        dec_prefix_pages=pp)
+
+    step = make_step(prefix_pages)
     d_computed, d_n_new = t(cfg.computed), t(cfg.n_new)
     d_off, d_pages = t(cfg.bt_off), t(cfg.bt_pages)
     d_ntok = t(cfg.num_tokens) if scheduled else None
@@ -304,6 +317,14 @@ def run_config(args, config, *, steps, warmup, with_cpu):
         kernels["decode"] = lambda: step.attn_decode(qkv, pool[0], out)
         # the same plan's pages read with the same loads and no arithmetic: the floor
         kernels["decode_read_floor"] = lambda: step.decode_read_floor(pool[0])
+        if prefix_pages > 0 and not scheduled:
+            # the same batch decoded without the shared-prefix groups (fqa_decode), for
+            # comparison: its own plan, packed once before capture
+            plain = make_step(0)
+            plain.prepare_inputs(d_computed, d_n_new, d_off, d_pages, rows_bound=T)
+            out_plain = torch.zeros_like(out)
+            kernels["decode_no_prefix"] = lambda: plain.attn_decode(qkv, pool[0], out_plain)
+            kernels["decode_read_floor_no_prefix"] = lambda: plain.decode_read_floor(pool[0])
     if has_prefill:
         kernels["prefill"] = lambda: step.attn_prefill(qkv, pool[0], out)
     kgraphs = {k: kernel_graph(f, reps) for k, f in kernels.items()}
@@ -346,9 +367,14 @@ def run_config(args, config, *, steps, warmup, with_cpu):
         bt_bytes = int(meta[9]) * 4
         bytes_per = logical + bt_bytes
         achieved = bytes_per / (kern_ms["decode"] * 1e-3) / 1e9
-        traffic, tsrc = _profile_traffic(config,
-                                         ["decode_split_kernel", "decode_combine_kernel"])
-        roof = {"kernel": "fqa_decode (decode_split_kernel + decode_combine_kernel)",
+        dec_kernels = ["decode_split_kernel", "decode_combine_kernel"]
+        name = "fqa_decode (decode_split_kernel + decode_combine_kernel)"
+        if prefix_pages > 0:
+            dec_kernels = ["decode_prefix_kernel"] + dec_kernels
+            name = ("fqa_decode_prefix (decode_prefix_kernel + decode_split_kernel + "
+                    "decode_combine_kernel)")
+        traffic, tsrc = _profile_traffic(config, dec_kernels)
+        roof = {"kernel": name,
                 "bound": "hbm",
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
@@ -357,6 +383,24 @@ def run_config(args, config, *, steps, warmup, with_cpu):
                 "launch_us": round(kern_ms["decode"] * 1e3, 2),
                 "read_floor_us": round(kern_ms["decode_read_floor"] * 1e3, 2),
                 "frac_of_read_floor": round(kern_ms["decode_read_floor"] / kern_ms["decode"], 4)}
+        if prefix_pages > 0:
+            # achieved counts a shared prefix's bytes once per reading sequence (the metric's
+            # definition); the plan reads each group's prefix once per 8 members, so the
+            # bytes the plan reads and their rate are stated beside it
+            items = step.dec_pre_items[:int(meta[10])].cpu().numpy()
+            item_runs = int((items[:, 3] - items[:, 2]).sum()) if len(items) else 0
+            run_bytes = synth.PAGE_BYTES // synth.N_KV
+            n_dec = int(meta[1])
+            plan_bytes = ((int(meta[9]) * synth.N_KV + item_runs) * run_bytes + bt_bytes +
+                          n_dec * 2 * synth.N_Q * synth.HEAD_DIM * 2)
+            roof["plan_read_bytes"] = plan_bytes
+            roof["plan_read_GBps"] = round(plan_bytes / (kern_ms["decode"] * 1e-3) / 1e9, 1)
+            roof["prefix_groups"] = int(meta[11])
+            roof["prefix_items"] = int(meta[10])
+            if "decode_no_prefix" in kern_ms:
+                roof["no_prefix_launch_us"] = round(kern_ms["decode_no_prefix"] * 1e3, 2)
+                roof["no_prefix_frac"] = round(
+                    bytes_per / (kern_ms["decode_no_prefix"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
     else:
         flops = synth.prefill_flops(comp_sel, n_sel)
         achieved = flops / (kern_ms["prefill"] * 1e-3) / 1e12
@@ -405,7 +449,7 @@ def run_config(args, config, *, steps, warmup, with_cpu):
                    "rows_per_step": T, "requests": int(len(n_sel)), "layers": layers,
                    "pool_pages_per_layer": cfg.pool_pages, "head_shape": "32q/8kv/128",
                    "dec_wave_runs": int(meta[6]), "dec_waves": int(meta[4]),
-                   "pre_items": int(meta[5])},
+                   "pre_items": int(meta[5]), "dec_prefix_pages": prefix_pages},
         "roofline": roof,
         "kernels_us": {k: round(v * 1e3, 2) for k, v in kern_ms.items()},
         "step_floor_us": round(floor_us, 2),

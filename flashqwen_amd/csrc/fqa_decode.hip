@@ -80,6 +80,10 @@ struct DecArgs {
   float* pws_m;           // prefix partials: [pre_cap][32 columns]
   float* pws_l;
   float* pws_acc;         // [pre_cap][32][128]
+  // a member's whole (uncut) stream: its partial, at the column its chunk-0 item gives it
+  float* pms_m;
+  float* pms_l;
+  float* pms_acc;
   int pre_cap;
 };
 
@@ -256,53 +260,20 @@ __device__ __forceinline__ void stream_pages(const DecArgs& a, const int32_t* bt
                                 reinterpret_cast<DecState(&)[1]>(st), first_page);
 }
 
-// The state a shared-prefix member's (kv head) stream starts from: the log-sum-exp merge
-// of its group's C chunk partials (decode_prefix_kernel) for its 4 query heads, in the
-// layout of DecState (lane: column n = head, rows d = b*16 + 4g + j; l on lane group 0).
-__device__ void prefix_state(const DecArgs& a, const int4 info, int kvh, int lane,
-                             DecState& st) {
-  const int n = lane & 15, g = lane >> 4;
-  if (n >= kG) return;  // columns past the 4 heads carry nothing
+// Column of member k (its k-th member, in decode order) of a shared-prefix group, head n,
+// in the prefix partials of chunk c: item (first item + (kvh * C + c) * Q + k / 8),
+// column (k % 8) * 4 + n.
+__device__ __forceinline__ long long prefix_slot(const int4 info, int kvh, int c, int n) {
   const int C = info.z & 0xFFFF, Q = info.z >> 16, k = info.w;
-  // the pack's items fit dec_pre_cap; a workspace planned for fewer is never read past
-  if ((long long)info.y + 8LL * C * Q > a.pre_cap) return;
-  const int col = (k & 7) * kG + n;  // member k & 7 of its item, head n
-  auto slot = [&](int c) {
-    return ((long long)info.y + ((long long)kvh * C + c) * Q + (k >> 3)) * kPrefixCols + col;
-  };
-  // online log-sum-exp merge, 8 chunks' loads in flight at a time (C <= 16)
-  float m0 = -1e30f, l = 0.f;
-  float4_t acc[8];
-#pragma unroll
-  for (int b = 0; b < 8; ++b) acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
-  constexpr int kB = 8;
-  for (int c0 = 0; c0 < C; c0 += kB) {
-    float mc[kB], lc[kB];
-    float4_t xc[kB][8];
-#pragma unroll
-    for (int j = 0; j < kB; ++j) {
-      const long long sl = slot(min(c0 + j, C - 1));
-      mc[j] = a.pws_m[sl];
-      lc[j] = a.pws_l[sl];
-      const float* src = a.pws_acc + sl * kD + g * 4;
-#pragma unroll
-      for (int b = 0; b < 8; ++b) xc[j][b] = *reinterpret_cast<const float4_t*>(src + b * 16);
-    }
-#pragma unroll
-    for (int j = 0; j < kB; ++j) {
-      if (c0 + j >= C) break;
-      const float mn = fmaxf(m0, mc[j]);
-      const float co = __builtin_amdgcn_exp2f(m0 - mn), cn = __builtin_amdgcn_exp2f(mc[j] - mn);
-      l = l * co + lc[j] * cn;
-#pragma unroll
-      for (int b = 0; b < 8; ++b) acc[b] = acc[b] * co + xc[j][b] * cn;
-      m0 = mn;
-    }
-  }
-  st.m = m0;
-  st.l = g == 0 ? l : 0.f;
-#pragma unroll
-  for (int b = 0; b < 8; ++b) st.acc[b] = acc[b];
+  return ((long long)info.y + ((long long)kvh * C + c) * Q + (k >> 3)) * kPrefixCols +
+         (k & 7) * kG + n;
+}
+
+// The pack's items fit dec_pre_cap; a workspace planned for fewer is never touched past its
+// end (the group's rows are then left out).
+__device__ __forceinline__ bool prefix_fits(const int4 info, int pre_cap) {
+  const int C = info.z & 0xFFFF, Q = info.z >> 16;
+  return (long long)info.y + 8LL * C * Q <= pre_cap;
 }
 
 // Shared-prefix items: one wavefront per item streams pages [page0, page1) of the group
@@ -433,7 +404,6 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
     for (int b = 0; b < 8; ++b) st.acc[b] = float4_t{0.f, 0.f, 0.f, 0.f};
     st.m = -1e30f;
     st.l = 0.f;
-    if (P > 0 && page == P) prefix_state(a, pinfo, kvh, lane, st);  // the stream's start
     if (shared)
       stream_pages<kBufs, false>(a, a.bt + (long long)r * a.max_blocks, kvh, page, page + cnt, L,
                                  qf, lane, st, sq.w);
@@ -443,7 +413,19 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel
     const float l_run = sum_rows4(st.l);
 
     if (n < kG) {
-      if (page == P && cnt == pages - P) {  // whole stream: final output
+      if (page == P && cnt == pages - P && P > 0) {
+        // a shared-prefix member's whole stream: the combine merges it with the prefix
+        if (prefix_fits(pinfo, a.pre_cap)) {
+          const long long slot = prefix_slot(pinfo, kvh, 0, n);
+          if (g == 0) {
+            a.pms_m[slot] = st.m;
+            a.pms_l[slot] = l_run;
+          }
+          float* wa = a.pms_acc + slot * kD + g * 4;
+#pragma unroll
+          for (int b = 0; b < 8; ++b) *reinterpret_cast<float4_t*>(wa + b * 16) = st.acc[b];
+        }
+      } else if (page == P && cnt == pages - P) {  // whole stream: final output
         const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
         uint16_t* o = a.out + (long long)row * (kHq * kD) + (kvh * kG + n) * kD + g * 4;
 #pragma unroll
@@ -553,7 +535,8 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_read_floor_k
 }
 
 // Log-sum-exp merge of a cut stream's partials (attn_cute.cu:225-238): one wave per
-// (decode sequence, kv head) stream, lane -> (head = lane/16, 8 dims).  The shares that
+// (decode sequence, kv head) stream, lane -> (head = lane/16, 8 dims).  A shared-prefix
+// member's stream is always merged: its group's C prefix chunk partials, then its own.  The shares that
 // hold stream s's page positions [F, S1) are w_first..w_last (share w = [w*W/G,
 // (w+1)*W/G)); the stream is the last of w_first's streams (slot 2w+1), or its first
 // (slot 2w) when w_first's share starts in s's own cost span [S0, F], and the first of
@@ -564,7 +547,9 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_combine_kern
   // di < n_reqs_bound, the rows of `seqs`: the sequence is read with the counts (one round
   // trip, not two)
   const int4 sq = *reinterpret_cast<const int4*>(a.seqs + 4 * (long long)di);
-  const int pfx = a.prefix ? a.prefix[8LL * di] : 0;
+  const int4 pinfo = a.prefix ? *reinterpret_cast<const int4*>(a.prefix + 8LL * di)
+                              : make_int4(0, 0, 0, 0);
+  const int pfx = pinfo.x;
   const int n_dec = a.meta[FQA_META_N_DECODE];
   asm volatile("" ::"v"(sq.x), "v"(pfx), "s"(n_dec));
   if (di >= n_dec) return;
@@ -577,12 +562,49 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_combine_kern
   const long long S0 = sq.w + (long long)kvh * (pages + sc);
   const long long F = S0 + sc, S1 = F + pages;  // page positions [F, S1)
   const long long wf = ((F + 1) * G - 1) / W, wl = (S1 * G - 1) / W;
-  if (wf == wl) return;  // finished by one wavefront
+  // a stream finished by one wavefront is final, unless a shared prefix precedes it
+  if (wf == wl && pfx == 0) return;
+  if (pfx > 0 && !prefix_fits(pinfo, a.pre_cap)) return;
   const int lane = threadIdx.x & 63;
   const int h = lane >> 4, d0 = (lane & 15) * 8;
   float gm = -1e30f, gl = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  // partials in batches of 4: all loads of a batch are issued before any is used
-  for (long long w0 = wf; w0 <= wl; w0 += 4) {
+  auto merge = [&](float m, float l, float4 x0, float4 x1) {
+    const float mn = fmaxf(gm, m);
+    const float co = exp2f(gm - mn), cn = exp2f(m - mn);
+    gl = gl * co + l * cn;
+    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = acc[i] * co + xs[i] * cn;
+    gm = mn;
+  };
+  // a shared prefix's C chunk partials (and, for a stream no wavefront cut, the stream's
+  // own partial), 4 loads in flight at a time
+  if (pfx > 0) {
+    const int C = pinfo.z & 0xFFFF;
+    const int nc = C + (wf == wl);
+    for (int c0 = 0; c0 < nc; c0 += 4) {
+      float m[4], l[4];
+      float4 x0[4], x1[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int c = min(c0 + k, nc - 1);
+        const bool own = c == C;  // the uncut stream's partial
+        const long long slot = prefix_slot(pinfo, kvh, own ? 0 : c, h);
+        m[k] = (own ? a.pms_m : a.pws_m)[slot];
+        l[k] = (own ? a.pms_l : a.pws_l)[slot];
+        const float4* src =
+            reinterpret_cast<const float4*>((own ? a.pms_acc : a.pws_acc) + slot * kD + d0);
+        x0[k] = src[0];
+        x1[k] = src[1];
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (c0 + k < nc) merge(m[k], l[k], x0[k], x1[k]);
+    }
+  }
+  // the cut stream's partials in batches of 4: all loads of a batch are issued before any
+  // is used
+  for (long long w0 = wf; w0 <= wl && wf < wl; w0 += 4) {
     float m[4], l[4];
     float4 x0[4], x1[4];
 #pragma unroll
@@ -598,16 +620,8 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_combine_kern
       x1[k] = src[1];
     }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      if (w0 + k > wl) break;
-      const float mn = fmaxf(gm, m[k]);
-      const float co = exp2f(gm - mn), cn = exp2f(m[k] - mn);
-      gl = gl * co + l[k] * cn;
-      const float xs[8] = {x0[k].x, x0[k].y, x0[k].z, x0[k].w, x1[k].x, x1[k].y, x1[k].z, x1[k].w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] = acc[i] * co + xs[i] * cn;
-      gm = mn;
-    }
+    for (int k = 0; k < 4; ++k)
+      if (w0 + k <= wl) merge(m[k], l[k], x0[k], x1[k]);
   }
   const float inv = gl > 0.f ? 1.0f / gl : 0.f;
   uint4 v = make_uint4(pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv),
@@ -640,7 +654,8 @@ int decode_launch(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* poo
   DecArgs a{qkv, pool, pool_pages, block_tables, max_blocks, dec_waves, dec_seqs, meta, ws,
             ws + slots, ws + 2 * slots, out, dims->qkv_stride, dims->scale * kLog2e, dec_wave_cap};
   if (dec_prefix) {
-    // prefix partials after the stream partials: m, l [pre_cap][32], acc [pre_cap][32][128]
+    // after the stream partials: the prefix chunk partials, m, l [pre_cap][32] and acc
+    // [pre_cap][32][128], then as many for the members' uncut streams
     float* pws = ws + slots * (2 + kD);
     const long long ps = (long long)kPrefixCols * dec_pre_cap;
     a.prefix = dec_prefix;
@@ -648,6 +663,10 @@ int decode_launch(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* poo
     a.pws_m = pws;
     a.pws_l = pws + ps;
     a.pws_acc = pws + 2 * ps;
+    float* pms = pws + ps * (2 + kD);
+    a.pms_m = pms;
+    a.pms_l = pms + ps;
+    a.pms_acc = pms + 2 * ps;
     a.pre_cap = dec_pre_cap;
     if (dec_pre_cap > 0)
       hipLaunchKernelGGL(decode_prefix_kernel,
@@ -761,7 +780,7 @@ int64_t fqa_decode_prefix_workspace_bytes(const fqa_dims* dims, int32_t dec_wave
                                           int32_t dec_pre_cap) {
   if (dec_wave_cap < 0 || dec_pre_cap < 0) return 0;
   return fqa_decode_workspace_bytes(dims, dec_wave_cap) +
-         (int64_t)kPrefixCols * dec_pre_cap * (2 + kD) * (int64_t)sizeof(float);
+         2 * (int64_t)kPrefixCols * dec_pre_cap * (2 + kD) * (int64_t)sizeof(float);
 }
 
 int fqa_decode_prefix(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,

@@ -76,8 +76,8 @@ extern "C" {
  * kv head) stream counts its pages plus this, so a wavefront whose share holds many short
  * streams gets fewer pages (a stream start costs a few dependent loads). */
 #define FQA_DEC_STREAM_COST 4
-/* ... and this more for a shared-prefix member's stream (dec_prefix_pages), which first
- * merges its group's prefix partials. */
+/* ... and this more for a shared-prefix member's stream (dec_prefix_pages): such a stream
+ * always leaves a partial for the combine (measured on config 5: 0, 2, 4 and 8 within 1%). */
 #define FQA_DEC_PREFIX_STREAM_COST 4
 /* Pages of a decode sequence compared with its group leader's for a shared prefix
  * (fqa_pack_cfg::dec_prefix_pages). */
@@ -364,8 +364,8 @@ int fqa_decode(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
 /* fqa_decode over a plan made with dec_prefix_pages (fqa_pack_cfg): first one wavefront
  * per prefix item attends pages [page0, page1) of its group's leader for the 4 query heads
  * of each of its (up to 8) members, at the decode's precision, leaving fp32 partials; then
- * the split kernel starts each member's (kv head) stream from the log-sum-exp merge of its
- * C chunk partials, and the combine runs as in fqa_decode.  dec_prefix / dec_pre_items
+ * the split kernel attends each member's (kv head) stream from page P on and leaves its
+ * partial, and the combine merges it with the group's C chunk partials (log-sum-exp).  dec_prefix / dec_pre_items
  * are the pack's arrays, dec_pre_cap their capacity (0: no prefix items).  `workspace`
  * must hold fqa_decode_prefix_workspace_bytes(dims, dec_wave_cap, dec_pre_cap) bytes.
  * The same output as fqa_decode up to fp32 rounding (the prefix keys are summed in
