@@ -317,9 +317,10 @@ def run_config(args, config, *, steps, warmup, with_cpu):
         kernels["decode"] = lambda: step.attn_decode(qkv, pool[0], out)
         # the same plan's pages read with the same loads and no arithmetic: the floor
         kernels["decode_read_floor"] = lambda: step.decode_read_floor(pool[0])
-        if prefix_pages > 0 and not scheduled:
+        if prefix_pages > 0 and not scheduled and not args.profile_kernels:
             # the same batch decoded without the shared-prefix groups (fqa_decode), for
-            # comparison: its own plan, packed once before capture
+            # comparison: its own plan, packed once before capture (not under the profiler,
+            # whose per-kernel averages would mix the two plans' split kernels)
             plain = make_step(0)
             plain.prepare_inputs(d_computed, d_n_new, d_off, d_pages, rows_bound=T)
             out_plain = torch.zeros_like(out)
