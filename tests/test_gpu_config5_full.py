@@ -2,7 +2,9 @@
 per layer, 5.5 GB each, so every layer but the first sits beyond 5 GB of the allocation and
 the last beyond 190 GB), then layers 0, 17 and 35 checked against the CPU oracle on those
 layers' pages: norm/RoPE of q and k, the append of k and v, and the attention kernels on the
-GPU's own post-append q and pool."""
+GPU's own post-append q and pool.  The decode runs as bench.py runs it: with the
+shared-prefix groups (dec_prefix_pages 8: the 4 groups of 24 sequences attend their 128-page
+prefix once per 8 members)."""
 from __future__ import annotations
 
 import numpy as np
@@ -38,7 +40,7 @@ def test_config5_36_layers_full_pool(gpu):
     out = torch.zeros((L, T, N_Q * HEAD_DIM), dtype=torch.bfloat16, device=gpu)
     wq, wk = synth.norm_weights()
     step = AttnStep(max_rows=T, max_reqs=R, max_ctx=cfg.max_ctx, pool_pages=cfg.pool_pages,
-                    device=gpu)
+                    device=gpu, dec_prefix_pages=8)
     step.prepare_inputs(t(cfg.computed), t(cfg.n_new), t(cfg.bt_off), t(cfg.bt_pages))
     wq_d, wk_d = t(wq), t(wk)
     for l in range(L):
@@ -46,9 +48,11 @@ def test_config5_36_layers_full_pool(gpu):
     torch.cuda.synchronize()
     print("  step done", flush=True)
 
-    kw = sc.pack_kwargs(cfg, dec_grid_waves=step.dec_grid_waves, dec_min_pages=8)
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=step.dec_grid_waves, dec_min_pages=8,
+                        dec_prefix_pages=8, dec_pre_cap=step.dec_pre_cap)
     pk = orc.pack(cfg.computed, cfg.n_new, cfg.bt_off, cfg.bt_pages, **kw)
     assert np.array_equal(step.meta_host(), pk["meta"])
+    assert int(pk["meta"][11]) == 4 and int(pk["meta"][10]) > 0  # the 4 groups were found
     cos, sin = orc.rope_tables(cfg.max_ctx)
     pages, toks = sc.written_mask(pk, T)
     no_slot = np.full(T, -1, np.int32)
