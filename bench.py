@@ -371,9 +371,8 @@ def run_config(args, config, *, steps, warmup, with_cpu):
         dec_kernels = ["decode_split_kernel", "decode_combine_kernel"]
         name = "fqa_decode (decode_split_kernel + decode_combine_kernel)"
         if prefix_pages > 0:
-            dec_kernels = ["decode_prefix_kernel"] + dec_kernels
-            name = ("fqa_decode_prefix (decode_prefix_kernel + decode_split_kernel + "
-                    "decode_combine_kernel)")
+            name = ("fqa_decode_prefix (decode_split_kernel, its workgroups past the "
+                    "shares running the prefix items, + decode_combine_kernel)")
         traffic, tsrc = _profile_traffic(config, dec_kernels)
         roof = {"kernel": name,
                 "bound": "hbm",

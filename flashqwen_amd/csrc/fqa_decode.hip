@@ -85,6 +85,7 @@ struct DecArgs {
   float* pms_l;
   float* pms_acc;
   int pre_cap;
+  int split_blocks;  // decode_split_kernel: workgroups past these run prefix items
 };
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -276,12 +277,13 @@ __device__ __forceinline__ bool prefix_fits(const int4 info, int pre_cap) {
   return (long long)info.y + 8LL * C * Q <= pre_cap;
 }
 
-// Shared-prefix items: one wavefront per item streams pages [page0, page1) of the group
-// leader's table (which its members' tables equal there) once for the 4 query heads of
-// each of up to 8 members (2 sets of 16 MFMA columns: member j, head h at column 4j + h),
-// with the decode's page loop and arithmetic, and leaves the 32 columns' fp32 partials.
-__global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_prefix_kernel(DecArgs a) {
-  const int w = blockIdx.x * kDecWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+// Shared-prefix item w, run by decode_split_kernel's workgroups past its shares (they take
+// the CUs the shares leave as they finish): one wavefront streams pages [page0, page1) of
+// the group leader's table (which its members' tables equal there) once for the 4 query
+// heads of each of up to 8 members (2 sets of 16 MFMA columns: member j, head h at column
+// 4j + h), with the decode's page loop and arithmetic, and leaves the 32 columns' fp32
+// partials.
+__device__ __forceinline__ void prefix_item(const DecArgs& a, int w) {
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   const int n_items = a.meta[FQA_META_DEC_PRE_ITEMS];
@@ -346,6 +348,11 @@ template <int kBufs>
 __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_split_kernel(DecArgs a) {
   __shared__ char lds_excl[kDecExclusiveLds];  // allocated, never accessed
   asm volatile("" ::"s"((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds_excl));
+  if (blockIdx.x >= a.split_blocks) {  // shared-prefix items, dispatched as CUs free up
+    prefix_item(a, (blockIdx.x - a.split_blocks) * kDecWavesPerBlock +
+                       __builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
+    return;
+  }
   // Everything a wave's loop indexes with is wave-uniform; readfirstlane says so, so that
   // block-table reads become scalar loads (see stream_pages).
   const int w = blockIdx.x * kDecWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -668,13 +675,10 @@ int decode_launch(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* poo
     a.pms_l = pms + ps;
     a.pms_acc = pms + 2 * ps;
     a.pre_cap = dec_pre_cap;
-    if (dec_pre_cap > 0)
-      hipLaunchKernelGGL(decode_prefix_kernel,
-                         dim3((dec_pre_cap + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
-                         dim3(kDecWavesPerBlock * kWave), 0, stream, a);
   }
-  hipLaunchKernelGGL(decode_split_kernel<kDecBufs>,
-                     dim3((dec_wave_cap + kDecWavesPerBlock - 1) / kDecWavesPerBlock),
+  a.split_blocks = (dec_wave_cap + kDecWavesPerBlock - 1) / kDecWavesPerBlock;
+  const int pre_blocks = a.prefix ? (dec_pre_cap + kDecWavesPerBlock - 1) / kDecWavesPerBlock : 0;
+  hipLaunchKernelGGL(decode_split_kernel<kDecBufs>, dim3(a.split_blocks + pre_blocks),
                      dim3(kDecWavesPerBlock * kWave), 0, stream, a);
   const int waves2 = n_reqs_bound * kHkv;
   hipLaunchKernelGGL(decode_combine_kernel,

@@ -361,11 +361,12 @@ int fqa_decode(const fqa_dims* dims, const uint16_t* qkv, const uint16_t* pool,
                int32_t dec_wave_cap, int32_t n_reqs_bound, void* workspace, uint16_t* out,
                void* stream);
 
-/* fqa_decode over a plan made with dec_prefix_pages (fqa_pack_cfg): first one wavefront
- * per prefix item attends pages [page0, page1) of its group's leader for the 4 query heads
- * of each of its (up to 8) members, at the decode's precision, leaving fp32 partials; then
- * the split kernel attends each member's (kv head) stream from page P on and leaves its
- * partial, and the combine merges it with the group's C chunk partials (log-sum-exp).  dec_prefix / dec_pre_items
+/* fqa_decode over a plan made with dec_prefix_pages (fqa_pack_cfg): the split kernel
+ * attends each member's (kv head) stream from page P on and leaves its partial; workgroups
+ * launched past its shares (they run as the shares' CUs free up) take one prefix item per
+ * wavefront: pages [page0, page1) of the group leader's table for the 4 query heads of each
+ * of the item's (up to 8) members, at the decode's precision, into fp32 partials.  The
+ * combine merges a member's stream with its group's C chunk partials (log-sum-exp).  dec_prefix / dec_pre_items
  * are the pack's arrays, dec_pre_cap their capacity (0: no prefix items).  `workspace`
  * must hold fqa_decode_prefix_workspace_bytes(dims, dec_wave_cap, dec_pre_cap) bytes.
  * The same output as fqa_decode up to fp32 rounding (the prefix keys are summed in
