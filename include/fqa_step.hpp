@@ -16,6 +16,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <stdexcept>
@@ -70,8 +71,11 @@ class StepContext {
  public:
   // dec_share: RunLayer / RunLayerBounded will be given a side stream, so the pack plans a
   // mixed batch's decode for the CUs the concurrent prefill leaves (fqa.h, dec_share).
+  // dec_prefix_pages > 0: decode sequences sharing at least that many leading pages attend
+  // them once per group (fqa_decode_prefix), with up to dec_pre_cap prefix items a step.
   StepContext(int max_rows, int slots, int max_ctx, int64_t pool_pages, int device = 0,
-              int dec_grid_waves = 0, int dec_min_pages = 8, bool dec_share = false)
+              int dec_grid_waves = 0, int dec_min_pages = 8, bool dec_share = false,
+              int dec_prefix_pages = 0, int dec_pre_cap = 4096)
       : max_rows_(max_rows), slots_(slots), max_ctx_(max_ctx), pool_pages_(pool_pages) {
     if (slots > FQA_MAX_REQS) throw std::runtime_error("slots > FQA_MAX_REQS");
     max_blocks_ = (max_ctx + FQA_PAGE_TOKENS - 1) / FQA_PAGE_TOKENS;
@@ -80,8 +84,10 @@ class StepContext {
     if (dec_grid_waves <= 0) dec_grid_waves = 1024;
     dec_cap_ = fqa_dec_wave_bound(slots, dec_grid_waves);
     pre_cap_ = fqa_pre_item_bound(slots, max_rows, FQA_PRE_TILE_Q);
+    prefix_ = dec_prefix_pages > 0;
+    dpre_cap_ = prefix_ ? dec_pre_cap : 0;
     cfg_ = {max_rows, max_blocks_, pool_pages, dec_grid_waves, dec_min_pages, dec_cap_, FQA_PRE_TILE_Q,
-            pre_cap_, dec_share ? 1 : 0};
+            pre_cap_, dec_share ? 1 : 0, prefix_ ? dec_prefix_pages : 0, dpre_cap_};
     computed_ = DeviceBuffer<int32_t>(slots);
     n_new_ = DeviceBuffer<int32_t>(slots);
     bt_off_ = DeviceBuffer<int32_t>(slots + 1);
@@ -99,7 +105,13 @@ class StepContext {
     items_ = DeviceBuffer<int32_t>((size_t)pre_cap_ * 4);
     meta_ = DeviceBuffer<int32_t>(FQA_META_LEN);
     nreq_ = DeviceBuffer<int32_t>(1);
-    ws_ = DeviceBuffer<unsigned char>((size_t)fqa_decode_workspace_bytes(&dims_, dec_cap_));
+    if (prefix_) {
+      dprefix_ = DeviceBuffer<int32_t>((size_t)std::max(slots, 1) * 8);
+      dpre_items_ = DeviceBuffer<int32_t>((size_t)std::max(dpre_cap_, 1) * 12);
+    }
+    ws_ = DeviceBuffer<unsigned char>(
+        (size_t)(prefix_ ? fqa_decode_prefix_workspace_bytes(&dims_, dec_cap_, dpre_cap_)
+                         : fqa_decode_workspace_bytes(&dims_, dec_cap_)));
     std::vector<float> c((size_t)max_ctx * 64), s((size_t)max_ctx * 64);
     Check(fqa_rope_tables(max_ctx, 128, 1.0e6f, c.data(), s.data()), "fqa_rope_tables");
     cos_ = DeviceBuffer<float>(c.size());
@@ -165,9 +177,7 @@ class StepContext {
                                  pool_pages_, 0, stream),
           "fqa_qknorm_rope_append");
     if (side) Fork(stream, side);
-    Check(fqa_decode(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_, dwaves_.D(),
-                     dseqs_.D(), meta_.D(), dec_cap_, slots_, ws_.D(), out, side ? side : stream),
-          "fqa_decode");
+    Decode(qkv, pool_layer, out, slots_, side ? side : stream);
     Check(fqa_prefill(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_, cu_.D(),
                       pos_.D(), items_.D(), meta_.D(), FQA_PRE_TILE_Q, pre_cap_, out, stream),
           "fqa_prefill");
@@ -198,9 +208,7 @@ class StepContext {
   void AttnDecode(const uint16_t* qkv, const uint16_t* pool_layer, uint16_t* out,
                   hipStream_t stream) const {
     if (!has_decode_) return;
-    Check(fqa_decode(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_, dwaves_.D(),
-                     dseqs_.D(), meta_.D(), dec_cap_, n_reqs_, ws_.D(), out, stream),
-          "fqa_decode");
+    Decode(qkv, pool_layer, out, n_reqs_, stream);
   }
   // LaunchAttnPrefillCute.
   void AttnPrefill(const uint16_t* qkv, const uint16_t* pool_layer, uint16_t* out,
@@ -242,6 +250,19 @@ class StepContext {
   }
 
  private:
+  // fqa_decode, or fqa_decode_prefix when the context plans shared-prefix groups
+  void Decode(const uint16_t* qkv, const uint16_t* pool_layer, uint16_t* out, int n_reqs_bound,
+              hipStream_t stream) const {
+    if (prefix_)
+      Check(fqa_decode_prefix(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_,
+                              dwaves_.D(), dseqs_.D(), dprefix_.D(), dpre_items_.D(), meta_.D(),
+                              dec_cap_, dpre_cap_, n_reqs_bound, ws_.D(), out, stream),
+            "fqa_decode_prefix");
+    else
+      Check(fqa_decode(&dims_, qkv, pool_layer, pool_pages_, bt_.D(), max_blocks_, dwaves_.D(),
+                       dseqs_.D(), meta_.D(), dec_cap_, n_reqs_bound, ws_.D(), out, stream),
+            "fqa_decode");
+  }
   // side starts after everything queued on stream so far; stream continues after side.
   // Events record and wait only (capture-safe).
   void Fork(hipStream_t stream, hipStream_t side) const {
@@ -255,12 +276,15 @@ class StepContext {
 
   fqa_pack_out PackOut() const {
     return fqa_pack_out{cu_.D(), qlen_.D(), pos_.D(), req_.D(), slot_.D(), bt_.D(),
-                        drids_.D(), prids_.D(), dseqs_.D(), dwaves_.D(), items_.D(), meta_.D()};
+                        drids_.D(), prids_.D(), dseqs_.D(), dwaves_.D(), items_.D(), meta_.D(),
+                        prefix_ ? dprefix_.D() : nullptr, prefix_ ? dpre_items_.D() : nullptr};
   }
 
   int max_rows_, slots_, max_ctx_, max_blocks_ = 0;
   int64_t pool_pages_;
   int dec_cap_ = 0, pre_cap_ = 0, n_reqs_ = 0, rows_ = 0;
+  bool prefix_ = false;  // shared-prefix decode groups (dec_prefix_pages > 0)
+  int dpre_cap_ = 0;
   bool has_decode_ = false, has_prefill_ = false;
   fqa_dims dims_{};
   fqa_pack_cfg cfg_{};
@@ -268,7 +292,7 @@ class StepContext {
   int32_t h_nreq_ = 0;  // host copy the request-count upload reads (kept until the copy ran)
   DeviceBuffer<int32_t> computed_, n_new_, bt_off_, bt_pages_;
   DeviceBuffer<int32_t> cu_, qlen_, pos_, req_, slot_, bt_, drids_, prids_, dseqs_, dwaves_, items_,
-      meta_, nreq_;
+      meta_, nreq_, dprefix_, dpre_items_;
   DeviceBuffer<unsigned char> ws_;
   DeviceBuffer<float> cos_, sin_;
   hipEvent_t fork_ = nullptr, join_ = nullptr;

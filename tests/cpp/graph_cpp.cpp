@@ -7,7 +7,8 @@
 //
 // With the environment variable FQA_DEC_SHARE=1 both runs build the context with dec_share
 // (the pack plans a mixed batch's decode for the CUs the concurrent prefill leaves) and the
-// eager run also puts decode on the side stream.
+// eager run also puts decode on the side stream.  FQA_DEC_PREFIX=N builds both with
+// dec_prefix_pages N (decodes sharing at least N leading pages attend them once per group).
 //
 // argv: script norm_weights [out];  script as tests/cpp/serve_cpp.cpp.  Prints
 // "steps S layers L compared N mismatched M" and exits 0 iff M == 0.  With `out`, the
@@ -71,6 +72,8 @@ int main(int argc, char** argv) {
   constexpr int kLayers = 3;
   const char* share_env = std::getenv("FQA_DEC_SHARE");
   const bool dec_share = share_env && share_env[0] == '1';
+  const char* prefix_env = std::getenv("FQA_DEC_PREFIX");
+  const int dec_prefix = prefix_env ? std::atoi(prefix_env) : 0;
   long long compared = 0, mismatched = 0;
   int steps_run = 0;
   try {
@@ -85,7 +88,7 @@ int main(int argc, char** argv) {
     std::vector<uint16_t> eager_pools;
 
     for (int mode = 0; mode < 2; ++mode) {
-      fqa::StepContext ctx(budget, n_slots, max_ctx, n_blocks, 0, 0, 8, dec_share);
+      fqa::StepContext ctx(budget, n_slots, max_ctx, n_blocks, 0, 0, 8, dec_share, dec_prefix);
       std::vector<fqa::DeviceBuffer<uint16_t>> pool, qkv, out;
       std::vector<fqa::LayerBuffers> lb;
       for (int l = 0; l < kLayers; ++l) {

@@ -23,10 +23,12 @@ EXE = Path(__file__).resolve().parent / "cpp" / "graph_cpp"
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("dec_share", [0, 1])
-def test_step_graph_replays_match_eager(gpu, tmp_path, dec_share):
+@pytest.mark.parametrize("dec_share,dec_prefix", [(0, 0), (1, 0), (0, 2)])
+def test_step_graph_replays_match_eager(gpu, tmp_path, dec_share, dec_prefix):
     """dec_share=1: both runs plan each mixed batch's decode for the CUs the prefill leaves,
-    and the eager run also queues decode on the side stream."""
+    and the eager run also queues decode on the side stream.  dec_prefix=2: decodes sharing
+    at least 2 leading pages (the prefix-cache hits on the common 70-token prompt start)
+    attend them once per group (fqa_decode_prefix), in the graph and eagerly."""
     if not EXE.exists():
         pytest.fail(f"{EXE} not built (run __graft_entry__.build())")
     rng = np.random.default_rng(78)
@@ -41,8 +43,8 @@ def test_step_graph_replays_match_eager(gpu, tmp_path, dec_share):
     wq, wk = synth.norm_weights()
     np.concatenate([wq.astype(np.float32), wk.astype(np.float32)]).tofile(tmp_path / "w.bin")
     print(f"[test_step_graph_replays_match_eager] 10 seqs, 16 steps, 3 layers, "
-          f"dec_share={dec_share}", flush=True)
-    env = dict(os.environ, FQA_DEC_SHARE=str(dec_share))
+          f"dec_share={dec_share} dec_prefix={dec_prefix}", flush=True)
+    env = dict(os.environ, FQA_DEC_SHARE=str(dec_share), FQA_DEC_PREFIX=str(dec_prefix))
     r = subprocess.run([str(EXE), str(tmp_path / "s.txt"), str(tmp_path / "w.bin"),
                         str(tmp_path / "graph.bin")], capture_output=True, text=True,
                        timeout=120, env=env)
@@ -63,7 +65,7 @@ def test_step_graph_replays_match_eager(gpu, tmp_path, dec_share):
         return a
 
     pools = [np.zeros(sc.pool_elems(n_blocks), np.uint16) for _ in range(layers)]
-    n_checked = shared = 0
+    n_checked = shared = grouped = 0
     # the decode grid StepContext takes by default: one wavefront per SIMD
     grid = 4 * torch.cuda.get_device_properties(gpu).multi_processor_count
     while o < raw.size:
@@ -77,12 +79,16 @@ def test_step_graph_replays_match_eager(gpu, tmp_path, dec_share):
         tables = [pages[off[i]:off[i + 1]] for i in range(R)]
         cfg = synth._assemble(f"step{t}", computed, n_new, tables, n_blocks, 512)
         kw = sc.pack_kwargs(cfg, max_rows=budget, dec_grid_waves=grid, dec_min_pages=8,
-                            max_reqs=slots, dec_share=dec_share)
+                            max_reqs=slots, dec_share=dec_share, dec_prefix_pages=dec_prefix,
+                            dec_pre_cap=4096)
         for l, (qkv_in, attn) in enumerate(per_layer):
             ref = sc.oracle_chain(cfg, qkv_in, pools[l], wq, wk, kw)
             if l == 0:
-                # rows, decode and prefill counts, and the decode plan's wavefront count
+                # rows, decode and prefill counts, the decode plan's wavefront count, and
+                # its prefix items and groups
                 assert meta[:5].tolist() == ref["pack"]["meta"][:5].tolist(), t
+                assert meta[10:12].tolist() == ref["pack"]["meta"][10:12].tolist(), t
+                grouped += int(meta[11]) > 0
                 if dec_share:  # steps whose plan the share changed
                     from oracle import oracle as orc
                     whole = orc.pack(cfg.computed, cfg.n_new, cfg.bt_off, cfg.bt_pages,
@@ -97,4 +103,6 @@ def test_step_graph_replays_match_eager(gpu, tmp_path, dec_share):
     assert n_checked == steps * layers
     # (this workload's batches are small: the share rarely moves their plans; config 4's
     # binding share is checked in test_gpu_path.py::test_mixed_step_decode_on_side_stream)
-    print(f"steps whose decode plan the share changed: {shared}")
+    print(f"steps whose decode plan the share changed: {shared}; with prefix groups: {grouped}")
+    if dec_prefix:
+        assert grouped > 0  # the groups were exercised
