@@ -460,26 +460,31 @@ def _random_step(seed: int):
 @pytest.mark.parametrize("seed", range(6))
 def test_random_steps(gpu, seed):
     """Random mixed steps (decode contexts, prefill prefixes and chunk lengths, shared
-    prefix pages, decode grid 16-2048 waves, minimum pages per wave, prefill tile) end to
-    end and kernel-only against the oracle; decode rows within one bf16 step."""
+    prefix pages, decode grid 16-2048 waves, minimum pages per wave, prefill tile, the
+    decode planned for a share of the CUs, shared-prefix decode groups) end to end and
+    kernel-only against the oracle; decode rows within one bf16 step."""
     cfg = _random_step(seed)
     rng = np.random.default_rng(1000 + seed)
     waves = int(rng.choice([16, 256, 1024, 2048]))
     min_pages = int(rng.choice([1, 2, 8]))
     tile = int(rng.choice([32, 64]))
+    prefix = (0, 1, 2)[seed % 3]
     print(f"[test_random_steps] seed={seed} reqs={cfg.n_reqs} rows={cfg.rows} "
-          f"waves={waves} min_pages={min_pages} tile={tile}", flush=True)
+          f"waves={waves} min_pages={min_pages} tile={tile} dec_share={seed % 2} "
+          f"dec_prefix_pages={prefix}", flush=True)
     kw = sc.pack_kwargs(cfg, dec_grid_waves=waves, dec_min_pages=min_pages, pre_tile_q=tile,
-                        dec_share=seed % 2)
+                        dec_share=seed % 2, dec_prefix_pages=prefix, dec_pre_cap=4096)
     _check_step(cfg, cfg, dict(kw, device=gpu), 500 + seed, f"random{seed}")
 
 
 @pytest.mark.gpu
-def test_decode_at_maximum_requests(gpu):
+@pytest.mark.parametrize("prefix", [0, 1])
+def test_decode_at_maximum_requests(gpu, prefix):
     """FQA_MAX_REQS (2048) decode sequences of 1-200 keys on the default 1024-wave grid: each
     wave walks many short streams (its segment loop reloads q and restarts the page
     rotation per stream), the combine runs on its largest grid, and some sequences share
-    their first pages.  End to end and kernel-only against the oracle."""
+    their first pages (prefix=1: those form shared-prefix groups).  End to end and
+    kernel-only against the oracle."""
     from flashqwen_amd import _lib
 
     rng = np.random.default_rng(4096)
@@ -499,8 +504,10 @@ def test_decode_at_maximum_requests(gpu):
             t[:k] = tabs[src][:k]
         tabs.append(t)
     cfg = synth._assemble("max-reqs", L - 1, np.ones(R, np.int32), tabs, pool, 4096)
-    print(f"[test_decode_at_maximum_requests] R={R} keys={int(L.sum())}", flush=True)
-    kw = sc.pack_kwargs(cfg, dec_grid_waves=1024, dec_min_pages=1)
+    print(f"[test_decode_at_maximum_requests] R={R} keys={int(L.sum())} prefix={prefix}",
+          flush=True)
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=1024, dec_min_pages=1, dec_prefix_pages=prefix,
+                        dec_pre_cap=4096)
     _check_step(cfg, cfg, dict(kw, device=gpu), 2048, "max-reqs")
 
 
