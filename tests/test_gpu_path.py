@@ -268,6 +268,37 @@ def test_pages_outside_pool_read_as_zeros(gpu):
 
 
 @pytest.mark.gpu
+def test_prefix_groups_with_pages_outside_pool(gpu):
+    """A shared-prefix group whose common leading pages include one past the pool's end
+    and one negative id: the pack flags the batch (status 4) and still plans the group,
+    the prefix items read those pages as zeros, as every member's own stream would, and
+    the decode rows match the oracle's."""
+    rng = np.random.default_rng(77)
+    pool_pages = 4096
+    perm = iter(rng.permutation(pool_pages).astype(np.int32).tolist())
+    run = [next(perm) for _ in range(20)]
+    run[6] = pool_pages + 11
+    run[13] = -5
+    comp, nnew, tabs = [], [], []
+    for i in range(6):
+        c = int(rng.integers(20 * PAGE, 20 * PAGE + 300))
+        nb = synth.cdiv(c + 1, PAGE)
+        tabs.append(np.array(run + [next(perm) for _ in range(nb - 20)], np.int32))
+        comp.append(c)
+        nnew.append(1)
+    cfg = synth._assemble("prefix-bad-pages", comp, nnew, tabs, pool_pages, 4096)
+    print("[test_prefix_groups_with_pages_outside_pool] 6 decodes on a 20-page shared run",
+          flush=True)
+    kw = sc.pack_kwargs(cfg, dec_grid_waves=64, dec_min_pages=2, dec_prefix_pages=2,
+                        dec_pre_cap=4096)
+    from oracle import oracle as orc
+    kwp = {k: v for k, v in kw.items() if k != "device"}
+    pk = orc.pack(cfg.computed, cfg.n_new, cfg.bt_off, cfg.bt_pages, **kwp)
+    assert int(pk["meta"][7]) == 4 and int(pk["meta"][11]) == 1  # flagged, one group
+    _check_step(cfg, cfg, dict(kw, device=gpu), 177, "prefix-bad-pages")
+
+
+@pytest.mark.gpu
 def test_mixed_step_decode_on_side_stream(gpu):
     """Config 4 with the decode on a second stream, concurrent with the prefill: the output
     and the pool are bit-identical to the one-stream step (the two write disjoint rows).
