@@ -448,7 +448,7 @@ def run_config(args, config, *, steps, warmup, with_cpu):
         "config": {"workload": f"config{config}: {_describe(config)}",
                    "rows_per_step": T, "requests": int(len(n_sel)), "layers": layers,
                    "pool_pages_per_layer": cfg.pool_pages, "head_shape": "32q/8kv/128",
-                   "dec_wave_runs": int(meta[6]), "dec_waves": int(meta[4]),
+                   "dec_wave_cost": int(meta[6]), "dec_waves": int(meta[4]),
                    "pre_items": int(meta[5]), "dec_prefix_pages": prefix_pages},
         "roofline": roof,
         "kernels_us": {k: round(v * 1e3, 2) for k, v in kern_ms.items()},

@@ -543,22 +543,26 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_read_floor_k
 
 // Log-sum-exp merge of a cut stream's partials (attn_cute.cu:225-238): one wave per
 // (decode sequence, kv head) stream, lane -> (head = lane/16, 8 dims).  A shared-prefix
-// member's stream is always merged: its group's C prefix chunk partials, then its own.  The shares that
-// hold stream s's page positions [F, S1) are w_first..w_last (share w = [w*W/G,
-// (w+1)*W/G)); the stream is the last of w_first's streams (slot 2w+1), or its first
-// (slot 2w) when w_first's share starts in s's own cost span [S0, F], and the first of
-// every later share (slot 2w).
+// member's stream is always merged: its group's C prefix chunk partials, then its own.
+// Stream s's pages take positions [F, S1), u per page, and a page belongs to the share
+// holding its last position: the shares w_first..w_last (share w = [w*W/G, (w+1)*W/G))
+// hold F + u - 1 and S1 - 1.  The stream is the last of w_first's streams (slot 2w+1), or
+// its first (slot 2w) when w_first's share starts in s's own cost span [S0, F + u), and
+// the first of every later share (slot 2w).
 __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_combine_kernel(DecArgs a) {
   const int wave = blockIdx.x * kDecWavesPerBlock + (threadIdx.x >> 6);
   const int di = wave >> 3, kvh = wave & 7;
   // di < n_reqs_bound, the rows of `seqs`: the sequence is read with the counts (one round
   // trip, not two)
   const int4 sq = *reinterpret_cast<const int4*>(a.seqs + 4 * (long long)di);
+  // the next sequence's cost start (the grid has 8 waves per row of `seqs`)
+  const int nb = gridDim.x * kDecWavesPerBlock / kHkv;
+  const int w_next = a.seqs[4 * (long long)min(di + 1, nb - 1) + 3];
   const int4 pinfo = a.prefix ? *reinterpret_cast<const int4*>(a.prefix + 8LL * di)
                               : make_int4(0, 0, 0, 0);
   const int pfx = pinfo.x;
   const int n_dec = a.meta[FQA_META_N_DECODE];
-  asm volatile("" ::"v"(sq.x), "v"(pfx), "s"(n_dec));
+  asm volatile("" ::"v"(sq.x), "v"(pfx), "v"(w_next), "s"(n_dec));
   if (di >= n_dec) return;
   const long long G = a.meta[FQA_META_DEC_WAVES];
   // the plan's cost positions (fqa.h): each stream's start positions, then its pages
@@ -566,9 +570,14 @@ __global__ void __launch_bounds__(kDecWavesPerBlock * kWave) decode_combine_kern
   // a stream's pages: [P, pages) with a shared prefix
   const int pages = ((sq.z & FQA_DEC_KEYS_MASK) + kPage - 1) / kPage - pfx;
   const int sc = FQA_DEC_STREAM_COST + (pfx > 0 ? FQA_DEC_PREFIX_STREAM_COST : 0);
-  const long long S0 = sq.w + (long long)kvh * (pages + sc);
-  const long long F = S0 + sc, S1 = F + pages;  // page positions [F, S1)
-  const long long wf = ((F + 1) * G - 1) / W, wl = (S1 * G - 1) / W;
+  // the stream's cost, 1/8 of the sequence's span, gives its page cost u
+  const long long c = ((di + 1 < n_dec ? (long long)w_next : W) - sq.w) / kHkv;
+  const int u = (int)((c - sc) / pages);
+  const long long S0 = sq.w + (long long)kvh * c;
+  const long long F = S0 + sc, S1 = F + (long long)pages * u;  // page positions [F, S1)
+  // a page belongs to the share holding its last position: the first page's is F + u - 1,
+  // the last page's S1 - 1
+  const long long wf = ((F + u) * G - 1) / W, wl = (S1 * G - 1) / W;
   // a stream finished by one wavefront is final, unless a shared prefix precedes it
   if (wf == wl && pfx == 0) return;
   if (pfx > 0 && !prefix_fits(pinfo, a.pre_cap)) return;

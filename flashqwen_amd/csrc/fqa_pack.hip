@@ -166,8 +166,8 @@ __device__ int dec_share_waves(int N, long long dpages, unsigned long long keyro
 }
 
 // A decode stream's start in the plan's cost units (fqa.h): FQA_DEC_STREAM_COST, plus
-// FQA_DEC_PREFIX_STREAM_COST for a shared-prefix member (it merges its group's partials
-// first).
+// FQA_DEC_PREFIX_STREAM_COST for a shared-prefix member (its stream always leaves a
+// partial for the combine).
 __host__ __device__ constexpr int stream_start_cost(int prefix_pages) {
   return FQA_DEC_STREAM_COST + (prefix_pages > 0 ? FQA_DEC_PREFIX_STREAM_COST : 0);
 }
@@ -375,7 +375,8 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   __shared__ int s_prer[FQA_MAX_REQS];        // by prefill index: request
   __shared__ int s_pit[FQA_MAX_REQS + 1];     // by prefill index: first item
   __shared__ int s_hkey[kHashSlots];          // first page ids of decode sequences
-  __shared__ int s_hcnt[kHashSlots];          // ... and how many sequences start there
+  __shared__ int s_hcnt[kHashSlots / 2];      // ... how many sequences start there (16 bits)
+  __shared__ int s_hmin[kHashSlots];          // ... and the first of them (decode index)
   __shared__ Stats s_stats[kPackWaves];
   __shared__ Counts s_counts[kPackWaves];
   __shared__ int sh32[kPackWaves];
@@ -390,7 +391,8 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   // the shared-prefix hash starts empty (published by the scan's barriers)
   for (int i = tid; i < kHashSlots; i += kPackThreads) {
     s_hkey[i] = -1;
-    s_hcnt[i] = 0;
+    if (i < kHashSlots / 2) s_hcnt[i] = 0;
+    s_hmin[i] = INT_MAX;
   }
   if (tid == 0) s_keyrows = 0;
 
@@ -435,8 +437,9 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       v.v[1] = n == 1;
       v.v[2] = n != 1;
       // a decode stream's cost in the plan: its pages plus the per-stream overhead (more
-      // for a shared-prefix member, which starts from its group's partials), and its pages
-      v.v[3] = n == 1 ? c / kPage + 1 - pfx + stream_start_cost(pfx) : 0;
+      // for a shared-prefix member), and its pages; the shared sequences' cheaper pages
+      // are taken off once the flags are known
+      v.v[3] = n == 1 ? (c / kPage + 1 - pfx) * FQA_DEC_PAGE_COST + stream_start_cost(pfx) : 0;
       v.v[5] = n == 1 ? c / kPage + 1 - pfx : 0;
       v.v[4] = n != 1 ? (n + QT - 1) / QT : 0;
     }
@@ -472,10 +475,9 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     for (int k = 0; k < kCounts; ++k) carry.v[k] += tot.v[k];
   }
   const int nd = carry.v[1], np = carry.v[2], npi = carry.v[4];
-  // decode plan: W = 8 x (stream pages + FQA_DEC_STREAM_COST per stream) cost units cut
-  // into G equal shares
+  // decode plan: W = 8 x (stream costs) cost units cut into G equal shares
   const int dpages = st.v[2];
-  const long long W = 8LL * carry.v[3];
+  long long W = 8LL * carry.v[3];
   if (tid == 0) {
     s_btoff[R] = bt_end;
     s_qstart[R] = carry.v[0];
@@ -495,13 +497,75 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       a.o.meta[tid] = tid == FQA_META_STATUS ? code : (tid == FQA_META_REQS ? R : 0);
     return;
   }
+  // ---- decode sequences whose first page starts another decode sequence too (a shared
+  // prefix): FQA_DEC_SHARED in their n_keys fields.  Page ids are hashed into LDS. -------
+  auto slot_of = [](int id) { return (int)(((uint32_t)id * 2654435761u) >> 20) & (kHashSlots - 1); };
+  if (nd > 1) {
+    for (int d = tid; d < nd; d += kPackThreads) {
+      const int id = s_dflag[d];
+      if (id < 0) continue;  // not a page (flagged by the range check): never shared
+      int h = slot_of(id);
+      for (int probe = 0; probe < kHashSlots; ++probe, h = (h + 1) & (kHashSlots - 1)) {
+        const int prev = atomicCAS(&s_hkey[h], -1, id);
+        if (prev == -1 || prev == id) {
+          atomicAdd(&s_hcnt[h >> 1], 1 << (16 * (h & 1)));  // counts <= 2048
+          atomicMin(&s_hmin[h], d);
+          break;
+        }
+      }
+    }
+    lds_sync();
+  }
+  // kCheap (beside FQA_DEC_SHARED in s_dflag, never stored): a shared sequence that is not
+  // the first with its first page; its pages cost FQA_DEC_SHARED_PAGE_COST in the plan
+  constexpr int kCheap = 1 << 29;
+  for (int d = tid; d < nd; d += kPackThreads) {
+    const int id = s_dflag[d];
+    int shared = 0, first = d;
+    if (id >= 0 && nd > 1) {
+      int h = slot_of(id);
+      for (int probe = 0; probe < kHashSlots; ++probe, h = (h + 1) & (kHashSlots - 1))
+        if (s_hkey[h] == id) {
+          shared = ((s_hcnt[h >> 1] >> (16 * (h & 1))) & 0xFFFF) > 1;
+          first = s_hmin[h];
+          break;
+        }
+    }
+    // a group member's streams cover its own pages: no flag
+    const bool fl = shared && s_dpfx[d] == 0;
+    s_dflag[d] = fl ? (FQA_DEC_SHARED | (first != d ? kCheap : 0)) : 0;
+  }
+  // the cheap sequences' pages cost FQA_DEC_SHARED_PAGE_COST: take the difference off the
+  // cost prefix (each thread rescans its own decode indices, which it flagged above)
+  bool any_cheap = false;
+  for (int d = tid; d < nd; d += kPackThreads) any_cheap |= (s_dflag[d] & kCheap) != 0;
+  if (__syncthreads_or(any_cheap)) {
+    int off = 0;
+    for (int base = 0; base < nd; base += kPackThreads) {
+      const int d = base + tid;
+      const int v = d < nd && (s_dflag[d] & kCheap)
+                        ? s_dpages[d] * (FQA_DEC_PAGE_COST - FQA_DEC_SHARED_PAGE_COST) : 0;
+      int tot;
+      const int e = block_excl_scan(v, sh32, &tot);
+      if (d < nd) s_dstart[d] -= 8 * (off + e);
+      off += tot;
+    }
+    W -= 8LL * off;
+    if (tid == 0) s_dstart[nd] = (int)W;
+    lds_sync();
+  }
+
+
   const int T = rows;
   const int gtid = blockIdx.x * kPackThreads + tid;
   const int gsz = gridDim.x * kPackThreads;
   int G = 0;
   if (W > 0) {
     const int minp = a.c.dec_min_pages > 0 ? a.c.dec_min_pages : 1;
-    G = (int)min((long long)a.c.dec_grid_waves, (W + minp - 1) / minp);
+    // shares of at least FQA_DEC_PAGE_COST * minp units: each holds the last position of
+    // a page of every stream it crosses
+    const long long unit = (long long)FQA_DEC_PAGE_COST * minp;
+    G = (int)min((long long)a.c.dec_grid_waves, (W + unit - 1) / unit);
     if (a.c.dec_share)  // CUs shared with a concurrent prefill (fqa.h)
       G = min(G, dec_share_waves(a.c.dec_grid_waves, dpages, s_keyrows));
   }
@@ -519,7 +583,8 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
     p = s_comp[r] + (t - s_qstart[r]);
   };
   // Cost position x lies in stream (d, h) at offset off: the stream's first
-  // FQA_DEC_STREAM_COST positions are its overhead, then one per page.  Pages before x:
+  // stream_start_cost positions are its overhead, then u per page (fqa.h).  Pages whose
+  // last position is below x:
   auto locate = [&](int x, int& d, int& h, int& skip) {
     d = upper_index(s_dstart, nd, x);
     if (d >= nd) {  // x == W
@@ -527,9 +592,10 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       return dpages * 8;
     }
     const int sc = stream_start_cost(s_dpfx[d]);
-    const int rem = x - s_dstart[d], cost = s_dpages[d] + sc;
+    const int u = (s_dflag[d] & kCheap) ? FQA_DEC_SHARED_PAGE_COST : FQA_DEC_PAGE_COST;
+    const int rem = x - s_dstart[d], cost = s_dpages[d] * u + sc;
     h = rem / cost;
-    skip = max(0, rem % cost - sc);  // pages of stream (d, h) before x
+    skip = max(0, rem % cost - sc) / u;  // pages of stream (d, h) before x
     return s_dpst[d] + h * s_dpages[d] + skip;
   };
   auto wave_of = [&](int w, int& di, int& kvh, int& page, int& n, int& r) {
@@ -552,7 +618,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   auto store_wave = [&](int w, int di, int kvh, int page, int n, int r, int id) {
     int4* dst = reinterpret_cast<int4*>(a.o.dec_waves + 8 * (long long)w);
     dst[0] = make_int4(di, kvh, page, n);
-    dst[1] = make_int4(r, s_qstart[r], (s_comp[r] + 1) | s_dflag[di], id);
+    dst[1] = make_int4(r, s_qstart[r], (s_comp[r] + 1) | (s_dflag[di] & FQA_DEC_SHARED), id);
   };
   const int bt_total = R * maxb;  // < 2^31: R <= 2048, max_blocks <= 2^19
   int r0 = 0, p0 = 0, page0 = 0, di1 = 0, kvh1 = 0, pg1 = 0, n1 = 0, r1 = 0, id1 = 0, bt0 = -1;
@@ -590,38 +656,6 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
       pgv[u] = pgv_src[max(min(u * kPackThreads + tid, pg_nvec - 1), 0)];
     pg_head_id = pg[min(tid, npages - 1)];
     pg_tail_id = pg[max(min(pg_lead + 4 * pg_nvec + tid, npages - 1), 0)];
-  }
-
-  // ---- decode sequences whose first page starts another decode sequence too (a shared
-  // prefix): FQA_DEC_SHARED in their n_keys fields.  Page ids are hashed into LDS. -------
-  auto slot_of = [](int id) { return (int)(((uint32_t)id * 2654435761u) >> 20) & (kHashSlots - 1); };
-  if (nd > 1) {
-    for (int d = tid; d < nd; d += kPackThreads) {
-      const int id = s_dflag[d];
-      if (id < 0) continue;  // not a page (flagged by the range check): never shared
-      int h = slot_of(id);
-      for (int probe = 0; probe < kHashSlots; ++probe, h = (h + 1) & (kHashSlots - 1)) {
-        const int prev = atomicCAS(&s_hkey[h], -1, id);
-        if (prev == -1 || prev == id) {
-          atomicAdd(&s_hcnt[h], 1);
-          break;
-        }
-      }
-    }
-    lds_sync();
-  }
-  for (int d = tid; d < nd; d += kPackThreads) {
-    const int id = s_dflag[d];
-    int shared = 0;
-    if (id >= 0 && nd > 1) {
-      int h = slot_of(id);
-      for (int probe = 0; probe < kHashSlots; ++probe, h = (h + 1) & (kHashSlots - 1))
-        if (s_hkey[h] == id) {
-          shared = s_hcnt[h] > 1;
-          break;
-        }
-    }
-    s_dflag[d] = shared && s_dpfx[d] == 0 ? FQA_DEC_SHARED : 0;  // a group member's own pages
   }
 
   // ---- prefill items, sorted by key count descending (stable) --------------------
@@ -688,7 +722,7 @@ __global__ void __launch_bounds__(kPackThreads) pack_kernel(PackArgs a) {
   for (int di = gtid; di < nd; di += gsz) {
     const int r = s_drid[di];
     *reinterpret_cast<int4*>(a.o.dec_seqs + 4 * (long long)di) =
-        make_int4(r, s_qstart[r], (s_comp[r] + 1) | s_dflag[di], s_dstart[di]);
+        make_int4(r, s_qstart[r], (s_comp[r] + 1) | (s_dflag[di] & FQA_DEC_SHARED), s_dstart[di]);
   }
 
   if (blockIdx.x != 0) return;

@@ -72,13 +72,21 @@ extern "C" {
 #define FQA_DEC_SHARED (1 << 30)
 #define FQA_DEC_KEYS_MASK (FQA_DEC_SHARED - 1)
 #define FQA_MAX_REQS 2048 /* max requests in one step (reference: `slots`, args.h:13) */
-/* Cost of starting a decode stream in the stream-K plan, in page runs: each (sequence,
- * kv head) stream counts its pages plus this, so a wavefront whose share holds many short
- * streams gets fewer pages (a stream start costs a few dependent loads). */
-#define FQA_DEC_STREAM_COST 4
+/* Costs in the decode plan's stream-K cut, in cost units.  A page run costs
+ * FQA_DEC_PAGE_COST, or FQA_DEC_SHARED_PAGE_COST in a "cheap" sequence: one flagged
+ * FQA_DEC_SHARED that is not the first decode sequence (by decode index) with its first
+ * page (the first one's reads bring the shared pages into the caches; the others' pages
+ * then stream ~1.5x faster, measured on config 5). */
+#define FQA_DEC_PAGE_COST 8
+#define FQA_DEC_SHARED_PAGE_COST 5
+/* Cost of starting a decode stream: each (sequence, kv head) stream counts its pages plus
+ * this, so a wavefront whose share holds many short streams gets fewer pages (a stream
+ * start costs a few dependent loads; 4 page runs). */
+#define FQA_DEC_STREAM_COST 32
 /* ... and this more for a shared-prefix member's stream (dec_prefix_pages): such a stream
- * always leaves a partial for the combine (measured on config 5: 0, 2, 4 and 8 within 1%). */
-#define FQA_DEC_PREFIX_STREAM_COST 4
+ * always leaves a partial for the combine (measured on config 5: 0 to 8 page runs within
+ * 1%). */
+#define FQA_DEC_PREFIX_STREAM_COST 32
 /* Pages of a decode sequence compared with its group leader's for a shared prefix
  * (fqa_pack_cfg::dec_prefix_pages). */
 #define FQA_DEC_PREFIX_CAP 8192
@@ -91,7 +99,7 @@ enum {
   FQA_META_MAX_QLEN = 3,     /* max(1, max prefill qlen) (model_runtime.cu:82) */
   FQA_META_DEC_WAVES = 4,    /* decode wavefronts with work this step         */
   FQA_META_PRE_ITEMS = 5,    /* prefill work items (request, query tile)      */
-  FQA_META_DEC_WAVE_PAGES = 6, /* cost of a decode share (>= the pages it streams) */
+  FQA_META_DEC_WAVE_PAGES = 6, /* cost units of a decode share (ceil(W / G))       */
   FQA_META_STATUS = 7,       /* 0 or an FQA_PACK_* code                       */
   FQA_META_REQS = 8,         /* R                                             */
   FQA_META_DEC_PAGES = 9,    /* sum over decode sequences of their stream pages */
@@ -142,16 +150,17 @@ typedef struct fqa_batch {
  *
  * Decode plan (stream-K): the decode requests' (sequence, kv head) page streams are laid
  * end to end in cost units, stream (di, kvh) of pages[di] pages costing
- * c = pages[di] + s, s = FQA_DEC_STREAM_COST (+ FQA_DEC_PREFIX_STREAM_COST for a
+ * c = pages[di] * u + s, u = FQA_DEC_PAGE_COST (FQA_DEC_SHARED_PAGE_COST in a cheap
+ * sequence, above), s = FQA_DEC_STREAM_COST (+ FQA_DEC_PREFIX_STREAM_COST for a
  * shared-prefix member): it spans [X[di]*8 + kvh*c, + c), where pages = ceil(n_keys/16)
  * and X is the exclusive prefix of the costs over decode indices; the first s positions
- * of a stream stand for its start, the others for its pages in order.  The W = 8*sum(c)
- * positions (meta[FQA_META_DEC_COST]) are cut into G = min(dec_grid_waves,
- * ceil(W/dec_min_pages)) equal contiguous shares, share w = [floor(w*W/G),
- * floor((w+1)*W/G)), one per decode wavefront, which streams the pages whose positions
- * fall in it; dec_waves[w] = {di, kvh, page, n_runs, r, row, n_keys, page id} is the
- * stream and page it starts at (a share that starts in a stream's start positions starts
- * at its first page), how many pages it streams, the first stream's request, row and
+ * of a stream stand for its start, then page k takes positions [s + k*u, s + (k+1)*u).
+ * The W = 8*sum(c) positions (meta[FQA_META_DEC_COST]) are cut into G =
+ * min(dec_grid_waves, ceil(W / (FQA_DEC_PAGE_COST * dec_min_pages))) equal contiguous
+ * shares, share w = [floor(w*W/G), floor((w+1)*W/G)), one per decode wavefront (each at
+ * least FQA_DEC_PAGE_COST positions), which streams the pages whose last position falls
+ * in it; dec_waves[w] = {di, kvh, page, n_runs, r, row, n_keys, page id} is the stream
+ * and page it starts at, how many pages it streams, the first stream's request, row and
  * key count, and its first page (so a wavefront's first loads need no further lookups).
  * dec_seqs[di] = {r, row = qstart[r], n_keys = computed[r]+1,
  * 8*X[di]}.  The n_keys fields of both carry FQA_DEC_SHARED.  Prefill plan: one item

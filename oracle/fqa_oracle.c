@@ -30,12 +30,20 @@
 #define PAGE 16
 /* pages compared for a shared decode prefix (FQA_DEC_PREFIX_CAP, include/fqa.h) */
 #define FQA_DEC_PREFIX_CAP 8192
-/* per-stream start cost of the decode plan, in page runs (FQA_DEC_STREAM_COST, fqa.h) */
-#define FQA_DEC_STREAM_COST 4
-#define FQA_DEC_PREFIX_STREAM_COST 4
+/* costs of the decode plan in cost units (FQA_DEC_PAGE_COST ..., include/fqa.h): a page
+ * run, one in a sequence flagged shared, a stream's start, a shared-prefix member's */
+#define FQA_DEC_PAGE_COST 8
+#define FQA_DEC_SHARED_PAGE_COST 5
+#define FQA_DEC_STREAM_COST 32
+#define FQA_DEC_PREFIX_STREAM_COST 32
 /* a decode stream's start cost: more for a shared-prefix member */
 static int64_t stream_start_cost(int pfx) {
   return FQA_DEC_STREAM_COST + (pfx > 0 ? FQA_DEC_PREFIX_STREAM_COST : 0);
+}
+/* a page run's cost in a decode sequence (cheap: flagged FQA_DEC_SHARED and not the
+ * first decode sequence with its first page) */
+static int64_t page_cost(int cheap) {
+  return cheap ? FQA_DEC_SHARED_PAGE_COST : FQA_DEC_PAGE_COST;
 }
 
 float fqo_bf16_to_f32(uint16_t b) {
@@ -241,21 +249,42 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
       for (int di = 0; di < nd; ++di) pfx[di] = 0;
     }
   }
+  /* A decode sequence whose first page is also another decode sequence's first page
+   * (a shared prefix) is flagged shared (bit 30, FQA_DEC_SHARED in fqa.h, in both n_keys
+   * fields) unless it is a group member (its streams then cover its own pages); a
+   * negative id is never shared.  This build's load-hint and cost policy; the reference
+   * has no plan to restate here. */
+  /* dcheap: a shared sequence that is not the first (by decode index) with its first
+   * page, whose pages the plan prices at FQA_DEC_SHARED_PAGE_COST (the first one's reads
+   * bring them into the caches) */
+  int32_t* dshared = (int32_t*)calloc(nd > 0 ? nd : 1, sizeof(int32_t));
+  int32_t* dcheap = (int32_t*)calloc(nd > 0 ? nd : 1, sizeof(int32_t));
+  for (int a = 0; a < nd; ++a) {
+    const int32_t id = bt_pages[bt_off[decode_rids[a]]];
+    int sh = 0, first = a;
+    for (int b = 0; id >= 0 && b < nd; ++b)
+      if (b != a && bt_pages[bt_off[decode_rids[b]]] == id) {
+        sh = 1;
+        if (b < first) first = b;
+      }
+    dshared[a] = sh && pfx[a] == 0;
+    dcheap[a] = dshared[a] && first != a;
+  }
   /* decode plan (stream-K): the (decode sequence, kv head) page streams [P, pages) end to
-   * end in cost positions (FQA_DEC_STREAM_COST start positions, then one per page),
-   * W = 8 * (total stream pages + FQA_DEC_STREAM_COST per sequence) cut into G equal
-   * shares [w*W/G, (w+1)*W/G) */
+   * end in cost positions (the stream's start positions, then u per page, u =
+   * page_cost), W = 8 * sum of the stream costs, cut into G equal shares
+   * [w*W/G, (w+1)*W/G); a share takes the pages whose last position falls in it */
   int64_t total = 0, cost_total = 0;
   for (int di = 0; di < nd; ++di) {
     const int len = computed[decode_rids[di]] / PAGE + 1 - pfx[di];
     total += len;
-    cost_total += len + stream_start_cost(pfx[di]);
+    cost_total += (int64_t)len * page_cost(dcheap[di]) + stream_start_cost(pfx[di]);
   }
   int64_t W = 8 * cost_total;
   int minp = dec_min_pages > 0 ? dec_min_pages : 1;
   int G = 0;
   if (W > 0) {
-    int64_t gmax = (W + minp - 1) / minp;
+    int64_t gmax = (W + (int64_t)FQA_DEC_PAGE_COST * minp - 1) / ((int64_t)FQA_DEC_PAGE_COST * minp);
     G = (int)(dec_grid_waves < gmax ? dec_grid_waves : gmax);
     /* dec_share (this library's plan for a decode that runs beside the prefill, fqa.h):
      * D = 783 * decode pages, P = prefill key-rows */
@@ -295,6 +324,8 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
     meta[7] = 6;
     free(pfx);
     free(lead);
+    free(dshared);
+    free(dcheap);
     return 6;
   }
   {
@@ -305,10 +336,11 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
       dec_seqs[4 * di + 1] = cu_seqlens[r];
       dec_seqs[4 * di + 2] = computed[r] + 1;
       dec_seqs[4 * di + 3] = (int32_t)(8 * X);
-      X += pages + stream_start_cost(pfx[di]);
+      X += (int64_t)pages * page_cost(dcheap[di]) + stream_start_cost(pfx[di]);
     }
     /* Position x: the sequence, kv head and offset in the stream's cost span, and the
-     * pages at positions below x (every stream's pages come after its start positions). */
+     * pages whose last position is below x (every stream's pages come after its start
+     * positions). */
     int64_t* pstart = (int64_t*)malloc(sizeof(int64_t) * (nd + 1)); /* 8 * page prefix */
     pstart[0] = 0;
     for (int di = 0; di < nd; ++di)
@@ -322,7 +354,8 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
         int64_t start = 0;
         int d = 0;
         while (d < nd) {
-          const int64_t cost = computed[decode_rids[d]] / PAGE + 1 - pfx[d] + stream_start_cost(pfx[d]);
+          const int64_t cost = (int64_t)(computed[decode_rids[d]] / PAGE + 1 - pfx[d]) *
+                                   page_cost(dcheap[d]) + stream_start_cost(pfx[d]);
           if (x < start + 8 * cost) break;
           start += 8 * cost;
           ++d;
@@ -332,8 +365,9 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
           continue;
         }
         const int64_t len = computed[decode_rids[d]] / PAGE + 1 - pfx[d];
-        const int64_t sc = stream_start_cost(pfx[d]), cost = len + sc, rem = x - start;
-        const int64_t o = rem % cost, skip = o > sc ? o - sc : 0;
+        const int64_t u = page_cost(dcheap[d]);
+        const int64_t sc = stream_start_cost(pfx[d]), cost = len * u + sc, rem = x - start;
+        const int64_t o = rem % cost, skip = o > sc ? (o - sc) / u : 0;
         below[e] = pstart[d] + (rem / cost) * len + skip;
         di = d;
         kvh = (int)(rem / cost);
@@ -350,17 +384,8 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
       dec_waves[8 * w + 7] = bt_pages[bt_off[r] + page];
     }
     free(pstart);
-    /* A decode sequence whose first page is also another decode sequence's first page
-     * (a shared prefix) carries the shared flag (bit 30, FQA_DEC_SHARED in fqa.h) in both
-     * n_keys fields; a negative id is never shared.  This build's load-hint policy; the
-     * reference has no plan to restate here. */
-    for (int a = 0; a < nd; ++a) {
-      const int32_t id = bt_pages[bt_off[decode_rids[a]]];
-      int shared = 0;
-      for (int b = 0; id >= 0 && b < nd && !shared; ++b)
-        shared = b != a && bt_pages[bt_off[decode_rids[b]]] == id;
-      if (shared && pfx[a] == 0) dec_seqs[4 * a + 2] |= 1 << 30; /* members: own pages */
-    }
+    for (int a = 0; a < nd; ++a)
+      if (dshared[a]) dec_seqs[4 * a + 2] |= 1 << 30; /* (members: their own pages) */
     for (int w = 0; w < G; ++w) dec_waves[8 * w + 6] |= dec_seqs[4 * dec_waves[8 * w] + 2] & (1 << 30);
   }
   /* prefix items, groups by leader: for each kv head, chunk c of CP pages and octet q of
@@ -401,6 +426,8 @@ int fqo_pack(int R, const int32_t* computed, const int32_t* n_new, const int32_t
   }
   free(pfx);
   free(lead);
+  free(dshared);
+  free(dcheap);
   {
     int32_t* tmp = (int32_t*)malloc(sizeof(int32_t) * 4 * (npi > 0 ? npi : 1));
     int k = 0;

@@ -121,25 +121,40 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
         for members, P in group_list:
             for di in members:
                 prefix[di] = P
+    # decode sequences whose first page starts another decode sequence too (group members
+    # aside): FQA_DEC_SHARED (bit 30) in both n_keys fields, and a cheaper page cost
+    from collections import Counter
+    firsts = Counter(tables[r][0] for r in dec if tables[r][0] >= 0)
+    shared = [tables[r][0] >= 0 and firsts[tables[r][0]] > 1 and not prefix[di]
+              for di, r in enumerate(dec)]
+    # ... priced cheaper unless the first (by decode index) to start at its page
+    seen = set()
+    cheap = []
+    for di, r in enumerate(dec):
+        cheap.append(shared[di] and tables[r][0] in seen)
+        seen.add(tables[r][0])
     # decode stream-K plan: concatenate streams (di, kvh) over pages [prefix, pages), each
-    # preceded by STREAM_COST start positions (None: a position that streams no page), cut
-    # into G equal shares of positions
-    STREAM_COST, PREFIX_STREAM_COST = 4, 4  # a member's stream also merges its group's partials
+    # preceded by STREAM_COST start positions, a page taking PAGE_COST positions (5 in a
+    # cheap one) and marked at its last one (None: a position that marks no page);
+    # cut into G equal shares of positions, a share taking the pages marked in it
+    PAGE_COST, SHARED_PAGE_COST = 8, 5
+    STREAM_COST, PREFIX_STREAM_COST = 32, 32  # a member's stream always leaves a partial
     runs = []  # None or (di, kvh, page), for every cost position, in order
     seqs = []
     P = X = 0
     for di, r in enumerate(dec):
         pages = computed[r] // PAGE + 1
+        u = SHARED_PAGE_COST if cheap[di] else PAGE_COST
         seqs.append([r, res["cu_seqlens"][r], computed[r] + 1, 8 * X])
         start = STREAM_COST + (PREFIX_STREAM_COST if prefix[di] else 0)
         for kvh in range(8):
             runs.extend([None] * start)
             for pg in range(prefix[di], pages):
-                runs.append((di, kvh, pg))
+                runs.extend([None] * (u - 1) + [(di, kvh, pg)])
         P += pages - prefix[di]
-        X += pages - prefix[di] + start
+        X += (pages - prefix[di]) * u + start
     W = len(runs)
-    G = min(dec_grid_waves, _cdiv(W, max(1, dec_min_pages))) if W else 0
+    G = min(dec_grid_waves, _cdiv(W, PAGE_COST * max(1, dec_min_pages))) if W else 0
     # dec_share: a decode beside the prefill gets a multiple of 32 wavefronts in
     # [32, N - 32]: the largest g whose modelled prefill time P N / (N - g) is no more than
     # the decode's D (36 g + 25 N) / (50 g), or g + 32 when the prefill there ends before
@@ -161,7 +176,7 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
     waves = []
     for w in range(G):
         g0, g1 = w * W // G, (w + 1) * W // G
-        # a share that starts at a stream's start positions starts at its first page
+        # a share starts at the first page marked at or after its start
         di, kvh, pg = next(x for x in runs[g0:] if x is not None)
         r = dec[di]
         n = sum(x is not None for x in runs[g0:g1])
@@ -178,12 +193,6 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
         meta = [0] * 16
         meta[8], meta[7] = R, 6
         return {"meta": meta}
-    # decode sequences whose first page starts another decode sequence too: bit 30
-    # (FQA_DEC_SHARED) in both n_keys fields
-    from collections import Counter
-    firsts = Counter(tables[r][0] for r in dec if tables[r][0] >= 0)
-    shared = [tables[r][0] >= 0 and firsts[tables[r][0]] > 1 and not prefix[di]
-              for di, r in enumerate(dec)]
     for di, s in enumerate(seqs):
         s[2] |= (1 << 30) if shared[di] else 0
     for wv in waves:

@@ -415,16 +415,17 @@ def test_pack_prefix_known_answer():
     flag = 1 << 30
     seqs = got["dec_seqs"][:4]
     assert [int(z) for z in seqs[:, 2]] == [41, 48, 21, 71]  # no flags: groups read their own
-    # streams of 1, 1, 2, 3 pages cost 9, 9, 6, 11 positions (4 for a stream's start, 4
-    # more for a member's, which merges its group's partials first)
-    assert [int(z) for z in seqs[:, 3]] == [0, 72, 144, 192]
-    # W = 280 positions in 7 shares starting at 0, 40, 80, 120, 160, 200, 240:
-    # {di, kvh, page (absolute), pages streamed, page id}.  Share 1 starts in (0, 4)'s
-    # start positions; share 3 holds pages of (1, 5..7) and (2, 0..1).
+    # streams of 1, 1, 2, 3 pages cost 72, 72, 48, 88 positions (8 per page, 32 for a
+    # stream's start, 32 more for a member's); 8 streams per sequence
+    assert [int(z) for z in seqs[:, 3]] == [0, 576, 1152, 1536]
+    # W = 2240 positions in 7 shares starting at 0, 320, 640, ..., 1920; a page belongs to
+    # the share holding its last position: {di, kvh, page (absolute), pages streamed,
+    # page id}.  Share 1 starts in (0, 4)'s start positions; share 3 holds pages of
+    # (1, 5..7) and (2, 0..1).
     assert [list(map(int, w[:4])) + [int(w[7])] for w in got["dec_waves"][:7]] == [
         [0, 0, 2, 4, 7], [0, 4, 2, 4, 7], [1, 0, 2, 5, 9], [1, 5, 2, 7, 9],
         [2, 2, 0, 12, 8], [3, 0, 2, 12, 7], [3, 4, 2, 12, 7]]
-    assert int(m[12]) == 280
+    assert int(m[12]) == 2240 and int(m[6]) == 320
     off, _ = _compare_pack(comp, nnew, tabs, dict(kw, dec_prefix_pages=3))
     assert (int(off["meta"][9]), int(off["meta"][10]), int(off["meta"][11])) == (13, 0, 0)
     assert [bool(z & flag) for z in off["dec_seqs"][:4, 2]] == [True, True, False, True]
@@ -526,17 +527,43 @@ def test_pack_known_answer():
     assert got["block_tables"][:12].tolist() == [5, 9, -1, 2, 7, -1, 11, -1, -1, 4, -1, -1]
     assert got["decode_rids"][:4].tolist() == [0, 2, -1, -1]
     assert got["prefill_rids"][:4].tolist() == [1, 3, -1, -1]
-    assert got["meta"][:10].tolist() == [5, 2, 2, 3, 5, 1, 18, 0, 4, 3]
-    # streams of 2 and 1 pages cost 6 and 5 positions (4 for a stream's start):
-    # W = 8*(6+5) = 88 positions over 5 waves, shares from 0, 17, 35, 52, 70 holding 5, 6,
-    # 5, 4, 4 of the 24 page runs (share 4 starts in (1, 4)'s start positions)
-    assert got["dec_seqs"][:2].tolist() == [[0, 0, 18, 0], [2, 4, 1, 48]]
+    assert got["meta"][:10].tolist() == [5, 2, 2, 3, 5, 1, 141, 0, 4, 3]
+    # streams of 2 and 1 pages cost 48 and 40 positions (32 for a stream's start, 8 per
+    # page): W = 8*(48+40) = 704 positions over 5 waves, shares from 0, 140, 281, 422, 563.
+    # A page belongs to the share of its last position: (0, h) page 0 at 48h+39, page 1
+    # at 48h+47, (1, h) page 0 at 423+40h; so 5, 6, 5, 4, 4 of the 24 page runs (share 3
+    # starts at (1, 0)'s page, share 4 in (1, 4)'s start positions)
+    assert got["dec_seqs"][:2].tolist() == [[0, 0, 18, 0], [2, 4, 1, 384]]
     assert got["dec_waves"][:5, :4].tolist() == [[0, 0, 0, 5], [0, 2, 1, 6], [0, 5, 1, 5],
                                                  [1, 0, 0, 4], [1, 4, 0, 4]]
     # {r, row, n_keys, first page id}: page 1 of request 0 is page id 9
     assert got["dec_waves"][:5, 4:].tolist() == [[0, 0, 18, 5], [0, 0, 18, 9], [0, 0, 18, 9],
                                                  [2, 4, 1, 11], [2, 4, 1, 11]]
     assert got["pre_items"][:1].tolist() == [[1, 0, 3, 18]]
+
+
+def test_pack_shared_page_cost_known_answer():
+    """The plan prices the pages of a shared sequence that is not the first with its first
+    page at 5 positions instead of 8 (the first one's reads bring them into the caches).
+    Decodes r0 (18 keys, pages 5 6) and r1 (41 keys, 5 8 9) share first page 5 (r0 first);
+    r2 (2 keys, page 11) shares nothing.  Stream costs 2*8+32 = 48, 3*5+32 = 47,
+    1*8+32 = 40; W = 8*135 = 1080 over 4 waves, shares from 0, 270, 540, 810.  Last
+    positions of the pages: (0, h) 48h+39 and 48h+47; (1, h) 384+47h + 36, 41, 46;
+    (2, h) 760+40h+39.  Share 0 takes (0, 0..4) (10 pages), share 1 (0, 5..7) and
+    (1, 0..2) (15), share 2 (1, 3..7) and (2, 0) (16), share 3 (2, 1..7) (7)."""
+    comp, nnew = [17, 40, 1], [1, 1, 1]
+    tabs = [[5, 6], [5, 8, 9], [11]]
+    kw = _kw(3, max_rows=4, max_blocks=3, dec_grid_waves=4, dec_min_pages=1, dec_wave_cap=4,
+             pre_tile_q=32, pre_item_cap=4)
+    got, _ = _compare_pack(comp, nnew, tabs, kw)
+    flag = 1 << 30
+    assert got["dec_seqs"][:3].tolist() == [[0, 0, 18 | flag, 0], [1, 1, 41 | flag, 384],
+                                            [2, 2, 2, 760]]
+    assert got["dec_waves"][:4, :4].tolist() == [[0, 0, 0, 10], [0, 5, 0, 15], [1, 3, 0, 16],
+                                                 [2, 1, 0, 7]]
+    assert got["dec_waves"][:4, 7].tolist() == [5, 5, 5, 11]
+    m = got["meta"]
+    assert (int(m[4]), int(m[6]), int(m[9]), int(m[12])) == (4, 270, 6, 1080)
 
 
 @pytest.mark.parametrize("case,code", [("short", 1), ("wide", 2), ("rows", 3), ("page", 4),
