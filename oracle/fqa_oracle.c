@@ -35,7 +35,7 @@
 #define FQA_DEC_PAGE_COST 8
 #define FQA_DEC_SHARED_PAGE_COST 5
 #define FQA_DEC_STREAM_COST 32
-#define FQA_DEC_PREFIX_STREAM_COST 32
+#define FQA_DEC_PREFIX_STREAM_COST 16
 /* a decode stream's start cost: more for a shared-prefix member */
 static int64_t stream_start_cost(int pfx) {
   return FQA_DEC_STREAM_COST + (pfx > 0 ? FQA_DEC_PREFIX_STREAM_COST : 0);

@@ -138,7 +138,7 @@ def pack(computed, n_new, tables, *, max_rows, max_blocks, pool_pages, dec_grid_
     # cheap one) and marked at its last one (None: a position that marks no page);
     # cut into G equal shares of positions, a share taking the pages marked in it
     PAGE_COST, SHARED_PAGE_COST = 8, 5
-    STREAM_COST, PREFIX_STREAM_COST = 32, 32  # a member's stream always leaves a partial
+    STREAM_COST, PREFIX_STREAM_COST = 32, 16  # a member's stream always leaves a partial
     runs = []  # None or (di, kvh, page), for every cost position, in order
     seqs = []
     P = X = 0

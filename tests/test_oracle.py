@@ -415,17 +415,18 @@ def test_pack_prefix_known_answer():
     flag = 1 << 30
     seqs = got["dec_seqs"][:4]
     assert [int(z) for z in seqs[:, 2]] == [41, 48, 21, 71]  # no flags: groups read their own
-    # streams of 1, 1, 2, 3 pages cost 72, 72, 48, 88 positions (8 per page, 32 for a
-    # stream's start, 32 more for a member's); 8 streams per sequence
-    assert [int(z) for z in seqs[:, 3]] == [0, 576, 1152, 1536]
-    # W = 2240 positions in 7 shares starting at 0, 320, 640, ..., 1920; a page belongs to
-    # the share holding its last position: {di, kvh, page (absolute), pages streamed,
-    # page id}.  Share 1 starts in (0, 4)'s start positions; share 3 holds pages of
-    # (1, 5..7) and (2, 0..1).
+    # streams of 1, 1, 2, 3 pages cost 56, 56, 48, 72 positions (8 per page, 32 for a
+    # stream's start, 16 more for a member's); 8 streams per sequence
+    assert [int(z) for z in seqs[:, 3]] == [0, 448, 896, 1280]
+    # W = 1856 positions in 7 shares starting at 0, 265, 530, 795, 1060, 1325, 1590; a
+    # page belongs to the share holding its last position ((0, h): 56h+55; (1, h):
+    # 503+56h; (2, h): 935+48h, 943+48h; (3, h): 1335+72h, +8, +16): {di, kvh, page
+    # (absolute), pages streamed, page id}.  Share 3 holds pages of (1, 6..7) and
+    # (2, 0..2).
     assert [list(map(int, w[:4])) + [int(w[7])] for w in got["dec_waves"][:7]] == [
-        [0, 0, 2, 4, 7], [0, 4, 2, 4, 7], [1, 0, 2, 5, 9], [1, 5, 2, 7, 9],
-        [2, 2, 0, 12, 8], [3, 0, 2, 12, 7], [3, 4, 2, 12, 7]]
-    assert int(m[12]) == 2240 and int(m[6]) == 320
+        [0, 0, 2, 4, 7], [0, 4, 2, 5, 7], [1, 1, 2, 5, 9], [1, 6, 2, 8, 9],
+        [2, 3, 0, 10, 8], [3, 0, 2, 12, 7], [3, 4, 2, 12, 7]]
+    assert int(m[12]) == 1856 and int(m[6]) == 266
     off, _ = _compare_pack(comp, nnew, tabs, dict(kw, dec_prefix_pages=3))
     assert (int(off["meta"][9]), int(off["meta"][10]), int(off["meta"][11])) == (13, 0, 0)
     assert [bool(z & flag) for z in off["dec_seqs"][:4, 2]] == [True, True, False, True]
